@@ -1,0 +1,158 @@
+/*
+ * trnopt_hip.h -- C ABI of the fused log-domain Sinkhorn half-step for AMD Instinct MI355X (gfx950).
+ *
+ * The library (libtrnopt_hip.so) replaces the device side of the reference package `trnopt`:
+ *   - the fused NKI kernels of src/trnopt/nki_sinkhorn.py (make_row_lse_kernel :150-172,
+ *     make_half_step_kernel :175-228), and
+ *   - the host loop of src/trnopt/sinkhorn.py:346-378 (eps schedule, stages, convergence checks),
+ *     which here runs on the device with no per-iteration host synchronisation.
+ *
+ * Conventions
+ *   - Every pointer named as "device" is a device pointer on the current HIP device; the library never
+ *     allocates or frees device memory. Scratch space is passed in as `ws` with its size in bytes.
+ *   - All work is enqueued on the caller's `stream` (a hipStream_t passed as void*, NULL = default
+ *     stream) and is asynchronous.
+ *   - Every entry point returns 0 on success, a negative SK_E* code for a rejected argument, or a
+ *     positive hipError_t for a runtime failure. sk_last_error() describes the last failure on the
+ *     calling thread. Nothing aborts the process.
+ *   - Point clouds are "packed": padded to a multiple of SK_TILE points and SK_KP_ALIGN coordinates
+ *     and stored in the tile-interleaved order that the MFMA kernels read with one coalesced 16-byte
+ *     load per lane (sk_pack_cloud_f32 builds it from a row-major (n, d) array).
+ *   - Shifted potentials follow the reference (src/trnopt/sinkhorn.py:28-33): fh = f - |x|^2.
+ */
+#ifndef TRNOPT_HIP_H
+#define TRNOPT_HIP_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SK_TILE 32            /* points per packed tile (one 32x32 MFMA output block) */
+#define SK_KP_ALIGN 8         /* coordinates are padded to a multiple of this */
+#define SK_KP_MAX 128         /* largest padded dimension the kernels are built for */
+#define SK_PAD_LOG_WEIGHT (-1e9)  /* log weight of a padding point (src/trnopt/sinkhorn.py:59) */
+
+#define SK_OK 0
+#define SK_E_ARG (-1)         /* null pointer, negative size, misaligned buffer */
+#define SK_E_SHAPE (-2)       /* dimension beyond SK_KP_MAX, size not a multiple of SK_TILE */
+#define SK_E_WORKSPACE (-3)   /* ws too small: ask the matching *_workspace_bytes() */
+#define SK_E_DEVICE (-4)      /* no usable gfx950 device */
+
+/* Library version: major * 10000 + minor * 100 + patch. */
+int sk_version(void);
+
+/* Message of the last failure on the calling thread ("" if none). */
+const char* sk_last_error(void);
+
+/* Padded sizes used by every other entry point. */
+int sk_pad_points(int n);      /* n rounded up to a multiple of SK_TILE */
+int sk_pad_dim(int d);         /* d rounded up to a multiple of SK_KP_ALIGN */
+
+/*
+ * Pack a row-major cloud pts (n, d), leading dimension ld >= d (device, fp32), into the tile layout
+ * out (npad * kp floats, device), npad = sk_pad_points(n), kp = sk_pad_dim(d). Padding is zero.
+ * Replaces the per-block [x^T ; 1] copies of _Cloud (src/trnopt/sinkhorn.py:159-165); the augmented
+ * "1" is not stored, the column term enters the accumulator instead.
+ */
+int sk_pack_cloud_f32(const float* pts, int n, int d, int ld, float* out, void* stream);
+
+/*
+ * Row-wise log-sum-exp of a matrix product (the core of the fused kernel):
+ *     lse[i] = log sum_j exp( xa[i, :] . ya[j, :] ),   i < rows, j < m,
+ * xa (rows, K) and ya (m, K) row-major fp32 device arrays, lse (rows,) fp32 device.
+ * Replaces make_row_lse_kernel(K, rows, m)(xa_T, ya_T) (src/trnopt/nki_sinkhorn.py:150-172); unlike
+ * the NKI kernel there is no constraint on rows or m and K may be up to SK_KP_MAX.
+ */
+size_t sk_row_lse_workspace_bytes(int rows, int m, int K);
+int sk_row_lse_f32(const float* xa, const float* ya, float* lse, int rows, int m, int K,
+                   void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * One fused half-step (the f update; the g update is the same call with the clouds swapped):
+ *     fh[i] = kappa * (xsq[i] + eps * off[i] - eps * lse_i) - xsq[i],
+ *     lse_i = LSE_j( (2 x_i . y_j + gh[j]) / eps + log_b[j] ),
+ * for i < rows_pad, without materialising the scores. Replaces make_half_step_kernel(d, rows, m)
+ * (src/trnopt/nki_sinkhorn.py:175-228) and the PyTorch _half_step (src/trnopt/sinkhorn.py:108-119).
+ *   x_pk   packed rows (rows_pad * kp), y_pk packed columns (m_pad * kp), kp = sk_pad_dim(d)
+ *   xsq, off  (rows_pad,)  |x|^2 and log(target/reference); off may be NULL (= 0)
+ *   gh, log_b (m_pad,)     the other side's shifted potential and log weights (padding: PAD_LOG_WEIGHT)
+ *   sc     device float[4] = {2/eps, 1/eps, eps, kappa}, as the NKI kernel's sc (nki_sinkhorn.py:180)
+ *   skip   device int or NULL: when *skip != 0 the call does nothing (the on-device loop's "done")
+ *   fh     (rows_pad,) output; must not alias gh
+ *   meas   NULL, or per-call convergence partials: then the previous contents of fh are the old
+ *          potential, and meas receives per-block {max_{i<n_real} |fh_new - fh_old|,
+ *          sum_i |w_i (exp(min((fh_old - fh_new)/eps, 50)) - 1)|} (src/trnopt/sinkhorn.py:360, 368-373);
+ *          w (rows_pad,) the row weights (padding 0) is then required. sk_half_step_meas_count()
+ *          gives the number of float2 entries written.
+ * rows_pad and m_pad must be multiples of SK_TILE.
+ */
+size_t sk_half_step_workspace_bytes(int rows_pad, int m_pad, int d);
+int sk_half_step_meas_count(int rows_pad);
+int sk_half_step_f32(const float* x_pk, const float* xsq, const float* off, int rows_pad,
+                     const float* y_pk, const float* gh, const float* log_b, int m_pad, int d,
+                     const float* sc, const int* skip, float* fh,
+                     float* meas, const float* w, int n_real,
+                     void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * On-device Sinkhorn loop: the body of src/trnopt/sinkhorn.py:346-378 (eps schedule or stages, f then
+ * g update, stage advance, balanced / unbalanced checks every check_every iterations, fp32 floors).
+ */
+typedef struct sk_cloud_f32 {
+    const float* pk;      /* packed points (npad * kp) */
+    const float* sq;      /* |p|^2 (npad), float64 sums cast to fp32 (src/trnopt/sinkhorn.py:149) */
+    const float* log_w;   /* log weights (npad), padding SK_PAD_LOG_WEIGHT */
+    const float* w;       /* exp(log_w) (npad), padding 0 */
+    const float* off;     /* log(target / reference) (npad) or NULL */
+    int n;                /* real points */
+    int npad;             /* sk_pad_points(n) */
+} sk_cloud_f32;
+
+/* Loop state, device resident, written by the loop's own kernels (layout is part of the ABI). */
+typedef struct sk_state {
+    double eps;           /* eps of the next iteration */
+    double err;           /* last convergence measure; NaN until a check has run */
+    int it;               /* iterations done */
+    int stage;            /* index into stages (n_stages = the final eps) */
+    int stage_it;         /* iterations in the current stage */
+    int done;             /* 1: converged or max_iters reached; later loop kernels do nothing */
+    int converged;
+    int checks;           /* convergence checks run */
+    float sc_x[4];        /* {2/eps, 1/eps, eps, kappa_x} of the next iteration (f update) */
+    float sc_y[4];        /* same with kappa_y (g update) */
+} sk_state;
+
+typedef struct sk_loop_f32 {
+    sk_cloud_f32 x, y;
+    int d;
+    float* fh;            /* (x.npad) shifted f, written by the f update */
+    float* gh;            /* (y.npad) shifted g, zero-initialised by the caller (g0 = |y|^2) */
+    sk_state* state;      /* device */
+    const double* sched;  /* device, n_sched eps values (eps_start schedule), or NULL */
+    int n_sched;
+    const double* stages; /* device, n_stages eps values (wot-style stages), or NULL */
+    int n_stages;
+    double eps;           /* final eps */
+    double rho_x, rho_y;  /* <= 0: that side balanced (kappa = 1) */
+    double tol;           /* already floored as the reference floors it */
+    double stage_tol;     /* already floored */
+    int max_iters, check_every, stage_max_iters;
+    int fixed_iters;      /* 1: never check */
+    int balanced;         /* 1: balanced error measure, 0: max potential change / eps */
+    void* ws;
+    size_t ws_bytes;
+} sk_loop_f32;
+
+size_t sk_loop_workspace_bytes(int nx_pad, int ny_pad, int d);
+/* Write the initial state (it = 0, first eps and its scalars). */
+int sk_loop_init_f32(const sk_loop_f32* L, void* stream);
+/* Enqueue `iters` iterations (f update, g update, control); iterations after `done` do nothing. */
+int sk_loop_run_f32(const sk_loop_f32* L, int iters, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TRNOPT_HIP_H */

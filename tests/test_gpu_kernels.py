@@ -1,0 +1,131 @@
+"""Kernel-level parity of the HIP row-LSE and half-step against float64 known answers and the float32
+torch half-step (the reference's examples/nki_sinkhorn_check.py, restated as assertions)."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import brute
+from oracle import reference as ref
+from conftest import inf_rel
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _lse_tol(xa, ya):
+    # fp32 contraction error bound per row: a few ulps of the largest |score| term sum, plus exp2/log2 ulps
+    mag = np.abs(xa.astype(np.float64)) @ np.abs(ya.astype(np.float64)).T
+    return 4e-7 * np.sqrt(xa.shape[1]) * mag.max(axis=1) + 2e-6
+
+
+@pytest.mark.parametrize("rows,m,K", [(1, 1, 1), (5, 7, 3), (33, 31, 8), (64, 300, 65), (300, 1000, 65),
+                                      (257, 4097, 31), (1000, 513, 128), (96, 2048, 65), (2, 5000, 17)])
+def test_row_lse_matches_float64(hip, rows, m, K):
+    rng = np.random.default_rng(rows * 1000 + m + K)
+    xa = rng.normal(size=(rows, K)).astype(np.float32)
+    ya = (rng.normal(size=(m, K)) * 0.7).astype(np.float32)
+    print(f"row_lse rows={rows} m={m} K={K}", flush=True)
+    out = hip.row_lse(torch.from_numpy(xa).to(DEV), torch.from_numpy(ya).to(DEV)).cpu().numpy()
+    want = brute.row_lse(xa, ya)
+    assert np.all(np.abs(out - want) <= _lse_tol(xa, ya)), np.abs(out - want).max()
+
+
+def test_row_lse_realistic_scores_with_padding(hip):
+    """examples/nki_sinkhorn_check.py:22-35: blob points, eps 0.1, a plausible gh, the last 300 columns padding
+    (y = 0, gh = 0, log b = -1e9), so padding must contribute exactly nothing."""
+    rng = np.random.default_rng(0)
+    rows, m, d, eps, real = 256, 4096, 64, 0.1, 4096 - 300
+    x = rng.normal(size=(rows, d)) * 0.15
+    y = rng.normal(size=(m, d)) * 0.15 + 0.02
+    gh = -(y ** 2).sum(1) + rng.normal(scale=0.05, size=m)
+    log_b = np.full(m, -np.log(m))
+    y[real:], gh[real:], log_b[real:] = 0.0, 0.0, -1e9
+    xa = np.hstack([x, np.ones((rows, 1))]).astype(np.float32)
+    ya = np.hstack([2.0 / eps * y, (gh / eps + log_b)[:, None]]).astype(np.float32)
+    out = hip.row_lse(torch.from_numpy(xa).to(DEV), torch.from_numpy(ya).to(DEV)).cpu().numpy()
+    want = brute.row_lse(xa, ya)
+    want_real = brute.row_lse(xa, ya[:real])
+    np.testing.assert_allclose(want, want_real, rtol=0, atol=1e-12)
+    assert np.abs(out - want).max() < 2e-4
+
+
+def _half_inputs(rows, m, d, eps, seed, pad_rows=0, pad_cols=0):
+    rng = np.random.default_rng(seed)
+    x = rng.normal(size=(rows, d))
+    y = rng.normal(size=(m, d)) * 0.8 + 0.3
+    gh = rng.normal(scale=2.0, size=m) - 0.5 * (y * y).sum(1)
+    log_b = np.log(rng.uniform(0.5, 1.5, m) / m)
+    off = rng.normal(scale=0.3, size=rows)
+    return x, y, gh, log_b, off
+
+
+@pytest.mark.parametrize("rows,m,d,eps,kappa", [(137, 91, 5, 0.1, 1.0), (1300, 1700, 50, 0.05, 0.9),
+                                                (2048, 2048, 64, 0.1, 1.0), (333, 4000, 30, 0.05, 50 / 50.05),
+                                                (64, 64, 128, 0.5, 0.7), (40, 3000, 1, 0.2, 1.0)])
+def test_half_step_matches_float64_and_torch(hip, rows, m, d, eps, kappa):
+    x, y, gh, log_b, off = _half_inputs(rows, m, d, eps, seed=rows + m + d)
+    X = hip.HipCloud(x, np.zeros(rows), DEV, off=off)
+    Y = hip.HipCloud(y, log_b, DEV)
+    gh_pad = np.zeros(Y.npad)
+    gh_pad[:m] = gh
+    gh_t = torch.as_tensor(gh_pad, dtype=torch.float32, device=DEV)
+    sc = hip.scalars(eps, kappa, DEV)
+    print(f"half_step rows={rows} m={m} d={d} eps={eps} kappa={kappa}", flush=True)
+    out = hip.half_step(X, Y, gh_t, sc).cpu().numpy()[:rows].astype(np.float64)
+    # float64 known answer on the same float32 inputs (padding columns included: weight exactly 0)
+    x32, y32 = x.astype(np.float32), y.astype(np.float32)
+    xsq32 = (x * x).sum(1).astype(np.float32)
+    want = brute.half_step_f64(x32, xsq32, off.astype(np.float32), y32, gh.astype(np.float32),
+                               log_b.astype(np.float32), eps, float(np.float32(kappa)))
+    # the reference's float32 torch half-step on the same inputs
+    t = lambda a: torch.as_tensor(np.asarray(a), dtype=torch.float32)  # noqa: E731
+    got32 = ref.half_step(t(x), t(xsq32), t(off), t(y).T.contiguous(), t(gh), t(log_b),
+                          torch.tensor(1.0 / eps, dtype=torch.float32), torch.tensor(eps, dtype=torch.float32),
+                          torch.tensor(kappa, dtype=torch.float32)).double().numpy()
+    scale = np.abs(want).max()
+    assert inf_rel(out, want) < 2e-6, (inf_rel(out, want), inf_rel(got32, want))
+    assert np.abs(out - got32).max() <= 4 * np.abs(got32 - want).max() + 2e-6 * scale
+
+
+def test_half_step_convergence_partials(hip):
+    """The g update's convergence partials (meas): max |new - old| over real rows and the balanced L1 column
+    error sum |w (exp(min((old - new)/eps, 50)) - 1)| (src/trnopt/sinkhorn.py:360, 368-373)."""
+    rows, m, d, eps = 1000, 700, 16, 0.1
+    x, y, gh, log_b, _ = _half_inputs(rows, m, d, eps, seed=5)
+    w = np.full(rows, 1.0 / rows)
+    X = hip.HipCloud(x, np.log(w), DEV)
+    Y = hip.HipCloud(y, log_b, DEV)
+    gh_t = torch.zeros(Y.npad, dtype=torch.float32, device=DEV)
+    gh_t[:m] = torch.as_tensor(gh, dtype=torch.float32)
+    sc = hip.scalars(eps, 1.0, DEV)
+    new = hip.half_step(X, Y, gh_t, sc)
+    old = new + torch.linspace(-0.3, 0.2, X.npad, device=DEV)
+    buf = old.clone()
+    lb = hip.lib()
+    nmeas = lb.sk_half_step_meas_count(X.npad)
+    meas = torch.zeros(2 * nmeas, dtype=torch.float32, device=DEV)
+    ws = torch.empty(lb.sk_half_step_workspace_bytes(X.npad, Y.npad, d), dtype=torch.uint8, device=DEV)
+    st = lb.sk_half_step_f32(X.pk.data_ptr(), X.sq.data_ptr(), None, X.npad, Y.pk.data_ptr(), gh_t.data_ptr(),
+                             Y.log_w.data_ptr(), Y.npad, d, sc.data_ptr(), None, buf.data_ptr(), meas.data_ptr(),
+                             X.w.data_ptr(), X.n, ws.data_ptr(), ws.numel(), torch.cuda.current_stream().cuda_stream)
+    assert st == 0
+    torch.testing.assert_close(buf, new, rtol=0, atol=0)
+    mv = meas.view(-1, 2).cpu().double().numpy()
+    o, nw = old.cpu().double().numpy(), new.cpu().double().numpy()
+    want_max = np.abs(nw - o)[:rows].max()
+    delta = np.minimum((o - nw) * np.float32(1 / eps), 50.0)
+    want_err = np.abs(X.w.cpu().double().numpy() * (np.exp(delta) - 1.0)).sum()
+    assert abs(mv[:, 0].max() - want_max) <= 1e-6 * want_max
+    assert abs(mv[:, 1].sum() - want_err) <= 1e-5 * want_err
+
+
+def test_errors_are_reported_not_fatal(hip):
+    lb = hip.lib()
+    assert lb.sk_half_step_f32(None, None, None, 32, None, None, None, 32, 4, None, None, None, None, None, 1,
+                               None, 0, None) == -1
+    assert b"null pointer" in lb.sk_last_error()
+    a = torch.zeros(64 * 200, device=DEV)
+    assert lb.sk_row_lse_f32(a.data_ptr(), a.data_ptr(), a.data_ptr(), 10, 10, 200, a.data_ptr(), 1 << 20, None) == -2
+    with pytest.raises(ValueError):
+        hip.row_lse(torch.zeros(3, 200, device=DEV), torch.zeros(4, 200, device=DEV))

@@ -1,0 +1,162 @@
+"""Solver parity of sinkhorn(kernel="hip") on the GPU against the oracle (the reference's plain-PyTorch
+Sinkhorn restated on the CPU) and the float64 brute force, on the reference's own test problems
+(tests/test_sinkhorn.py) and the correctness workload (2048 x 2048, d 64, eps 0.1, 100 fixed iterations)."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import brute, data
+from oracle import reference as ref
+from conftest import inf_rel
+
+from trnopt import Backend
+from trnopt.sinkhorn import SinkhornOptions, sinkhorn, transport_plan
+from trnopt.singlecell import wot_eps_stages
+
+pytestmark = pytest.mark.gpu
+ROCM = Backend.preset("rocm")
+F32_TOL = 2e-3            # allowed max plan error relative to max(P) in float32 (tests/test_sinkhorn.py:19-20)
+
+
+def plan_err(P, Q):
+    return np.abs(P - Q).max() / Q.max()
+
+
+def hip_opts(**kw):
+    return SinkhornOptions(kernel="hip", backend=ROCM, **kw)
+
+
+def test_hip_is_selected_by_auto(hip):
+    from trnopt.sinkhorn import _use_hip
+    assert _use_hip(SinkhornOptions(backend=ROCM), 64)
+    assert not _use_hip(SinkhornOptions(backend=ROCM, kernel="torch"), 64)
+    assert not _use_hip(SinkhornOptions(backend=ROCM), 200)          # d above the fused kernel's limit
+
+
+def test_fixed_iterations_2048_d64_matches_reference():
+    """100 fixed iterations from g0 = |y|^2, eps 0.1, raw N(0, 1) clouds: potentials within 1e-5 (inf-norm
+    relative) of the reference's float64 and float32 plain-PyTorch runs."""
+    x, y = data.balanced_gaussian()
+    o = dict(eps=0.1, normalize=False, max_iters=100, fixed_iters=True)
+    print("hip 2048x2048 d64 100 its", flush=True)
+    res = sinkhorn(x, y, opts=hip_opts(**o))
+    r64 = ref.sinkhorn_ref(x, y, dtype=torch.float64, **o)
+    r32 = ref.sinkhorn_ref(x, y, dtype=torch.float32, **o)
+    assert res.iterations == 100 and not res.converged
+    for want in (r64, r32):
+        assert inf_rel(res.f, want.f) < 1e-5, inf_rel(res.f, want.f)
+        assert inf_rel(res.g, want.g) < 1e-5, inf_rel(res.g, want.g)
+    # the float32 reference's own distance to float64, for scale
+    print("hip vs f64", inf_rel(res.f, r64.f), "torch f32 vs f64", inf_rel(r32.f, r64.f))
+
+
+@pytest.mark.parametrize("iters", [1, 2, 7])
+def test_first_iterations_match_dense_float64(iters):
+    """Iterate-by-iterate: the reference's init (g0 = |y|^2) and update order against the dense brute force."""
+    x, y = data.clouds(n=300, m=200, d=8, seed=11)
+    res = sinkhorn(x, y, opts=hip_opts(eps=0.2, normalize=False, max_iters=iters, fixed_iters=True))
+    f, g, _ = brute.sinkhorn_dense(x, y, 0.2, iters=iters)
+    assert inf_rel(res.f, f) < 1e-5 and inf_rel(res.g, g) < 1e-5
+
+
+def test_balanced_matches_reference():
+    """tests/test_sinkhorn.py:78-88 on the GPU."""
+    x, y = data.clouds()
+    res = sinkhorn(x, y, opts=hip_opts(eps=0.1, tol=1e-5, max_iters=5000))
+    assert res.converged
+    P_ref = brute.dense_plan(*_normed(x, y), *brute.sinkhorn_dense(*_normed(x, y), 0.1, g0=np.zeros(len(y)),
+                                                                  iters=20000, tol=1e-12)[:2], 0.1)
+    P = transport_plan(x, y, res)
+    assert plan_err(P, P_ref) < F32_TOL
+    np.testing.assert_allclose(P.sum(axis=1), 1 / len(x), rtol=F32_TOL * 10)
+    np.testing.assert_allclose(P.sum(axis=0), 1 / len(y), rtol=F32_TOL * 10 + 1e-5)
+
+
+def _normed(x, y):
+    c, s = ref.normalization(x, y)
+    return (x - c) / np.sqrt(s), (y - c) / np.sqrt(s)
+
+
+def test_matches_torch_path_iteration_for_iteration():
+    """The on-device loop against the reference loop in float32: same iteration count and error at the
+    same checks, potentials within 1e-5."""
+    x, y = data.clouds(n=400, m=350, d=10, seed=3)
+    o = dict(eps=0.05, tol=1e-5, max_iters=3000)
+    res = sinkhorn(x, y, opts=hip_opts(**o))
+    r32 = ref.sinkhorn_ref(x, y, dtype=torch.float32, **o)
+    assert res.converged and r32.converged
+    assert abs(res.iterations - r32.iterations) <= 10
+    assert inf_rel(res.f, r32.f) < 1e-4
+
+
+def test_blocked_matches_unblocked():
+    x, y = data.clouds()
+    o = dict(eps=0.1, tol=1e-5, max_iters=5000)
+    full = sinkhorn(x, y, opts=hip_opts(**o))
+    blk = sinkhorn(x, y, opts=hip_opts(block=32, block_y=40, **o))
+    assert blk.converged and plan_err(transport_plan(x, y, blk), transport_plan(x, y, full)) < F32_TOL
+
+
+def test_unbalanced_matches_reference():
+    """tests/test_sinkhorn.py:103-112: unique potentials compared directly."""
+    x, y = data.clouds()
+    a = np.random.default_rng(1).uniform(0.5, 1.5, len(x)) / len(x)
+    res = sinkhorn(x, y, a=a, opts=hip_opts(eps=0.1, rho=1.0, tol=1e-5, max_iters=5000, block=50))
+    assert res.converged
+    xs, ys = _normed(x, y)
+    f, g, _ = brute.sinkhorn_dense(xs, ys, 0.1, a=a, rho_x=1.0, rho_y=1.0, iters=20000, tol=1e-12)
+    assert plan_err(transport_plan(x, y, res, a=a), brute.dense_plan(xs, ys, f, g, 0.1, a=a)) < F32_TOL
+    np.testing.assert_allclose(res.f, f, atol=F32_TOL * 10)
+    r32 = ref.sinkhorn_ref(x, y, a=a, eps=0.1, rho=1.0, tol=1e-5, max_iters=5000, block=50, dtype=torch.float32)
+    assert res.iterations == r32.iterations
+    np.testing.assert_allclose(res.row_mass, r32.row_mass, rtol=1e-4)
+    np.testing.assert_allclose(res.col_mass, r32.col_mass, rtol=1e-4)
+
+
+def test_weighted_balanced():
+    x, y = data.clouds()
+    rng = np.random.default_rng(2)
+    a = rng.uniform(0.2, 1.0, len(x)); a /= a.sum()
+    b = rng.uniform(0.2, 1.0, len(y)); b /= b.sum()
+    res = sinkhorn(x, y, a, b, hip_opts(eps=0.1, tol=1e-5, max_iters=5000))
+    xs, ys = _normed(x, y)
+    f, g, _ = brute.sinkhorn_dense(xs, ys, 0.1, a=a, b=b, g0=np.zeros(len(y)), iters=20000, tol=1e-12)
+    assert plan_err(transport_plan(x, y, res, a, b), brute.dense_plan(xs, ys, f, g, 0.1, a, b)) < F32_TOL
+
+
+def test_eps_scaling_matches_torch_path():
+    x, y = data.clouds(n=300, m=250, d=10, seed=3)
+    o = dict(eps=0.02, tol=1e-5, max_iters=20_000, eps_start=2.0, eps_decay=0.8)
+    res = sinkhorn(x, y, opts=hip_opts(**o))
+    r32 = ref.sinkhorn_ref(x, y, dtype=torch.float32, **o)
+    assert res.converged and abs(res.iterations - r32.iterations) <= 10
+    assert plan_err(transport_plan(x, y, res), ref.transport_plan(x, y, r32)) < F32_TOL
+
+
+def test_fixed_iters_runs_exactly():
+    x, y = data.clouds()
+    res = sinkhorn(x, y, opts=hip_opts(max_iters=7, fixed_iters=True))
+    assert res.iterations == 7 and not res.converged and np.isnan(res.error)
+
+
+@pytest.mark.parametrize("staged", [False, True])
+def test_wot_formulation_matches_wot_scaling(staged):
+    """tests/test_sinkhorn.py:208-226 on the GPU: targets, rho per side, median normalisation, wot's stages."""
+    x, y = data.clouds(n=90, m=70, d=4, seed=7)
+    G = np.random.default_rng(8).uniform(0.5, 2.0, len(x))
+    eps, lam1, lam2 = 0.2, 1.0, 50.0
+    I, J = len(x), len(y)
+    o = hip_opts(eps=eps, rho=(lam1, lam2), normalize="median", tol=1e-6, max_iters=20_000, check_every=5,
+                 eps_stages=wot_eps_stages(eps) if staged else None)
+    res = sinkhorn(x, y, np.full(I, 1 / I), np.full(J, 1 / J), o, a_target=G / I, b_target=np.full(J, G.mean() / J))
+    assert res.converged
+    T = I * transport_plan(x, y, res, np.full(I, 1 / I), np.full(J, 1 / J))
+    R = brute.wot_scaling(x, y, eps, lam1, lam2, G)
+    assert plan_err(T, R) < F32_TOL * 5
+    np.testing.assert_allclose(I * res.row_mass, R.sum(1), rtol=F32_TOL * 5)
+    np.testing.assert_allclose(I * res.col_mass, R.sum(0), rtol=F32_TOL * 5)
+    r32 = ref.sinkhorn_ref(x, y, np.full(I, 1 / I), np.full(J, 1 / J), eps=eps, rho=(lam1, lam2), normalize="median",
+                           tol=1e-6, max_iters=20_000, check_every=5, eps_stages=wot_eps_stages(eps) if staged else None,
+                           a_target=G / I, b_target=np.full(J, G.mean() / J), dtype=torch.float32)
+    assert abs(res.iterations - r32.iterations) <= 10

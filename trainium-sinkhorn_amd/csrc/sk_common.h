@@ -1,0 +1,59 @@
+// Definitions shared by the two translation units of libtrnopt_hip.so: the MFMA partial kernel
+// (sk_lse_partial.hip, built without NaN semantics so row maxima need no canonicalisation) and the rest
+// (sk_kernels.hip: packing, finalisation, loop control, C ABI).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+namespace sk {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr float kLog2e = 1.44269504088896340736f;
+constexpr float kLn2 = 0.69314718055994530942f;
+constexpr float kEmpty = -1.0e30f;     // running max of a row before its first column (finite on purpose)
+constexpr int kWaves = 4;              // waves per workgroup of the partial kernel (one per SIMD)
+constexpr int kBlock = kWaves * 64;
+constexpr int kXcds = 8;
+constexpr int kMaxKq = 16;             // kp = 8 * kq <= 128
+
+enum Mode { kHalfStep = 0, kPlainLse = 1 };
+
+// Work split shared by the partial and the finalisation kernels: the (row group, column tile) units are
+// cut into P equal contiguous ranges, one per workgroup.
+struct Split {
+    long long work;  // row groups * column tiles
+    int nt;          // column tiles
+    int P;           // workgroups
+};
+
+// Workgroup p owns units [p * work / P, (p + 1) * work / P). The owner of unit x is the largest p with
+// floor(p * work / P) <= x, i.e. ((x + 1) * P - 1) / work.
+__host__ __device__ inline int owner_of(long long x, const Split& s) {
+    const long long p = ((x + 1) * (long long)s.P - 1) / s.work;
+    return (int)(p < s.P - 1 ? p : s.P - 1);
+}
+__host__ __device__ inline int first_wg(int g, const Split& s) { return owner_of((long long)g * s.nt, s); }
+__host__ __device__ inline int last_wg(int g, const Split& s) {
+    return owner_of((long long)(g + 1) * s.nt - 1, s);
+}
+
+struct PartialArgs {
+    const float* xr;    // packed rows
+    const float* yc;    // packed columns
+    const float* u;     // column term = alpha * u + beta * v  (m_pad each)
+    const float* v;
+    const float* sc;    // {2/eps, 1/eps, eps, kappa} (half-step mode)
+    const int* skip;
+    float2* part;       // [slot][rows_pad] partial (M, S): M = max_j a_ij, S = sum_j exp2(c (a_ij - M))
+    int nrb;            // row blocks of 32
+    int rows_pad;
+    int mode;
+    Split s;
+};
+
+// Launch the partial kernel for kp = 8 * kq and RB = rb row blocks per wave on P workgroups.
+hipError_t launch_partial(const PartialArgs& a, int kq, int rb, hipStream_t stream);
+
+}  // namespace sk

@@ -1,0 +1,651 @@
+// Fused log-domain Sinkhorn half-step for AMD Instinct MI355X (gfx950), and the on-device Sinkhorn loop.
+//
+// What is computed (reference: src/trnopt/sinkhorn.py:108-119 and src/trnopt/nki_sinkhorn.py:175-228):
+//
+//     fh_i = kappa * (|x_i|^2 + eps * off_i - eps * lse_i) - |x_i|^2
+//     lse_i = LSE_j( (2 x_i . y_j + gh_j) / eps + log b_j )
+//
+// Score layout. With c = (2 / eps) log2(e) and
+//
+//     a_ij = x_i . y_j + (gh_j + eps * log b_j) / 2           ("accumulator units")
+//
+// the score is c a_ij in log2 units. x_i . y_j is a fp32 MFMA contraction from zero over the padded
+// dimension kp (bit-identical in the f and g updates, so a dominant pair's rounding cannot drive the two
+// potentials apart); the column term is added on the VALU. The running (max, sum) of a row is kept as
+//
+//     eps * lse_i = 2 M_i + eps ln(2) log2 S_i,   S_i = sum_j exp2(c (a_ij - M_i)),  M_i = max_j a_ij.
+//
+// MFMA orientation. v_mfma_f32_32x32x2_f32 computes D(32x32) += A(32x2) * B(2x32). A holds 32 columns j
+// (the "y" side), B holds 32 rows i (the "x" side), so lane l's 16 accumulators all belong to row
+// i = l % 32 and to 16 different columns j. Row reductions therefore stay inside a lane; lanes l and
+// l + 32 (the two K halves of the operand layout) are merged once per work segment.
+//
+// Packed cloud layout ("tile-interleaved"). Points are padded to a multiple of 32 (one tile) and
+// coordinates to kp = 8 * KQ. Within tile T the float4 number (q * 64 + h * 32 + r) holds
+// coordinates [h * kp/2 + 4q, h * kp/2 + 4q + 4) of point T * 32 + r. Lane l = h * 32 + r then reads its
+// operand for MFMA steps s = 4q .. 4q+3 with ONE coalesced 16-byte load per q (the wave reads 1 KB
+// contiguous), and MFMA step s contracts coordinates s and kp/2 + s. The same layout serves a cloud in
+// either role (rows in one half-step, columns in the other).
+//
+// Work decomposition ("stream-K" over row groups x column tiles). A workgroup is 4 waves; wave w of a
+// workgroup owns RB row blocks of 32 rows of a row group (4 * RB blocks) and all 4 waves walk the same
+// column tiles, so a column tile is fetched from L2 once per workgroup and hit in L1 by the other waves.
+// The (row group, column tile) units are split into equal contiguous ranges, one per workgroup, so every
+// workgroup does the same amount of MFMA work whatever n and m are. A range may end inside a row group;
+// each (workgroup, row group) segment writes a partial (M, S) per row into its own slot, and a
+// finalisation pass merges the slots of every row and applies the kappa / offset epilogue.
+//
+// The on-device loop (src/trnopt/sinkhorn.py:346-378) is three more tiny pieces: the g update's
+// finalisation also produces per-block convergence partials, and a one-wave control kernel advances
+// (it, stage, stage_it), runs the balanced / unbalanced checks at the reference's cadence, sets `done`,
+// and writes the next iteration's eps and {2/eps, 1/eps, eps, kappa} into the device state. Every loop
+// kernel returns immediately once `done` is set, so the host may enqueue whole batches of iterations.
+
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <algorithm>
+
+#include "sk_common.h"
+#include "trnopt_hip.h"
+
+namespace {
+
+using namespace sk;
+
+constexpr float kMaskOut = -1.0e30f;   // column term of a padding column in the plain row-LSE mode
+constexpr float kDeltaCap = 50.0f;     // cap of (g_old - g_new) / eps in the balanced check (sinkhorn.py:60)
+constexpr int kFinalBlock = 256;
+
+__device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float lg2(float x) { return __builtin_amdgcn_logf(x); }
+
+// ---------------------------------------------------------------------------------------------------
+// Pack a row-major (n, d) cloud into the tile-interleaved layout.
+
+__global__ void pack_cloud_kernel(const float* __restrict__ src, int n, int d, int ld,
+                                  float* __restrict__ dst, int npad, int kp) {
+    const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long long total = (long long)npad * kp;
+    if (idx >= total) return;
+    const int kq = kp / 8;
+    const int e = (int)(idx & 3);
+    long long t = idx >> 2;
+    const int r = (int)(t % 32);
+    t /= 32;
+    const int h = (int)(t % 2);
+    t /= 2;
+    const int q = (int)(t % kq);
+    const long long T = t / kq;
+    const long long row = T * 32 + r;
+    const int k = h * (kp / 2) + q * 4 + e;
+    dst[idx] = (row < n && k < d) ? src[row * ld + k] : 0.0f;
+}
+
+__global__ void fill_mask_kernel(float* __restrict__ mask, int m, int mpad) {
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j < mpad) mask[j] = j < m ? 0.0f : kMaskOut;
+}
+
+// ---------------------------------------------------------------------------------------------------
+// Finalisation: merge the partial slots of each row, then the epilogue.
+
+struct FinalArgs {
+    const float2* part;
+    int rows_pad;
+    int rows_per_group;   // 32 * RB * kWaves
+    Split s;
+    const float* sc;
+    const int* skip;
+    int mode;
+    const float* xsq;
+    const float* off;
+    float* out;
+    int n_store;          // rows written (the rest of rows_pad is computed and dropped)
+    float2* meas;         // per-block convergence partials, or null
+    const float* w;
+    int n_real;
+};
+
+__global__ __launch_bounds__(kFinalBlock) void lse_finalize_kernel(FinalArgs a) {
+    if (a.skip != nullptr && *a.skip != 0) return;
+    const int i = blockIdx.x * kFinalBlock + threadIdx.x;
+    const float c = a.mode == kHalfStep ? a.sc[0] * kLog2e : kLog2e;
+    float dmax = 0.0f;
+    double derr = 0.0;
+    if (i < a.rows_pad) {
+        const int g = i / a.rows_per_group;
+        const int p0 = first_wg(g, a.s), p1 = last_wg(g, a.s);
+        const float2* pp = a.part + i;
+        float M = kEmpty;
+        for (int p = p0; p <= p1; ++p) M = fmaxf(M, pp[(size_t)(p - p0) * a.rows_pad].x);
+        float S = 0.0f;
+        for (int p = p0; p <= p1; ++p) {
+            const float2 v = pp[(size_t)(p - p0) * a.rows_pad];
+            S += v.y * ex2(c * (v.x - M));
+        }
+        // lse = (2 / eps) M + ln S (half-step) or M + ln S (plain): the max enters exactly, in accumulator units
+        const float l2s = lg2(S);
+        if (a.mode == kHalfStep) {
+            const float eps = a.sc[2], kappa = a.sc[3];
+            const float x2 = a.xsq[i];
+            const float o = a.off != nullptr ? a.off[i] : 0.0f;
+            const float eps_lse = 2.0f * M + (eps * kLn2) * l2s;
+            const float val = kappa * ((x2 + eps * o) - eps_lse) - x2;
+            if (a.meas != nullptr) {
+                const float old = a.out[i];
+                if (i < a.n_real) dmax = fabsf(val - old);
+                const float delta = fminf((old - val) * a.sc[1], kDeltaCap);
+                derr = (double)fabsf(a.w[i] * (expf(delta) - 1.0f));
+            }
+            if (i < a.n_store) a.out[i] = val;
+        } else if (i < a.n_store) {
+            a.out[i] = M + kLn2 * l2s;
+        }
+    }
+    if (a.meas != nullptr) {
+        // Block reduction in a fixed order (deterministic for a given launch shape).
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            dmax = fmaxf(dmax, __shfl_xor(dmax, o));
+            derr += __shfl_xor(derr, o);
+        }
+        __shared__ float smax[kFinalBlock / 64];
+        __shared__ double ssum[kFinalBlock / 64];
+        const int wv = threadIdx.x >> 6;
+        if ((threadIdx.x & 63) == 0) {
+            smax[wv] = dmax;
+            ssum[wv] = derr;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            float mx = smax[0];
+            double sm = ssum[0];
+            for (int k = 1; k < kFinalBlock / 64; ++k) {
+                mx = fmaxf(mx, smax[k]);
+                sm += ssum[k];
+            }
+            a.meas[blockIdx.x] = make_float2(mx, (float)sm);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------
+// On-device loop control.
+
+struct LoopCfg {
+    const double* sched;
+    const double* stages;
+    int n_sched, n_stages;
+    double eps, rho_x, rho_y, tol, stage_tol;
+    int max_iters, check_every, stage_max_iters, fixed_iters, balanced;
+};
+
+// eps of the iteration that starts with `it` iterations done (sinkhorn.py:347-350).
+__device__ double eps_for(const LoopCfg& c, int it, int stage) {
+    if (c.n_stages > 0) return stage < c.n_stages ? c.stages[stage] : c.eps;
+    return it < c.n_sched ? c.sched[it] : c.eps;
+}
+
+// The scalars of one eps, computed in double and rounded once, as consts() does (sinkhorn.py:323-334).
+__device__ void set_scalars(sk_state* st, double e, double rho_x, double rho_y) {
+    const double kx = rho_x > 0.0 ? rho_x / (rho_x + e) : 1.0;
+    const double ky = rho_y > 0.0 ? rho_y / (rho_y + e) : 1.0;
+    st->eps = e;
+    st->sc_x[0] = (float)(2.0 / e);
+    st->sc_x[1] = (float)(1.0 / e);
+    st->sc_x[2] = (float)e;
+    st->sc_x[3] = (float)kx;
+    st->sc_y[0] = (float)(2.0 / e);
+    st->sc_y[1] = (float)(1.0 / e);
+    st->sc_y[2] = (float)e;
+    st->sc_y[3] = (float)ky;
+}
+
+__global__ void loop_init_kernel(sk_state* st, LoopCfg c) {
+    if (threadIdx.x != 0) return;
+    st->it = 0;
+    st->stage = 0;
+    st->stage_it = 0;
+    st->done = c.max_iters <= 0 ? 1 : 0;
+    st->converged = 0;
+    st->checks = 0;
+    st->err = __builtin_nan("");
+    set_scalars(st, eps_for(c, 0, 0), c.rho_x, c.rho_y);
+}
+
+// After the g update of one iteration: the body of sinkhorn.py:356-378.
+__global__ __launch_bounds__(64) void loop_control_kernel(sk_state* st, const float2* __restrict__ meas,
+                                                          int nmeas, LoopCfg c) {
+    if (st->done != 0) return;
+    float mx = 0.0f;
+    double sm = 0.0;
+    for (int k = threadIdx.x; k < nmeas; k += 64) {
+        const float2 v = meas[k];
+        mx = fmaxf(mx, v.x);
+        sm += (double)v.y;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        mx = fmaxf(mx, __shfl_xor(mx, o));
+        sm += __shfl_xor(sm, o);
+    }
+    if (threadIdx.x != 0) return;
+    const float inv_eps = st->sc_x[1];          // 1/eps of the iteration that just ran
+    const int it = st->it + 1;
+    int stage = st->stage;
+    int stage_it = st->stage_it + 1;
+    int conv = 0;
+    if (c.n_stages > 0 && stage < c.n_stages) {
+        // An intermediate stage: advance once the potentials settle or after stage_max_iters.
+        if (stage_it % c.check_every == 0) {
+            const double ch = (double)(mx * inv_eps);
+            if (ch < c.stage_tol || stage_it >= c.stage_max_iters) {
+                stage += 1;
+                stage_it = 0;
+            }
+        }
+    } else {
+        const bool check = c.fixed_iters == 0 && (c.n_stages > 0 || it > c.n_sched) &&
+                           (stage_it % c.check_every == 0 || it == c.max_iters);
+        if (check) {
+            const double err = c.balanced != 0 ? sm : (double)(mx * inv_eps);
+            st->err = err;
+            st->checks += 1;
+            if (err < c.tol) conv = 1;
+        }
+    }
+    const int done = (conv != 0 || it >= c.max_iters) ? 1 : 0;
+    st->it = it;
+    st->stage = stage;
+    st->stage_it = stage_it;
+    st->converged = conv;
+    if (done == 0) set_scalars(st, eps_for(c, it, stage), c.rho_x, c.rho_y);
+    st->done = done;
+}
+
+// ---------------------------------------------------------------------------------------------------
+// Host side: errors, device facts, planning, dispatch.
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* where) {
+    return fail((int)e, "%s: %s", where, hipGetErrorString(e));
+}
+
+int cu_count() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
+
+int env_int(const char* name, int dflt) {
+    const char* v = getenv(name);
+    if (v == nullptr || *v == 0) return dflt;
+    return atoi(v);
+}
+
+struct Plan {
+    int kq, rb;
+    int nrb, nt, ngroups;
+    Split s;
+    int slots;       // partial slots per row
+};
+
+Plan make_plan(int rows_pad, int m_pad, int kp) {
+    Plan pl;
+    pl.kq = kp / 8;
+    pl.nrb = rows_pad / SK_TILE;
+    pl.nt = m_pad / SK_TILE;
+    int rb = env_int("TRNOPT_HIP_RB", 0);
+    if (rb != 1 && rb != 2) rb = 1;
+    pl.rb = rb;
+    pl.ngroups = (pl.nrb + kWaves * rb - 1) / (kWaves * rb);
+    pl.s.nt = pl.nt;
+    pl.s.work = (long long)pl.ngroups * pl.nt;
+    int per_cu = env_int("TRNOPT_HIP_WG_PER_CU", 2);
+    if (per_cu < 1 || per_cu > 8) per_cu = 2;
+    long long P = (long long)cu_count() * per_cu;
+    if (P > pl.s.work) P = pl.s.work;
+    if (P < 1) P = 1;
+    pl.s.P = (int)P;
+    int slots = 1;
+    for (int g = 0; g < pl.ngroups; ++g) slots = std::max(slots, last_wg(g, pl.s) - first_wg(g, pl.s) + 1);
+    pl.slots = slots;
+    return pl;
+}
+
+size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
+
+size_t partial_bytes(const Plan& pl, int rows_pad) { return align_up((size_t)pl.slots * rows_pad * sizeof(float2)); }
+
+int meas_count(int rows_pad) { return (rows_pad + kFinalBlock - 1) / kFinalBlock; }
+
+// One LSE pass (partial + finalisation) over packed rows and columns.
+struct Pass {
+    const float* xr;
+    int rows_pad;
+    const float* yc;
+    int m_pad;
+    int kp;
+    const float* u;
+    const float* v;
+    const float* sc;
+    const int* skip;
+    int mode;
+    const float* xsq;
+    const float* off;
+    float* out;
+    int n_store;
+    float2* meas;
+    const float* w;
+    int n_real;
+    float2* part;   // workspace
+};
+
+hipError_t run_pass(const Pass& ps, const Plan& pl, hipStream_t st) {
+    PartialArgs a;
+    a.xr = ps.xr;
+    a.yc = ps.yc;
+    a.u = ps.u;
+    a.v = ps.v;
+    a.sc = ps.sc;
+    a.skip = ps.skip;
+    a.part = ps.part;
+    a.nrb = pl.nrb;
+    a.rows_pad = ps.rows_pad;
+    a.mode = ps.mode;
+    a.s = pl.s;
+    hipError_t e = launch_partial(a, pl.kq, pl.rb, st);
+    if (e != hipSuccess) return e;
+    FinalArgs f;
+    f.part = ps.part;
+    f.rows_pad = ps.rows_pad;
+    f.rows_per_group = SK_TILE * pl.rb * kWaves;
+    f.s = pl.s;
+    f.sc = ps.sc;
+    f.skip = ps.skip;
+    f.mode = ps.mode;
+    f.xsq = ps.xsq;
+    f.off = ps.off;
+    f.out = ps.out;
+    f.n_store = ps.n_store;
+    f.meas = ps.meas;
+    f.w = ps.w;
+    f.n_real = ps.n_real;
+    hipLaunchKernelGGL(lse_finalize_kernel, dim3(meas_count(ps.rows_pad)), dim3(kFinalBlock), 0, st, f);
+    return hipGetLastError();
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+int check_kp(int d) {
+    if (d < 1) return fail(SK_E_SHAPE, "dimension %d must be >= 1", d);
+    const int kp = sk_pad_dim(d);
+    if (kp > SK_KP_MAX) return fail(SK_E_SHAPE, "dimension %d pads to %d > SK_KP_MAX (%d)", d, kp, SK_KP_MAX);
+    return SK_OK;
+}
+
+LoopCfg loop_cfg(const sk_loop_f32* L) {
+    LoopCfg c;
+    c.sched = L->sched;
+    c.stages = L->stages;
+    c.n_sched = L->sched != nullptr ? L->n_sched : 0;
+    c.n_stages = L->stages != nullptr ? L->n_stages : 0;
+    c.eps = L->eps;
+    c.rho_x = L->rho_x;
+    c.rho_y = L->rho_y;
+    c.tol = L->tol;
+    c.stage_tol = L->stage_tol;
+    c.max_iters = L->max_iters;
+    c.check_every = L->check_every > 0 ? L->check_every : 1;
+    c.stage_max_iters = L->stage_max_iters;
+    c.fixed_iters = L->fixed_iters;
+    c.balanced = L->balanced;
+    return c;
+}
+
+int check_cloud(const sk_cloud_f32& c, const char* name) {
+    if (c.pk == nullptr || c.sq == nullptr || c.log_w == nullptr || c.w == nullptr)
+        return fail(SK_E_ARG, "cloud %s: null pointer", name);
+    if (c.n < 1 || c.npad != sk_pad_points(c.n))
+        return fail(SK_E_SHAPE, "cloud %s: n %d, npad %d (expected %d)", name, c.n, c.npad, sk_pad_points(c.n));
+    if (!aligned16(c.pk) || !aligned16(c.log_w)) return fail(SK_E_ARG, "cloud %s: buffers must be 16-byte aligned", name);
+    return SK_OK;
+}
+
+}  // namespace
+
+// ===================================================================================================
+// C ABI
+
+extern "C" {
+
+int sk_version(void) { return 100; }
+
+const char* sk_last_error(void) { return g_err; }
+
+int sk_pad_points(int n) { return n <= 0 ? 0 : (n + SK_TILE - 1) / SK_TILE * SK_TILE; }
+
+int sk_pad_dim(int d) { return d <= 0 ? 0 : (d + SK_KP_ALIGN - 1) / SK_KP_ALIGN * SK_KP_ALIGN; }
+
+int sk_pack_cloud_f32(const float* pts, int n, int d, int ld, float* out, void* stream) {
+    if (pts == nullptr || out == nullptr) return fail(SK_E_ARG, "sk_pack_cloud_f32: null pointer");
+    if (n < 1 || ld < d) return fail(SK_E_SHAPE, "sk_pack_cloud_f32: n %d, d %d, ld %d", n, d, ld);
+    if (int r = check_kp(d)) return r;
+    const int npad = sk_pad_points(n), kp = sk_pad_dim(d);
+    const long long total = (long long)npad * kp;
+    const int threads = 256;
+    const long long blocks = (total + threads - 1) / threads;
+    hipLaunchKernelGGL(pack_cloud_kernel, dim3((unsigned)blocks), dim3(threads), 0, (hipStream_t)stream, pts, n, d,
+                       ld, out, npad, kp);
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? SK_OK : hip_fail(e, "sk_pack_cloud_f32");
+}
+
+size_t sk_row_lse_workspace_bytes(int rows, int m, int K) {
+    if (rows < 1 || m < 1 || K < 1 || sk_pad_dim(K) > SK_KP_MAX) return 0;
+    const int rp = sk_pad_points(rows), mp = sk_pad_points(m), kp = sk_pad_dim(K);
+    const Plan pl = make_plan(rp, mp, kp);
+    return align_up((size_t)rp * kp * 4) + align_up((size_t)mp * kp * 4) + align_up((size_t)mp * 4) +
+           partial_bytes(pl, rp);
+}
+
+int sk_row_lse_f32(const float* xa, const float* ya, float* lse, int rows, int m, int K, void* ws, size_t ws_bytes,
+                   void* stream) {
+    if (xa == nullptr || ya == nullptr || lse == nullptr || ws == nullptr)
+        return fail(SK_E_ARG, "sk_row_lse_f32: null pointer");
+    if (rows < 1 || m < 1) return fail(SK_E_SHAPE, "sk_row_lse_f32: rows %d, m %d", rows, m);
+    if (int r = check_kp(K)) return r;
+    const size_t need = sk_row_lse_workspace_bytes(rows, m, K);
+    if (ws_bytes < need) return fail(SK_E_WORKSPACE, "sk_row_lse_f32: workspace %zu < %zu bytes", ws_bytes, need);
+    if (((uintptr_t)ws & 255) != 0) return fail(SK_E_ARG, "sk_row_lse_f32: workspace must be 256-byte aligned");
+    const int rp = sk_pad_points(rows), mp = sk_pad_points(m), kp = sk_pad_dim(K);
+    const Plan pl = make_plan(rp, mp, kp);
+    char* p = (char*)ws;
+    float* xpk = (float*)p;
+    p += align_up((size_t)rp * kp * 4);
+    float* ypk = (float*)p;
+    p += align_up((size_t)mp * kp * 4);
+    float* mask = (float*)p;
+    p += align_up((size_t)mp * 4);
+    float2* part = (float2*)p;
+    hipStream_t st = (hipStream_t)stream;
+    if (int r = sk_pack_cloud_f32(xa, rows, K, K, xpk, stream)) return r;
+    if (int r = sk_pack_cloud_f32(ya, m, K, K, ypk, stream)) return r;
+    hipLaunchKernelGGL(fill_mask_kernel, dim3((mp + 255) / 256), dim3(256), 0, st, mask, m, mp);
+    Pass ps = {};
+    ps.xr = xpk;
+    ps.rows_pad = rp;
+    ps.yc = ypk;
+    ps.m_pad = mp;
+    ps.kp = kp;
+    ps.u = mask;
+    ps.v = mask;
+    ps.sc = mask;       // not read in this mode; a valid address all the same
+    ps.mode = kPlainLse;
+    ps.out = lse;
+    ps.n_store = rows;
+    ps.part = part;
+    hipError_t e = run_pass(ps, pl, st);
+    return e == hipSuccess ? SK_OK : hip_fail(e, "sk_row_lse_f32");
+}
+
+size_t sk_half_step_workspace_bytes(int rows_pad, int m_pad, int d) {
+    if (rows_pad < SK_TILE || m_pad < SK_TILE || d < 1 || sk_pad_dim(d) > SK_KP_MAX) return 0;
+    const Plan pl = make_plan(rows_pad, m_pad, sk_pad_dim(d));
+    return partial_bytes(pl, rows_pad);
+}
+
+int sk_half_step_meas_count(int rows_pad) { return rows_pad < 1 ? 0 : meas_count(rows_pad); }
+
+int sk_half_step_f32(const float* x_pk, const float* xsq, const float* off, int rows_pad, const float* y_pk,
+                     const float* gh, const float* log_b, int m_pad, int d, const float* sc, const int* skip,
+                     float* fh, float* meas, const float* w, int n_real, void* ws, size_t ws_bytes, void* stream) {
+    if (x_pk == nullptr || xsq == nullptr || y_pk == nullptr || gh == nullptr || log_b == nullptr || sc == nullptr ||
+        fh == nullptr || ws == nullptr)
+        return fail(SK_E_ARG, "sk_half_step_f32: null pointer");
+    if (meas != nullptr && w == nullptr) return fail(SK_E_ARG, "sk_half_step_f32: meas needs w");
+    if (fh == gh) return fail(SK_E_ARG, "sk_half_step_f32: fh must not alias gh");
+    if (rows_pad < SK_TILE || rows_pad % SK_TILE != 0 || m_pad < SK_TILE || m_pad % SK_TILE != 0)
+        return fail(SK_E_SHAPE, "sk_half_step_f32: rows_pad %d and m_pad %d must be positive multiples of %d",
+                    rows_pad, m_pad, SK_TILE);
+    if (int r = check_kp(d)) return r;
+    if (!aligned16(x_pk) || !aligned16(y_pk) || !aligned16(gh) || !aligned16(log_b))
+        return fail(SK_E_ARG, "sk_half_step_f32: packed clouds, gh and log_b must be 16-byte aligned");
+    const size_t need = sk_half_step_workspace_bytes(rows_pad, m_pad, d);
+    if (ws_bytes < need) return fail(SK_E_WORKSPACE, "sk_half_step_f32: workspace %zu < %zu bytes", ws_bytes, need);
+    const Plan pl = make_plan(rows_pad, m_pad, sk_pad_dim(d));
+    Pass ps = {};
+    ps.xr = x_pk;
+    ps.rows_pad = rows_pad;
+    ps.yc = y_pk;
+    ps.m_pad = m_pad;
+    ps.kp = sk_pad_dim(d);
+    ps.u = gh;
+    ps.v = log_b;
+    ps.sc = sc;
+    ps.skip = skip;
+    ps.mode = kHalfStep;
+    ps.xsq = xsq;
+    ps.off = off;
+    ps.out = fh;
+    ps.n_store = rows_pad;
+    ps.meas = (float2*)meas;
+    ps.w = w;
+    ps.n_real = n_real;
+    ps.part = (float2*)ws;
+    hipError_t e = run_pass(ps, pl, (hipStream_t)stream);
+    return e == hipSuccess ? SK_OK : hip_fail(e, "sk_half_step_f32");
+}
+
+size_t sk_loop_workspace_bytes(int nx_pad, int ny_pad, int d) {
+    if (nx_pad < SK_TILE || ny_pad < SK_TILE || d < 1 || sk_pad_dim(d) > SK_KP_MAX) return 0;
+    const int kp = sk_pad_dim(d);
+    const size_t pf = partial_bytes(make_plan(nx_pad, ny_pad, kp), nx_pad);
+    const size_t pg = partial_bytes(make_plan(ny_pad, nx_pad, kp), ny_pad);
+    return std::max(pf, pg) + align_up((size_t)meas_count(ny_pad) * sizeof(float2));
+}
+
+int sk_loop_init_f32(const sk_loop_f32* L, void* stream) {
+    if (L == nullptr || L->state == nullptr) return fail(SK_E_ARG, "sk_loop_init_f32: null pointer");
+    if (L->n_sched > 0 && L->sched == nullptr) return fail(SK_E_ARG, "sk_loop_init_f32: n_sched without sched");
+    if (L->n_stages > 0 && L->stages == nullptr) return fail(SK_E_ARG, "sk_loop_init_f32: n_stages without stages");
+    if (!(L->eps > 0.0)) return fail(SK_E_ARG, "sk_loop_init_f32: eps must be > 0");
+    hipLaunchKernelGGL(loop_init_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, L->state, loop_cfg(L));
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? SK_OK : hip_fail(e, "sk_loop_init_f32");
+}
+
+int sk_loop_run_f32(const sk_loop_f32* L, int iters, void* stream) {
+    if (L == nullptr || L->state == nullptr || L->fh == nullptr || L->gh == nullptr || L->ws == nullptr)
+        return fail(SK_E_ARG, "sk_loop_run_f32: null pointer");
+    if (int r = check_cloud(L->x, "x")) return r;
+    if (int r = check_cloud(L->y, "y")) return r;
+    if (int r = check_kp(L->d)) return r;
+    if (iters < 0) return fail(SK_E_ARG, "sk_loop_run_f32: iters %d < 0", iters);
+    const size_t need = sk_loop_workspace_bytes(L->x.npad, L->y.npad, L->d);
+    if (L->ws_bytes < need) return fail(SK_E_WORKSPACE, "sk_loop_run_f32: workspace %zu < %zu bytes", L->ws_bytes, need);
+    if (((uintptr_t)L->ws & 255) != 0) return fail(SK_E_ARG, "sk_loop_run_f32: workspace must be 256-byte aligned");
+    const int kp = sk_pad_dim(L->d);
+    const Plan pf = make_plan(L->x.npad, L->y.npad, kp);
+    const Plan pg = make_plan(L->y.npad, L->x.npad, kp);
+    const size_t part_sz = std::max(partial_bytes(pf, L->x.npad), partial_bytes(pg, L->y.npad));
+    float2* part = (float2*)L->ws;
+    float2* meas = (float2*)((char*)L->ws + part_sz);
+    const int nmeas = meas_count(L->y.npad);
+    sk_state* st = L->state;
+    const int* skip = &st->done;
+    const LoopCfg cfg = loop_cfg(L);
+    hipStream_t hs = (hipStream_t)stream;
+
+    Pass f = {};
+    f.xr = L->x.pk;
+    f.rows_pad = L->x.npad;
+    f.yc = L->y.pk;
+    f.m_pad = L->y.npad;
+    f.kp = kp;
+    f.u = L->gh;
+    f.v = L->y.log_w;
+    f.sc = st->sc_x;
+    f.skip = skip;
+    f.mode = kHalfStep;
+    f.xsq = L->x.sq;
+    f.off = L->x.off;
+    f.out = L->fh;
+    f.n_store = L->x.npad;
+    f.part = part;
+
+    Pass g = {};
+    g.xr = L->y.pk;
+    g.rows_pad = L->y.npad;
+    g.yc = L->x.pk;
+    g.m_pad = L->x.npad;
+    g.kp = kp;
+    g.u = L->fh;
+    g.v = L->x.log_w;
+    g.sc = st->sc_y;
+    g.skip = skip;
+    g.mode = kHalfStep;
+    g.xsq = L->y.sq;
+    g.off = L->y.off;
+    g.out = L->gh;
+    g.n_store = L->y.npad;
+    g.meas = meas;
+    g.w = L->y.w;
+    g.n_real = L->y.n;
+    g.part = part;
+
+    for (int k = 0; k < iters; ++k) {
+        hipError_t e = run_pass(f, pf, hs);
+        if (e == hipSuccess) e = run_pass(g, pg, hs);
+        if (e == hipSuccess) {
+            hipLaunchKernelGGL(loop_control_kernel, dim3(1), dim3(64), 0, hs, st, meas, nmeas, cfg);
+            e = hipGetLastError();
+        }
+        if (e != hipSuccess) return hip_fail(e, "sk_loop_run_f32");
+    }
+    return SK_OK;
+}
+
+}  // extern "C"

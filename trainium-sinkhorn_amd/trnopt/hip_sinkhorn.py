@@ -1,0 +1,343 @@
+"""The fused Sinkhorn half-step on AMD Instinct MI355X (gfx950): ctypes binding of libtrnopt_hip.so.
+
+This module plays the part nki_sinkhorn.py plays in the reference (src/trnopt/nki_sinkhorn.py): it holds the
+device kernels' entry points and their calling conventions, and sinkhorn.py dispatches to it. The kernels
+are hand-written HIP (trainium-sinkhorn_amd/csrc), built ahead of time by trnopt._build into
+trnopt/_lib/libtrnopt_hip.so; nothing here compiles at run time. The C ABI is declared in
+include/trnopt_hip.h.
+
+What the kernels compute (same as the NKI kernels, src/trnopt/nki_sinkhorn.py:5-22):
+
+    row_lse:    lse_i = log sum_j exp(xa_i . ya_j)
+    half_step:  fh_i = kappa * (|x_i|^2 + eps * off_i - eps * lse_i) - |x_i|^2,
+                lse_i = LSE_j((2 x_i . y_j + gh_j) / eps + log b_j)
+
+without materialising the scores. On top of that, DeviceLoop runs the whole Sinkhorn iteration loop of
+src/trnopt/sinkhorn.py:346-378 on the device (eps schedule / stages, convergence checks), and the host
+only reads the loop state back once per batch of iterations.
+
+Memory comes from PyTorch (device tensors, the caching allocator), work goes on PyTorch's current stream.
+If the library is missing every entry point raises: there is no fallback to another implementation.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import numpy as np
+import torch
+
+PAD_LOG_WEIGHT = -1e9                    # src/trnopt/sinkhorn.py:59
+TILE = 32                                 # SK_TILE
+KP_ALIGN = 8                              # SK_KP_ALIGN
+KP_MAX = 128                              # SK_KP_MAX
+LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libtrnopt_hip.so"
+
+_c_float_p = ctypes.c_void_p             # device pointers travel as integers
+
+
+class SkCloud(ctypes.Structure):
+    _fields_ = [("pk", ctypes.c_void_p), ("sq", ctypes.c_void_p), ("log_w", ctypes.c_void_p),
+                ("w", ctypes.c_void_p), ("off", ctypes.c_void_p), ("n", ctypes.c_int), ("npad", ctypes.c_int)]
+
+
+class SkState(ctypes.Structure):
+    _fields_ = [("eps", ctypes.c_double), ("err", ctypes.c_double), ("it", ctypes.c_int),
+                ("stage", ctypes.c_int), ("stage_it", ctypes.c_int), ("done", ctypes.c_int),
+                ("converged", ctypes.c_int), ("checks", ctypes.c_int),
+                ("sc_x", ctypes.c_float * 4), ("sc_y", ctypes.c_float * 4)]
+
+
+class SkLoop(ctypes.Structure):
+    _fields_ = [("x", SkCloud), ("y", SkCloud), ("d", ctypes.c_int),
+                ("fh", ctypes.c_void_p), ("gh", ctypes.c_void_p), ("state", ctypes.c_void_p),
+                ("sched", ctypes.c_void_p), ("n_sched", ctypes.c_int),
+                ("stages", ctypes.c_void_p), ("n_stages", ctypes.c_int),
+                ("eps", ctypes.c_double), ("rho_x", ctypes.c_double), ("rho_y", ctypes.c_double),
+                ("tol", ctypes.c_double), ("stage_tol", ctypes.c_double),
+                ("max_iters", ctypes.c_int), ("check_every", ctypes.c_int), ("stage_max_iters", ctypes.c_int),
+                ("fixed_iters", ctypes.c_int), ("balanced", ctypes.c_int),
+                ("ws", ctypes.c_void_p), ("ws_bytes", ctypes.c_size_t)]
+
+
+# name -> (restype, argtypes); the exported symbols of include/trnopt_hip.h
+_SIGS = {
+    "sk_version": (ctypes.c_int, []),
+    "sk_last_error": (ctypes.c_char_p, []),
+    "sk_pad_points": (ctypes.c_int, [ctypes.c_int]),
+    "sk_pad_dim": (ctypes.c_int, [ctypes.c_int]),
+    "sk_pack_cloud_f32": (ctypes.c_int, [_c_float_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, _c_float_p,
+                                         ctypes.c_void_p]),
+    "sk_row_lse_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int, ctypes.c_int, ctypes.c_int]),
+    "sk_row_lse_f32": (ctypes.c_int, [_c_float_p, _c_float_p, _c_float_p, ctypes.c_int, ctypes.c_int,
+                                      ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    "sk_half_step_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int, ctypes.c_int, ctypes.c_int]),
+    "sk_half_step_meas_count": (ctypes.c_int, [ctypes.c_int]),
+    "sk_half_step_f32": (ctypes.c_int, [_c_float_p, _c_float_p, _c_float_p, ctypes.c_int, _c_float_p, _c_float_p,
+                                        _c_float_p, ctypes.c_int, ctypes.c_int, _c_float_p, ctypes.c_void_p,
+                                        _c_float_p, _c_float_p, _c_float_p, ctypes.c_int, ctypes.c_void_p,
+                                        ctypes.c_size_t, ctypes.c_void_p]),
+    "sk_loop_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int, ctypes.c_int, ctypes.c_int]),
+    "sk_loop_init_f32": (ctypes.c_int, [ctypes.POINTER(SkLoop), ctypes.c_void_p]),
+    "sk_loop_run_f32": (ctypes.c_int, [ctypes.POINTER(SkLoop), ctypes.c_int, ctypes.c_void_p]),
+}
+SYMBOLS = tuple(_SIGS)
+
+_lib = None
+_load_error: str | None = None
+
+
+def _load():
+    global _lib, _load_error
+    if _lib is not None or _load_error is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        _load_error = f"{LIB_PATH} is not built (run trnopt._build.build() or __graft_entry__.build())"
+        return None
+    try:
+        lib = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(lib, name)
+            fn.restype, fn.argtypes = res, args
+    except OSError as e:                 # pragma: no cover - depends on the machine
+        _load_error = f"cannot load {LIB_PATH}: {e}"
+        return None
+    _lib = lib
+    return lib
+
+
+def available() -> bool:
+    """True if libtrnopt_hip.so is built and loads (says nothing about a GPU being present)."""
+    return _load() is not None
+
+
+def lib():
+    """The loaded library; raises ImportError (naming the reason) if it is not there."""
+    lb = _load()
+    if lb is None:
+        raise ImportError(f"the HIP kernels are not available: {_load_error}")
+    return lb
+
+
+def _check(status: int, what: str) -> None:
+    if status != 0:
+        msg = lib().sk_last_error().decode(errors="replace")
+        if status < 0:
+            raise ValueError(f"{what}: {msg} (status {status})")
+        raise RuntimeError(f"{what}: {msg} (hipError {status})")
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def pad_points(n: int) -> int:
+    return -(-n // TILE) * TILE
+
+
+def pad_dim(d: int) -> int:
+    return -(-d // KP_ALIGN) * KP_ALIGN
+
+
+def _require_device_f32(name: str, t: torch.Tensor, numel: int | None = None) -> None:
+    if not isinstance(t, torch.Tensor) or t.device.type != "cuda" or t.dtype != torch.float32:
+        raise ValueError(f"{name} must be a float32 tensor on the GPU")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if numel is not None and t.numel() < numel:
+        raise ValueError(f"{name} has {t.numel()} elements, needs {numel}")
+
+
+def _workspace(nbytes: int, device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+
+
+# ---------------------------------------------------------------------------------------------------------
+# Kernel-level entry points (the NKI module's make_row_lse_kernel / make_half_step_kernel)
+
+def pack_cloud(pts: torch.Tensor) -> torch.Tensor:
+    """(n, d) float32 device points -> the packed tile layout (pad_points(n) * pad_dim(d),)."""
+    _require_device_f32("pts", pts)
+    if pts.dim() != 2:
+        raise ValueError("pts must be (n, d)")
+    n, d = pts.shape
+    if pad_dim(d) > KP_MAX:
+        raise ValueError(f"d = {d} is above the kernels' limit ({KP_MAX})")
+    out = torch.empty(pad_points(n) * pad_dim(d), dtype=torch.float32, device=pts.device)
+    _check(lib().sk_pack_cloud_f32(pts.data_ptr(), n, d, pts.stride(0), out.data_ptr(), _stream()),
+           "sk_pack_cloud_f32")
+    return out
+
+
+def row_lse(xa: torch.Tensor, ya: torch.Tensor) -> torch.Tensor:
+    """lse_i = log sum_j exp(xa_i . ya_j) for xa (rows, K), ya (m, K) float32 on the GPU.
+
+    Replaces make_row_lse_kernel(K, rows, m)(xa_T, ya_T) (src/trnopt/nki_sinkhorn.py:150-172); takes the
+    row-major (rows, K) / (m, K) arrays instead of their transposes."""
+    _require_device_f32("xa", xa)
+    _require_device_f32("ya", ya)
+    if xa.dim() != 2 or ya.dim() != 2 or xa.shape[1] != ya.shape[1]:
+        raise ValueError("xa (rows, K) and ya (m, K) must share K")
+    rows, K = xa.shape
+    m = ya.shape[0]
+    lb = lib()
+    ws = _workspace(lb.sk_row_lse_workspace_bytes(rows, m, K), xa.device)
+    out = torch.empty(rows, dtype=torch.float32, device=xa.device)
+    _check(lb.sk_row_lse_f32(xa.data_ptr(), ya.data_ptr(), out.data_ptr(), rows, m, K, ws.data_ptr(), ws.numel(),
+                             _stream()), "sk_row_lse_f32")
+    return out
+
+
+def scalars(eps: float, kappa: float, device) -> torch.Tensor:
+    """{2/eps, 1/eps, eps, kappa}: each computed in double and rounded once to float32, as consts() does
+    (src/trnopt/sinkhorn.py:331-332)."""
+    return torch.tensor([2.0 / eps, 1.0 / eps, eps, kappa], dtype=torch.float32, device=device)
+
+
+class HipCloud:
+    """One point cloud on the GPU in the kernels' layout: the counterpart of _Cloud (src/trnopt/sinkhorn.py:131-167).
+
+    Padded to a multiple of 32 points with log weight PAD_LOG_WEIGHT (weight exactly 0) and zero coordinates,
+    |p|^2 summed in float64 and cast, coordinates packed once (they never change during a solve)."""
+
+    def __init__(self, pts: np.ndarray, log_w: np.ndarray, device, off: np.ndarray | None = None):
+        n, d = pts.shape
+        if pad_dim(d) > KP_MAX:
+            raise ValueError(f"d = {d} is above the HIP kernels' limit (d <= {KP_MAX})")
+        npad = pad_points(n)
+        P = np.zeros((npad, d))
+        P[:n] = pts
+        L = np.full(npad, PAD_LOG_WEIGHT)
+        L[:n] = log_w
+        f32 = dict(dtype=torch.float32, device=device)
+        self.n, self.npad, self.d, self.device = n, npad, d, device
+        self.sq = torch.as_tensor((P * P).sum(axis=1), dtype=torch.float32).to(device)
+        self.log_w = torch.as_tensor(L, dtype=torch.float32).to(device)
+        self.w = torch.as_tensor(np.exp(L), dtype=torch.float32).to(device)
+        if off is not None:
+            O = np.zeros(npad)
+            O[:n] = off
+            self.off = torch.as_tensor(O, dtype=torch.float32).to(device)
+        else:
+            self.off = None
+        self.zero_off = torch.zeros(npad, **f32)
+        pts32 = torch.as_tensor(P, dtype=torch.float32).to(device)
+        self.pk = pack_cloud(pts32)
+
+    def c_struct(self) -> SkCloud:
+        return SkCloud(self.pk.data_ptr(), self.sq.data_ptr(), self.log_w.data_ptr(), self.w.data_ptr(),
+                       _ptr(self.off), self.n, self.npad)
+
+
+def half_step(side: HipCloud, other: HipCloud, other_h: torch.Tensor, sc: torch.Tensor, use_off: bool = True,
+              out: torch.Tensor | None = None) -> torch.Tensor:
+    """One fused half-step: the new shifted potential of `side`'s points (side.npad,) against `other`.
+
+    The counterpart of _NkiStep.__call__ (src/trnopt/sinkhorn.py:185-193) and of make_half_step_kernel's
+    kernel (src/trnopt/nki_sinkhorn.py:175-228): sc = {2/eps, 1/eps, eps, kappa} on the device."""
+    _require_device_f32("other_h", other_h, other.npad)
+    _require_device_f32("sc", sc, 4)
+    if side.d != other.d:
+        raise ValueError("clouds of different dimension")
+    lb = lib()
+    ws = _workspace(lb.sk_half_step_workspace_bytes(side.npad, other.npad, side.d), side.device)
+    if out is None:
+        out = torch.empty(side.npad, dtype=torch.float32, device=side.device)
+    off = side.off if use_off else None
+    _check(lb.sk_half_step_f32(side.pk.data_ptr(), side.sq.data_ptr(), _ptr(off), side.npad, other.pk.data_ptr(),
+                               other_h.data_ptr(), other.log_w.data_ptr(), other.npad, side.d, sc.data_ptr(), None,
+                               out.data_ptr(), None, None, side.n, ws.data_ptr(), ws.numel(), _stream()),
+           "sk_half_step_f32")
+    return out
+
+
+# ---------------------------------------------------------------------------------------------------------
+# The on-device loop
+
+class DeviceLoop:
+    """The iteration loop of src/trnopt/sinkhorn.py:346-378 on the GPU.
+
+    Each enqueued iteration is: f update (X rows against Y), g update (Y rows against X, which also reduces
+    the convergence measures), and a one-wave control kernel that advances it / stage / stage_it, runs the
+    reference's checks at its cadence, sets `done` and writes the next eps's scalars. Kernels enqueued after
+    `done` return at once, so the host enqueues batches and reads the 72-byte state once per batch, with the
+    next batch already queued behind it (no per-iteration synchronisation)."""
+
+    def __init__(self, X: HipCloud, Y: HipCloud, *, eps: float, rho_x, rho_y, sched, stages, tol: float,
+                 stage_tol: float, max_iters: int, check_every: int, stage_max_iters: int, fixed_iters: bool,
+                 balanced: bool):
+        dev = X.device
+        lb = lib()
+        self.X, self.Y = X, Y
+        self.fh = torch.zeros(X.npad, dtype=torch.float32, device=dev)
+        self.gh = torch.zeros(Y.npad, dtype=torch.float32, device=dev)      # gh = 0: g0 = |y|^2 (sinkhorn.py:336)
+        self.state = torch.zeros(ctypes.sizeof(SkState), dtype=torch.uint8, device=dev)
+        self._sched = torch.tensor(list(sched), dtype=torch.float64, device=dev) if len(sched) else None
+        self._stages = torch.tensor(list(stages), dtype=torch.float64, device=dev) if len(stages) else None
+        self.ws = _workspace(lb.sk_loop_workspace_bytes(X.npad, Y.npad, X.d), dev)
+        self.max_iters = int(max_iters)
+        self.check_every = max(1, int(check_every))
+        self.fixed_iters = bool(fixed_iters)
+        L = SkLoop()
+        L.x, L.y, L.d = X.c_struct(), Y.c_struct(), X.d
+        L.fh, L.gh, L.state = self.fh.data_ptr(), self.gh.data_ptr(), self.state.data_ptr()
+        L.sched, L.n_sched = _ptr(self._sched), len(sched)
+        L.stages, L.n_stages = _ptr(self._stages), len(stages)
+        L.eps = float(eps)
+        L.rho_x = float(rho_x) if rho_x is not None else -1.0
+        L.rho_y = float(rho_y) if rho_y is not None else -1.0
+        L.tol, L.stage_tol = float(tol), float(stage_tol)
+        L.max_iters, L.check_every, L.stage_max_iters = self.max_iters, self.check_every, int(stage_max_iters)
+        L.fixed_iters, L.balanced = int(bool(fixed_iters)), int(bool(balanced))
+        L.ws, L.ws_bytes = self.ws.data_ptr(), self.ws.numel()
+        self._L = L
+        self._pinned = [torch.empty(ctypes.sizeof(SkState), dtype=torch.uint8, pin_memory=True) for _ in range(2)]
+
+    def init(self) -> None:
+        _check(lib().sk_loop_init_f32(ctypes.byref(self._L), _stream()), "sk_loop_init_f32")
+
+    def enqueue(self, iters: int) -> None:
+        _check(lib().sk_loop_run_f32(ctypes.byref(self._L), int(iters), _stream()), "sk_loop_run_f32")
+
+    def read_state(self) -> SkState:
+        """Synchronous read of the current state (waits for everything enqueued)."""
+        host = self.state.to("cpu")
+        return SkState.from_buffer_copy(host.numpy().tobytes())
+
+    def run(self, batch: int | None = None) -> SkState:
+        """Run to `done` (converged or max_iters). Returns the final state."""
+        self.init()
+        if self.fixed_iters:
+            self.enqueue(self.max_iters)
+            return self.read_state()
+        batch = max(1, int(batch or max(self.check_every, 10)))
+        queued = 0
+        inflight = []                         # (pinned buffer, event) per enqueued batch, oldest first
+        slot = 0
+        while True:
+            if queued < self.max_iters:
+                k = min(batch, self.max_iters - queued)
+                self.enqueue(k)
+                queued += k
+                buf = self._pinned[slot % 2]
+                slot += 1
+                buf.copy_(self.state, non_blocking=True)
+                ev = torch.cuda.Event()
+                ev.record()
+                inflight.append((buf, ev))
+                if len(inflight) < 2 and queued < self.max_iters:
+                    continue                  # keep a second batch queued behind the one we wait on
+            buf, ev = inflight.pop(0)
+            ev.synchronize()
+            st = SkState.from_buffer_copy(buf.numpy().tobytes())
+            if st.done:
+                torch.cuda.current_stream().synchronize()
+                return self.read_state()
+            if not inflight and queued >= self.max_iters:  # pragma: no cover - done must be set by then
+                return self.read_state()
+

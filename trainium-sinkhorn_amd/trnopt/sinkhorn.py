@@ -1,0 +1,347 @@
+"""Entropic optimal transport between point clouds by log-domain Sinkhorn, with a fused HIP half-step.
+
+The public API is the reference's (src/trnopt/sinkhorn.py): sinkhorn(x, y, a, b, opts, a_target, b_target)
+-> SinkhornResult, SinkhornOptions, normalization(), transport_plan(), with the same fields, defaults,
+validation errors and numerics. What is new is where the work runs:
+
+* kernel="hip" (and kernel="auto" on Backend.preset("rocm")): the half-steps are the fused gfx950 kernels of
+  hip_sinkhorn.py, which never materialise the n x m scores, and the iteration loop itself (eps schedule or
+  stages, the f then g updates, convergence checks) runs on the GPU. The host enqueues batches of iterations
+  and reads a small state block once per batch instead of synchronising on every check.
+* kernel="torch": the plain PyTorch half-step (the reference's own, src/trnopt/sinkhorn.py:108-119) and the
+  host loop, on any device and dtype. This is the path the fused kernels are checked against.
+* kernel="nki" is recognised and refused (no NeuronCore in this build).
+
+Problem and conventions (src/trnopt/sinkhorn.py:1-47). Plan P_ij = a_i b_j exp((f_i + g_j - C_ij) / eps),
+C_ij = |x_i - y_j|^2. One iteration is the f update then the g update,
+
+    f_i = -kappa_x eps LSE_j(log b_j + (g_j - C_ij) / eps),  g_j likewise with the roles swapped,
+
+kappa = rho / (rho + eps) when unbalanced (1 when balanced). The state carried is the shifted potential
+fh = f - |x|^2 (gh = g - |y|^2), so a half-step is a matrix product plus a column term and a row-wise
+log-sum-exp; the loop starts from gh = 0 (g = |y|^2).
+"""
+
+from __future__ import annotations
+
+import time
+from dataclasses import dataclass
+from types import SimpleNamespace
+
+import numpy as np
+import torch
+
+from .backend import Backend
+
+PAD_LOG_WEIGHT = -1e9          # log weight of a padding point: exactly zero weight, and finite (sinkhorn.py:59)
+_DELTA_CAP = 50.0              # cap on (g_old - g_new) / eps in the balanced check, so exp stays finite (:60)
+KERNELS = ("auto", "torch", "hip", "nki")
+
+
+@dataclass
+class SinkhornOptions:
+    eps: float = 0.05              # entropic blur, in cost units (after normalisation: of the typical cost)
+    rho: float | tuple | None = None   # None: balanced; else the KL marginal penalty, one value or (rho_x, rho_y)
+    max_iters: int = 2000
+    tol: float = 1e-4              # balanced: L1 column-marginal error; unbalanced: max potential change / eps
+                                   #   (float32 unbalanced: at least 5e-6)
+    check_every: int = 10          # iterations between convergence checks
+    block: int | None = None       # torch kernel: rows of x per block in the f update (None: all at once).
+                                   #   The fused HIP kernel streams every row and column, so it ignores blocks.
+    block_y: int | None = None     # torch kernel: rows of y per block in the g update (None: same as block)
+    eps_start: float | None = None # eps-scaling: start here, multiply by eps_decay each iteration down to eps
+    eps_decay: float = 0.9
+    eps_stages: tuple | None = None  # wot-style stages: each eps in turn until the max potential change / eps
+    stage_tol: float = 1e-6        #   < stage_tol (at least 1e-5 in float32) or stage_max_iters; then eps to tol
+    stage_max_iters: int = 1000
+    normalize: bool | str | tuple = True  # True / "mean", "median", False, or a precomputed (center, cost_scale)
+    fixed_iters: bool = False      # run exactly max_iters, no checks (benchmarks)
+    cores: int = 1                 # the reference's NeuronCore row split; this build runs on one GPU (1 only)
+    kernel: str = "auto"           # "auto" (hip on a ROCm GPU in float32 with d <= 128, else torch), "hip",
+                                   #   "torch", or "nki" (refused: no Neuron device here)
+    backend: Backend = Backend.preset("cpu")
+
+
+@dataclass
+class SinkhornResult:
+    f: np.ndarray                  # potentials, float64, normalised cost units (times cost_scale: original)
+    g: np.ndarray
+    iterations: int
+    error: float                   # last convergence measure; nan if never checked
+    converged: bool
+    cost: float                    # balanced: <a, f> + <b, g>; nan if unbalanced
+    seconds: float                 # wall time of the iteration loop (including read-back and masses)
+    eps: float
+    rho: float | tuple | None
+    center: np.ndarray             # x_used = (x - center) / sqrt(cost_scale)
+    cost_scale: float
+    row_mass: np.ndarray | None = None   # unbalanced: the plan's actual row and column sums
+    col_mass: np.ndarray | None = None
+
+
+# ---------------------------------------------------------------------------------------------------------
+# The plain PyTorch half-step and its host loop (kernel="torch")
+
+def _half_step(x_blk, xsq_blk, off_blk, yT, gh, log_b, inv_eps, eps, kappa):
+    """The f update of one block of rows in shifted form: the reference's op sequence
+    (src/trnopt/sinkhorn.py:116-119), scores materialised (k, m). Scalars are 0-d tensors so a compiled
+    version does not specialise on eps."""
+    scores = (2.0 * (x_blk @ yT) + gh[None, :]) * inv_eps + log_b[None, :]
+    top = scores.amax(dim=1, keepdim=True)
+    lse = top[:, 0] + torch.log(torch.exp(scores - top).sum(dim=1))
+    return kappa * (xsq_blk + eps * off_blk - eps * lse) - xsq_blk
+
+
+class _TorchCloud:
+    """A cloud padded to whole blocks for the torch half-step, as _Cloud does (src/trnopt/sinkhorn.py:131-158)."""
+
+    def __init__(self, pts: np.ndarray, log_w: np.ndarray, block: int, be: Backend, off: np.ndarray | None):
+        n, d = pts.shape
+        npad = -(-n // block) * block
+        P = np.zeros((npad, d))
+        P[:n] = pts
+        L = np.full(npad, PAD_LOG_WEIGHT)
+        L[:n] = log_w
+        O = np.zeros(npad)
+        if off is not None:
+            O[:n] = off
+        self.n, self.npad = n, npad
+        pts_t = be.tensor(P)
+        self.xT = pts_t.T.contiguous()
+        self.sq = be.tensor((P * P).sum(axis=1))              # float64 sums, then cast
+        off_t, zero_t = be.tensor(O), be.tensor(np.zeros(npad))
+        self.blocks = [(pts_t[s:s + block].contiguous(), self.sq[s:s + block].contiguous(),
+                        off_t[s:s + block].contiguous(), zero_t[s:s + block].contiguous())
+                       for s in range(0, npad, block)]
+        self.log_w = be.tensor(L)
+        self.w = be.tensor(np.exp(L))                           # padding weight exactly 0
+
+
+def _solve_torch(p, opts: SinkhornOptions):
+    be = opts.backend
+    X = _TorchCloud(p.xs, p.log_a, opts.block or len(p.xs), be, p.off_x)
+    Y = _TorchCloud(p.ys, p.log_b, opts.block_y or opts.block or len(p.ys), be, p.off_y)
+    step = be.compile_fn(_half_step)
+    scal: dict = {}
+
+    def consts(e, rho):
+        """(1/eps, eps, kappa) as 0-d tensors, each computed in double then rounded (sinkhorn.py:323-334)."""
+        key = (e, rho)
+        if key not in scal:
+            kappa = 1.0 if rho is None else rho / (rho + e)
+            if len(scal) > 8:
+                scal.clear()
+            scal[key] = tuple(torch.tensor(v, dtype=be.dtype, device=be.device) for v in (1.0 / e, e, kappa))
+        return scal[key]
+
+    def sweep(side, other, other_h, c, use_off=True):
+        inv_eps, eps_t, kappa = c
+        return torch.cat([step(xb, sqb, ob if use_off else zb, other.xT, other_h, other.log_w, inv_eps, eps_t, kappa)
+                          for xb, sqb, ob, zb in side.blocks])
+
+    gh = torch.zeros(Y.npad, dtype=be.dtype, device=be.device)
+    fh = torch.zeros(X.npad, dtype=be.dtype, device=be.device)
+    err, converged, it = float("nan"), False, 0
+    stage, stage_it = 0, 0
+    stages, sched = p.stages, p.sched
+    t0 = time.perf_counter()
+    while it < opts.max_iters:
+        if stages:
+            e = stages[stage] if stage < len(stages) else opts.eps
+        else:
+            e = sched[it] if it < len(sched) else opts.eps
+        cx, cy = consts(e, p.rho_x), consts(e, p.rho_y)
+        inv_eps = cx[0]
+        fh = sweep(X, Y, gh, cx)
+        gh_new = sweep(Y, X, fh, cy)
+        it += 1
+        stage_it += 1
+        if stages and stage < len(stages):
+            # an intermediate stage: move on once the potentials settle (or after stage_max_iters)
+            if stage_it % opts.check_every == 0:
+                ch = float((((gh_new - gh)[:Y.n].abs().amax()) * inv_eps).item())
+                if ch < p.stage_tol or stage_it >= opts.stage_max_iters:
+                    stage, stage_it = stage + 1, 0
+            gh = gh_new
+            continue
+        check = (not opts.fixed_iters and (bool(stages) or it > len(sched))
+                 and (stage_it % opts.check_every == 0 or it == opts.max_iters))
+        if check:
+            if p.balanced:
+                # column sums of the plan with (new f, old g) are b_j exp((g_old_j - g_new_j) / eps)
+                delta = ((gh - gh_new) * inv_eps).clamp(max=_DELTA_CAP)
+                err = float((Y.w * (torch.exp(delta) - 1.0)).abs().sum().item())
+            else:
+                err = float((((gh_new - gh)[:Y.n].abs().amax()) * inv_eps).item())
+        gh = gh_new
+        if check and err < p.tol:
+            converged = True
+            break
+    f = (fh + X.sq)[:X.n].detach().to("cpu", torch.float64).numpy()
+    g = (gh + Y.sq)[:Y.n].detach().to("cpu", torch.float64).numpy()
+    fb = gb = None
+    if not p.balanced:
+        c1 = consts(opts.eps, None)
+        fb = (sweep(X, Y, gh, c1, use_off=False) + X.sq)[:X.n].detach().to("cpu", torch.float64).numpy()
+        gb = (sweep(Y, X, fh, c1, use_off=False) + Y.sq)[:Y.n].detach().to("cpu", torch.float64).numpy()
+    return f, g, fb, gb, it, err, converged, t0
+
+
+# ---------------------------------------------------------------------------------------------------------
+# The fused HIP path (kernel="hip")
+
+def _solve_hip(p, opts: SinkhornOptions):
+    from . import hip_sinkhorn as hk
+    dev = torch.device(opts.backend.device)
+    if dev.index is None:
+        dev = torch.device("cuda", torch.cuda.current_device())
+    with torch.cuda.device(dev):
+        X = hk.HipCloud(p.xs, p.log_a, dev, p.off_x)
+        Y = hk.HipCloud(p.ys, p.log_b, dev, p.off_y)
+        loop = hk.DeviceLoop(X, Y, eps=opts.eps, rho_x=p.rho_x, rho_y=p.rho_y, sched=p.sched, stages=p.stages,
+                             tol=p.tol, stage_tol=p.stage_tol, max_iters=opts.max_iters,
+                             check_every=opts.check_every, stage_max_iters=opts.stage_max_iters,
+                             fixed_iters=opts.fixed_iters, balanced=p.balanced)
+        t0 = time.perf_counter()
+        st = loop.run()
+        # f = fh + |x|^2 in float32 on the device, then float64, as the reference reads it back (:379-380)
+        f = (loop.fh + X.sq)[:X.n].to("cpu", torch.float64).numpy()
+        g = (loop.gh + Y.sq)[:Y.n].to("cpu", torch.float64).numpy()
+        fb = gb = None
+        if not p.balanced:
+            # one balanced half-step each way (kappa = 1, no offset) at the final eps (:381-389)
+            c1 = hk.scalars(opts.eps, 1.0, dev)
+            fb = (hk.half_step(X, Y, loop.gh, c1, use_off=False) + X.sq)[:X.n].to("cpu", torch.float64).numpy()
+            gb = (hk.half_step(Y, X, loop.fh, c1, use_off=False) + Y.sq)[:Y.n].to("cpu", torch.float64).numpy()
+    return f, g, fb, gb, int(st.it), float(st.err), bool(st.converged), t0
+
+
+def _use_hip(opts: SinkhornOptions, d: int) -> bool:
+    """Kernel selection, the counterpart of _use_nki (src/trnopt/sinkhorn.py:196-208). The fused kernels need a
+    ROCm GPU, float32 and d <= 128. kernel="hip" outside that is an error; so is a missing kernel library
+    whenever the fused kernels are selected (there is no silent fallback)."""
+    if opts.kernel not in KERNELS:
+        raise ValueError(f"unknown kernel {opts.kernel!r}; choose from {KERNELS}")
+    if opts.kernel == "torch":
+        return False
+    if opts.kernel == "nki":
+        raise ValueError("kernel='nki' needs a Neuron device; this build's fused kernel is kernel='hip'")
+    from . import hip_sinkhorn as hk
+    be = opts.backend
+    ok = be.is_rocm_gpu and be.dtype == torch.float32 and hk.pad_dim(d) <= hk.KP_MAX
+    if opts.kernel == "hip" and not ok:
+        raise ValueError("kernel='hip' needs a ROCm GPU device (Backend.preset('rocm')), float32 and d <= 128")
+    if ok:
+        hk.lib()                     # ImportError if libtrnopt_hip.so is missing
+    return ok
+
+
+# ---------------------------------------------------------------------------------------------------------
+# Inputs, normalisation, driver
+
+def _log_weights(w, n: int, name: str) -> np.ndarray:
+    if w is None:
+        return np.full(n, -np.log(n))
+    w = np.asarray(w, dtype=np.float64)
+    if w.shape != (n,) or np.any(w <= 0):
+        raise ValueError(f"{name} must be {n} positive weights")
+    return np.log(w)
+
+
+def normalization(x: np.ndarray, y: np.ndarray, samples: int = 20_000, seed: int = 0,
+                  how: str = "mean") -> tuple[np.ndarray, float]:
+    """(center, cost_scale) as the reference computes them (src/trnopt/sinkhorn.py:220-238): center = mean of all
+    points; cost_scale = the mean squared x-y distance over `samples` random pairs (rng seed `seed`), or with
+    how="median" the median over all pairs when n m <= 1e8 (else over the random pairs). 1 if that is 0."""
+    center = np.concatenate([x, y]).mean(axis=0)
+    if how == "median" and len(x) * len(y) <= 100_000_000:
+        xc, yc = x - center, y - center
+        C = ((xc * xc).sum(1)[:, None] + (yc * yc).sum(1)[None, :] - 2.0 * (xc @ yc.T)).ravel()
+        scale = float(np.median(np.maximum(C, 0.0)))
+    else:
+        rng = np.random.default_rng(seed)
+        i, j = rng.integers(len(x), size=samples), rng.integers(len(y), size=samples)
+        dd = ((x[i] - y[j]) ** 2).sum(axis=1)
+        scale = float(np.median(dd) if how == "median" else dd.mean())
+    return center, (scale if scale > 0 else 1.0)
+
+
+def _prepare(x, y, a, b, opts: SinkhornOptions, a_target, b_target):
+    """Validation, weights, normalisation and the eps schedule (src/trnopt/sinkhorn.py:250-320, 340-344)."""
+    be = opts.backend
+    x = np.asarray(x, dtype=np.float64)
+    y = np.asarray(y, dtype=np.float64)
+    log_a, log_b = _log_weights(a, len(x), "a"), _log_weights(b, len(y), "b")
+    balanced = opts.rho is None
+    if balanced and abs(np.exp(log_a).sum() - np.exp(log_b).sum()) > 1e-9 * np.exp(log_a).sum():
+        raise ValueError("balanced OT needs sum(a) == sum(b); pass rho for unbalanced")
+    if balanced and (a_target is not None or b_target is not None):
+        raise ValueError("a_target / b_target are for unbalanced OT (pass rho)")
+    if balanced:
+        rho_x = rho_y = None
+    elif isinstance(opts.rho, (tuple, list)):
+        rho_x, rho_y = tuple(opts.rho)
+    else:
+        rho_x = rho_y = opts.rho
+    off_x = None if a_target is None else _log_weights(a_target, len(x), "a_target") - log_a
+    off_y = None if b_target is None else _log_weights(b_target, len(y), "b_target") - log_b
+    if isinstance(opts.normalize, tuple):
+        center, scale = np.asarray(opts.normalize[0], dtype=np.float64), float(opts.normalize[1])
+    elif opts.normalize:
+        center, scale = normalization(x, y, how=opts.normalize if isinstance(opts.normalize, str) else "mean")
+    else:
+        center, scale = np.zeros(x.shape[1]), 1.0
+    root = np.sqrt(scale)
+    xs, ys = (x - center) / root, (y - center) / root
+    stages = [e for e in (opts.eps_stages or ()) if e > opts.eps]
+    sched = []
+    if not stages and opts.eps_start is not None and opts.eps_start > opts.eps:
+        e = opts.eps_start
+        while e > opts.eps and len(sched) < opts.max_iters:
+            sched.append(e)
+            e *= opts.eps_decay
+    f32 = be.dtype == torch.float32
+    # float32 rounding noise in the potentials' change sits near 1e-6 of eps: floor the thresholds (:340-344)
+    stage_tol = max(opts.stage_tol, 1e-5 if f32 else 0.0)
+    tol = max(opts.tol, 5e-6) if (f32 and not balanced) else opts.tol
+    return SimpleNamespace(x=x, y=y, xs=xs, ys=ys, log_a=log_a, log_b=log_b, off_x=off_x, off_y=off_y,
+                           rho_x=rho_x, rho_y=rho_y, balanced=balanced, center=center, scale=scale,
+                           stages=stages, sched=sched, tol=tol, stage_tol=stage_tol)
+
+
+def sinkhorn(x, y, a=None, b=None, opts: SinkhornOptions | None = None, a_target=None,
+             b_target=None) -> SinkhornResult:
+    """Entropic OT between clouds x (n, d) and y (m, d) with weights a, b (default uniform).
+
+    a, b are the reference measure of the entropy term eps KL(P | a b^T). Unbalanced (rho given), the penalties
+    rho KL(P 1 | a_target) and rho KL(P^T 1 | b_target) pull the plan's sums toward a_target and b_target (default
+    a and b): wot's formulation is a uniform reference, a_target = growth / I, b_target = mean growth / J."""
+    opts = opts or SinkhornOptions()
+    p = _prepare(x, y, a, b, opts, a_target, b_target)
+    hip = _use_hip(opts, p.x.shape[1])
+    if max(1, int(opts.cores)) > 1:
+        raise ValueError("cores > 1 split rows across NeuronCores in the reference; this build runs on one GPU")
+    if hip:
+        f, g, fb, gb, it, err, converged, t0 = _solve_hip(p, opts)
+    else:
+        f, g, fb, gb, it, err, converged, t0 = _solve_torch(p, opts)
+    row_mass = col_mass = None
+    if not p.balanced:
+        # the plan's marginals: row_i = a_i exp((f_i - fb_i) / eps), fb one balanced f update from g
+        row_mass = np.exp(p.log_a + (f - fb) / opts.eps)
+        col_mass = np.exp(p.log_b + (g - gb) / opts.eps)
+    seconds = time.perf_counter() - t0
+    cost = float(np.exp(p.log_a) @ f + np.exp(p.log_b) @ g) if p.balanced else float("nan")
+    return SinkhornResult(f=f, g=g, iterations=it, error=err, converged=converged, cost=cost, seconds=seconds,
+                          eps=opts.eps, rho=opts.rho, center=p.center, cost_scale=p.scale, row_mass=row_mass,
+                          col_mass=col_mass)
+
+
+def transport_plan(x, y, res: SinkhornResult, a=None, b=None) -> np.ndarray:
+    """The dense plan P (n x m, float64) of a result, for small problems and tests (src/trnopt/sinkhorn.py:397-403)."""
+    root = np.sqrt(res.cost_scale)
+    x = (np.asarray(x, dtype=np.float64) - res.center) / root
+    y = (np.asarray(y, dtype=np.float64) - res.center) / root
+    log_a, log_b = _log_weights(a, len(x), "a"), _log_weights(b, len(y), "b")
+    C = ((x[:, None, :] - y[None, :, :]) ** 2).sum(axis=2)
+    return np.exp(log_a[:, None] + log_b[None, :] + (res.f[:, None] + res.g[None, :] - C) / res.eps)

@@ -44,8 +44,9 @@ class Backend:
 
     @property
     def is_rocm_gpu(self) -> bool:
-        """A GPU device of a ROCm build of PyTorch (where the fused HIP kernels run)."""
-        return self.device.startswith("cuda") and torch.version.hip is not None
+        """A GPU device of a ROCm build of PyTorch that is present (where the fused HIP kernels run)."""
+        return (self.device.startswith("cuda") and torch.version.hip is not None
+                and torch.cuda.is_available())
 
     def compile_fn(self, f):
         """f through torch.compile when this backend compiles, else f itself. One compiled function per

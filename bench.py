@@ -1,6 +1,7 @@
 """Benchmark: ms per Sinkhorn iteration (f half-step + g half-step) on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--profile-only]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+    python bench.py --profile [--reps R]     # for rocprofv3: R fused half-steps, then a 256 MiB copy
 
 Workload: synthetic balanced 10,000 x 10,000, d = 64, fp32, x ~ N(0, 1) (seed 0), y ~ N(0, 1) + 0.5
 (seed 1), uniform weights, squared-Euclidean cost, no normalisation, eps = 0.1 (the reference's
@@ -33,6 +34,15 @@ sys.path.insert(0, str(ROOT / "trainium-sinkhorn_amd"))
 N, M, D, EPS = 10_000, 10_000, 64, 0.1
 MFMA_F32_PEAK = 157.3e12
 EXP_PEAK = 9.83e12
+
+
+def profiled_traffic():
+    """Fabric bytes per fused half-step from the committed counter summary (FETCH_SIZE and WRITE_SIZE passes,
+    scaled by the copy calibration), or None if the summary is absent."""
+    import re
+    p = ROOT / "profiles" / "half_step_10k_d64_counters.md"
+    m = re.search(r"traffic_bytes_per_launch:\s*(\d+)", p.read_text()) if p.exists() else None
+    return int(m.group(1)) if m else None
 
 
 def make_inputs():
@@ -96,6 +106,33 @@ def gpu_run(steps, warmup, kernel_reps=50):
     return dict(ms_per_it=ms_per_it, half_ms=half_ms, achieved=achieved, flop=flop, e2e=e2e, loop_s=r.seconds)
 
 
+def profile_run(reps):
+    """What the rocprofv3 summaries are taken from: `reps` fused half-steps (f update) of the workload, then
+    one plain device copy of 256 MiB, whose FETCH_SIZE / WRITE_SIZE calibrate the counters (the copy reads and
+    writes exactly 262144 KiB)."""
+    import numpy as np
+    import torch
+    from trnopt import hip_sinkhorn as hk
+
+    hk.lib()
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    x, y = make_inputs()
+    X = hk.HipCloud(x, np.full(N, -np.log(N)), dev)
+    Y = hk.HipCloud(y, np.full(M, -np.log(M)), dev)
+    gh = torch.zeros(Y.npad, dtype=torch.float32, device=dev)
+    sc = hk.scalars(EPS, 1.0, dev)
+    out = torch.empty(X.npad, dtype=torch.float32, device=dev)
+    for _ in range(reps):
+        hk.half_step(X, Y, gh, sc, out=out)
+    src = torch.ones(64 << 20, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"profile: {reps} half-steps of {N} x {M} d {D}, then a 256 MiB copy", flush=True)
+
+
 def cpu_baseline(iters=2):
     """The reference's plain-PyTorch CPU path (oracle restatement), float32, block 2048, all host cores:
     `iters` fixed iterations after one untimed warm-up iteration, best of 2."""
@@ -120,11 +157,16 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-iters", type=int, default=2)
+    ap.add_argument("--profile", action="store_true", help="only the launches the rocprofv3 summaries use")
+    ap.add_argument("--reps", type=int, default=20)
     a = ap.parse_args()
     if a.gpus != 1:
         print("bench.py measures one GPU: this build's path is single-GPU (the multi-GPU row split is a design "
               "only); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
+    if a.profile:
+        profile_run(a.reps)
+        return
     g = gpu_run(a.steps, a.warmup)
     cpu = None if a.no_cpu else cpu_baseline(a.cpu_iters)
     t_roof = max(4.0 * N * M * (D + 1) / MFMA_F32_PEAK, 2.0 * N * M / EXP_PEAK)
@@ -144,7 +186,7 @@ def main():
         "config": {"workload": "balanced Sinkhorn 10000 x 10000, d 64, eps 0.1, fixed iterations", "n": N, "m": M,
                    "d": D, "eps": EPS},
         "roofline": {"bound": "mfma", "achieved": round(g["achieved"] / 1e12, 3), "peak": MFMA_F32_PEAK / 1e12,
-                     "unit": "TFLOP/s", "frac": round(g["achieved"] / MFMA_F32_PEAK, 4), "traffic": None,
+                     "unit": "TFLOP/s", "frac": round(g["achieved"] / MFMA_F32_PEAK, 4), "traffic": profiled_traffic(),
                      "kernel": "fused half-step (MFMA partial pass + merge)", "kernel_ms": round(g["half_ms"], 5),
                      "flop_per_launch": g["flop"]},
         "iteration_roofline_frac": round(t_roof * 1e3 / g["ms_per_it"], 4),

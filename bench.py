@@ -62,8 +62,8 @@ def gpu_run(steps, warmup, kernel_reps=50):
     torch.cuda.set_device(dev)
     x, y = make_inputs()
     la, lb = np.full(N, -np.log(N)), np.full(M, -np.log(M))
-    X = hk.HipCloud(x, la, dev)
-    Y = hk.HipCloud(y, lb, dev)
+    X = hk.HipCloud(x, la, dev, role=0)
+    Y = hk.HipCloud(y, lb, dev, role=1)
     loop = hk.DeviceLoop(X, Y, eps=EPS, rho_x=None, rho_y=None, sched=[], stages=[], tol=1e-4, stage_tol=1e-5,
                          max_iters=warmup + steps + 1, check_every=10, stage_max_iters=1000, fixed_iters=True,
                          balanced=True)
@@ -118,8 +118,8 @@ def profile_run(reps):
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     x, y = make_inputs()
-    X = hk.HipCloud(x, np.full(N, -np.log(N)), dev)
-    Y = hk.HipCloud(y, np.full(M, -np.log(M)), dev)
+    X = hk.HipCloud(x, np.full(N, -np.log(N)), dev, role=0)
+    Y = hk.HipCloud(y, np.full(M, -np.log(M)), dev, role=1)
     gh = torch.zeros(Y.npad, dtype=torch.float32, device=dev)
     sc = hk.scalars(EPS, 1.0, dev)
     out = torch.empty(X.npad, dtype=torch.float32, device=dev)

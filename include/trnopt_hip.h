@@ -15,9 +15,13 @@
  *   - Every entry point returns 0 on success, a negative SK_E* code for a rejected argument, or a
  *     positive hipError_t for a runtime failure. sk_last_error() describes the last failure on the
  *     calling thread. Nothing aborts the process.
- *   - Point clouds are "packed": padded to a multiple of SK_TILE points and SK_KP_ALIGN coordinates
- *     and stored in the tile-interleaved order that the MFMA kernels read with one coalesced 16-byte
- *     load per lane (sk_pack_cloud_f32 builds it from a row-major (n, d) array).
+ *   - Point clouds are "packed": padded to a multiple of SK_TILE points and SK_KP_ALIGN coordinates,
+ *     every fp32 coordinate split exactly into three bf16 pieces (v = v0 + v1 + v2), and stored in the
+ *     tile-interleaved order that the bf16 MFMA kernels read with one coalesced 16-byte load per lane
+ *     (sk_pack_cloud_f32 builds it from a row-major (n, d) fp32 array; sk_packed_bytes gives its size).
+ *     The kernels form x.y from the six leading cross products of the pieces, accumulated in fp32: as
+ *     accurate as an fp32 dot product, and bit-identical in the two directions of a pair of half-steps
+ *     (rows_role 0 and 1) over the same two clouds.
  *   - Shifted potentials follow the reference (src/trnopt/sinkhorn.py:28-33): fh = f - |x|^2.
  */
 #ifndef TRNOPT_HIP_H
@@ -30,7 +34,8 @@ extern "C" {
 #endif
 
 #define SK_TILE 32            /* points per packed tile (one 32x32 MFMA output block) */
-#define SK_KP_ALIGN 8         /* coordinates are padded to a multiple of this */
+#define SK_KP_ALIGN 16        /* coordinates are padded to a multiple of this (one bf16 MFMA K chunk) */
+#define SK_PACKED_BYTES_PER_COORD 6   /* three bf16 pieces per padded coordinate */
 #define SK_KP_MAX 128         /* largest padded dimension the kernels are built for */
 #define SK_PAD_LOG_WEIGHT (-1e9)  /* log weight of a padding point (src/trnopt/sinkhorn.py:59) */
 
@@ -52,11 +57,13 @@ int sk_pad_dim(int d);         /* d rounded up to a multiple of SK_KP_ALIGN */
 
 /*
  * Pack a row-major cloud pts (n, d), leading dimension ld >= d (device, fp32), into the tile layout
- * out (npad * kp floats, device), npad = sk_pad_points(n), kp = sk_pad_dim(d). Padding is zero.
+ * out (sk_packed_bytes(n, d) bytes, device, 16-byte aligned): npad = sk_pad_points(n) points,
+ * kp = sk_pad_dim(d) coordinates, three bf16 pieces each. Padding is zero.
  * Replaces the per-block [x^T ; 1] copies of _Cloud (src/trnopt/sinkhorn.py:159-165); the augmented
  * "1" is not stored, the column term enters the accumulator instead.
  */
-int sk_pack_cloud_f32(const float* pts, int n, int d, int ld, float* out, void* stream);
+size_t sk_packed_bytes(int n, int d);
+int sk_pack_cloud_f32(const float* pts, int n, int d, int ld, void* out, void* stream);
 
 /*
  * Row-wise log-sum-exp of a matrix product (the core of the fused kernel):
@@ -75,9 +82,12 @@ int sk_row_lse_f32(const float* xa, const float* ya, float* lse, int rows, int m
  *     lse_i = LSE_j( (2 x_i . y_j + gh[j]) / eps + log_b[j] ),
  * for i < rows_pad, without materialising the scores. Replaces make_half_step_kernel(d, rows, m)
  * (src/trnopt/nki_sinkhorn.py:175-228) and the PyTorch _half_step (src/trnopt/sinkhorn.py:108-119).
- *   x_pk   packed rows (rows_pad * kp), y_pk packed columns (m_pad * kp), kp = sk_pad_dim(d)
+ *   x_pk   packed rows, y_pk packed columns (sk_pack_cloud_f32 layout, d coordinates)
  *   xsq, off  (rows_pad,)  |x|^2 and log(target/reference); off may be NULL (= 0)
  *   gh, log_b (m_pad,)     the other side's shifted potential and log weights (padding: PAD_LOG_WEIGHT)
+ *   rows_role  0 if the rows are the first cloud of the pair (the f update of a solve), 1 if they are the
+ *          second (the g update): fixes the order of the piece products so that both directions form
+ *          bit-identical x_i . y_j
  *   sc     device float[4] = {2/eps, 1/eps, eps, kappa}, as the NKI kernel's sc (nki_sinkhorn.py:180)
  *   skip   device int or NULL: when *skip != 0 the call does nothing (the on-device loop's "done")
  *   fh     (rows_pad,) output; must not alias gh
@@ -90,9 +100,9 @@ int sk_row_lse_f32(const float* xa, const float* ya, float* lse, int rows, int m
  */
 size_t sk_half_step_workspace_bytes(int rows_pad, int m_pad, int d);
 int sk_half_step_meas_count(int rows_pad);
-int sk_half_step_f32(const float* x_pk, const float* xsq, const float* off, int rows_pad,
-                     const float* y_pk, const float* gh, const float* log_b, int m_pad, int d,
-                     const float* sc, const int* skip, float* fh,
+int sk_half_step_f32(const void* x_pk, const float* xsq, const float* off, int rows_pad,
+                     const void* y_pk, const float* gh, const float* log_b, int m_pad, int d,
+                     int rows_role, const float* sc, const int* skip, float* fh,
                      float* meas, const float* w, int n_real,
                      void* ws, size_t ws_bytes, void* stream);
 
@@ -101,7 +111,7 @@ int sk_half_step_f32(const float* x_pk, const float* xsq, const float* off, int 
  * g update, stage advance, balanced / unbalanced checks every check_every iterations, fp32 floors).
  */
 typedef struct sk_cloud_f32 {
-    const float* pk;      /* packed points (npad * kp) */
+    const void* pk;       /* packed points (sk_pack_cloud_f32 layout) */
     const float* sq;      /* |p|^2 (npad), float64 sums cast to fp32 (src/trnopt/sinkhorn.py:149) */
     const float* log_w;   /* log weights (npad), padding SK_PAD_LOG_WEIGHT */
     const float* w;       /* exp(log_w) (npad), padding 0 */

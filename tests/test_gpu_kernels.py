@@ -65,8 +65,8 @@ def _half_inputs(rows, m, d, eps, seed, pad_rows=0, pad_cols=0):
                                                 (64, 64, 128, 0.5, 0.7), (40, 3000, 1, 0.2, 1.0)])
 def test_half_step_matches_float64_and_torch(hip, rows, m, d, eps, kappa):
     x, y, gh, log_b, off = _half_inputs(rows, m, d, eps, seed=rows + m + d)
-    X = hip.HipCloud(x, np.zeros(rows), DEV, off=off)
-    Y = hip.HipCloud(y, log_b, DEV)
+    X = hip.HipCloud(x, np.zeros(rows), DEV, off=off, role=0)
+    Y = hip.HipCloud(y, log_b, DEV, role=1)
     gh_pad = np.zeros(Y.npad)
     gh_pad[:m] = gh
     gh_t = torch.as_tensor(gh_pad, dtype=torch.float32, device=DEV)
@@ -94,8 +94,8 @@ def test_half_step_convergence_partials(hip):
     rows, m, d, eps = 1000, 700, 16, 0.1
     x, y, gh, log_b, _ = _half_inputs(rows, m, d, eps, seed=5)
     w = np.full(rows, 1.0 / rows)
-    X = hip.HipCloud(x, np.log(w), DEV)
-    Y = hip.HipCloud(y, log_b, DEV)
+    X = hip.HipCloud(x, np.log(w), DEV, role=0)
+    Y = hip.HipCloud(y, log_b, DEV, role=1)
     gh_t = torch.zeros(Y.npad, dtype=torch.float32, device=DEV)
     gh_t[:m] = torch.as_tensor(gh, dtype=torch.float32)
     sc = hip.scalars(eps, 1.0, DEV)
@@ -107,7 +107,7 @@ def test_half_step_convergence_partials(hip):
     meas = torch.zeros(2 * nmeas, dtype=torch.float32, device=DEV)
     ws = torch.empty(lb.sk_half_step_workspace_bytes(X.npad, Y.npad, d), dtype=torch.uint8, device=DEV)
     st = lb.sk_half_step_f32(X.pk.data_ptr(), X.sq.data_ptr(), None, X.npad, Y.pk.data_ptr(), gh_t.data_ptr(),
-                             Y.log_w.data_ptr(), Y.npad, d, sc.data_ptr(), None, buf.data_ptr(), meas.data_ptr(),
+                             Y.log_w.data_ptr(), Y.npad, d, 0, sc.data_ptr(), None, buf.data_ptr(), meas.data_ptr(),
                              X.w.data_ptr(), X.n, ws.data_ptr(), ws.numel(), torch.cuda.current_stream().cuda_stream)
     assert st == 0
     torch.testing.assert_close(buf, new, rtol=0, atol=0)
@@ -122,10 +122,39 @@ def test_half_step_convergence_partials(hip):
 
 def test_errors_are_reported_not_fatal(hip):
     lb = hip.lib()
-    assert lb.sk_half_step_f32(None, None, None, 32, None, None, None, 32, 4, None, None, None, None, None, 1,
+    assert lb.sk_half_step_f32(None, None, None, 32, None, None, None, 32, 4, 0, None, None, None, None, None, 1,
                                None, 0, None) == -1
     assert b"null pointer" in lb.sk_last_error()
     a = torch.zeros(64 * 200, device=DEV)
     assert lb.sk_row_lse_f32(a.data_ptr(), a.data_ptr(), a.data_ptr(), 10, 10, 200, a.data_ptr(), 1 << 20, None) == -2
     with pytest.raises(ValueError):
         hip.row_lse(torch.zeros(3, 200, device=DEV), torch.zeros(4, 200, device=DEV))
+
+
+def _dots_by_half_step(hip, rows_pts, rows_role, col_pt):
+    """x_i . y for every row i and one column point y, read exactly off a half-step: one real column (log b = 0,
+    gh = 0, the padding columns weigh exactly 0), |x|^2 = 0, eps = 1, kappa = 1 gives fh_i = -2 x_i . y."""
+    n, d = rows_pts.shape
+    R = hip.HipCloud(rows_pts, np.zeros(n), DEV, role=rows_role)
+    C = hip.HipCloud(col_pt[None, :], np.zeros(1), DEV, role=1 - rows_role)
+    R.sq.zero_()
+    gh = torch.zeros(C.npad, dtype=torch.float32, device=DEV)
+    out = hip.half_step(R, C, gh, hip.scalars(1.0, 1.0, DEV)).cpu().numpy()[:n]
+    return -0.5 * out
+
+
+@pytest.mark.parametrize("d", [3, 16, 64, 100, 128])
+def test_f_and_g_updates_form_bit_identical_dots(hip, d):
+    """The f update (rows x, role 0) and the g update (rows y, role 1) issue the piece products in the same
+    order: x_i . y_j agrees bit for bit in both directions, and is fp32-accurate."""
+    rng = np.random.default_rng(d)
+    x = rng.normal(size=(70, d)).astype(np.float32)
+    y = (rng.normal(size=(40, d)) * 1.7 + 0.3).astype(np.float32)
+    for j in (0, 7, 39):
+        f_side = _dots_by_half_step(hip, x, 0, y[j])                     # x_i . y_j, i = 0..69
+        for i in (0, 33, 69):
+            g_side = _dots_by_half_step(hip, y, 1, x[i])                 # y_j' . x_i, j' = 0..39
+            assert f_side[i].tobytes() == np.float32(g_side[j]).tobytes(), (i, j, f_side[i], g_side[j])
+        exact = x.astype(np.float64) @ y[j].astype(np.float64)
+        bound = np.abs(x.astype(np.float64)) @ np.abs(y[j].astype(np.float64))
+        assert np.all(np.abs(f_side - exact) <= 4e-7 * bound + 1e-30)

@@ -68,12 +68,14 @@ def test_constants_match_the_header(hk):
         assert lb.sk_pad_points(n) == hk.pad_points(n)
     for d in (1, 7, 8, 30, 64, 65, 128):
         assert lb.sk_pad_dim(d) == hk.pad_dim(d)
+        assert lb.sk_packed_bytes(1000, d) == hk.packed_bytes(1000, d) == 1024 * hk.pad_dim(d) * 6
+    assert lb.sk_packed_bytes(10, 129) == 0 and lb.sk_packed_bytes(0, 8) == 0
 
 
 def test_rejected_arguments_return_codes_not_aborts(hk):
     """Validation that happens before any device call: null pointers, shapes, the dimension limit."""
     lb = hk.lib()
-    assert lb.sk_half_step_f32(None, None, None, 32, None, None, None, 32, 4, None, None, None, None, None, 1,
+    assert lb.sk_half_step_f32(None, None, None, 32, None, None, None, 32, 4, 0, None, None, None, None, None, 1,
                                None, 0, None) == -1
     assert b"null pointer" in lb.sk_last_error()
     fake = 4096   # a non-null address that is never dereferenced: validation fails first
@@ -82,6 +84,7 @@ def test_rejected_arguments_return_codes_not_aborts(hk):
     assert lb.sk_row_lse_f32(fake, fake, fake, 0, 10, 8, fake, 1 << 20, None) == -2
     assert lb.sk_pack_cloud_f32(None, 10, 4, 4, None, None) == -1
     assert lb.sk_pack_cloud_f32(fake, 10, 8, 4, fake, None) == -2          # ld < d
+    assert lb.sk_pack_cloud_f32(fake, 10, 4, 4, fake + 8, None) == -1      # out not 16-byte aligned
     assert lb.sk_loop_init_f32(None, None) == -1
     assert lb.sk_loop_run_f32(None, 1, None) == -1
 
@@ -90,14 +93,18 @@ def test_half_step_shape_rules(hk):
     lb = hk.lib()
     fake = 4096
     # rows_pad not a multiple of 32
-    assert lb.sk_half_step_f32(fake, fake, None, 33, fake, fake + 256, fake, 32, 4, fake, None, fake + 512, None,
+    assert lb.sk_half_step_f32(fake, fake, None, 33, fake, fake + 256, fake, 32, 4, 0, fake, None, fake + 512, None,
                                None, 1, fake, 1 << 20, None) == -2
     # fh aliasing gh
-    assert lb.sk_half_step_f32(fake, fake, None, 32, fake, fake, fake, 32, 4, fake, None, fake, None, None, 1,
+    assert lb.sk_half_step_f32(fake, fake, None, 32, fake, fake, fake, 32, 4, 0, fake, None, fake, None, None, 1,
                                fake, 1 << 20, None) == -1
     # meas without w
-    assert lb.sk_half_step_f32(fake, fake, None, 32, fake, fake + 256, fake, 32, 4, fake, None, fake + 512, fake,
+    assert lb.sk_half_step_f32(fake, fake, None, 32, fake, fake + 256, fake, 32, 4, 0, fake, None, fake + 512, fake,
                                None, 1, fake, 1 << 20, None) == -1
+    # rows_role other than 0 / 1
+    assert lb.sk_half_step_f32(fake, fake, None, 32, fake, fake + 256, fake, 32, 4, 2, fake, None, fake + 512, None,
+                               None, 1, fake, 1 << 20, None) == -1
+    assert b"rows_role" in lb.sk_last_error()
 
 
 # ---------------------------------------------------------------------------------------------------------

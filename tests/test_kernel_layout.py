@@ -1,18 +1,21 @@
 """CPU emulation of the HIP kernels' index arithmetic (trainium-sinkhorn_amd/csrc).
 
-Every load and store of pack_cloud_kernel, lse_partial_kernel and lse_finalize_kernel is replayed in numpy
-with the kernels' own formulas (workgroup renumbering, stream-K ranges, partial slots, tile-interleaved
-packing, the v_mfma_f32_32x32x2_f32 operand and accumulator lane mapping), asserting that every index is
-inside its buffer and that the emulated result equals a direct float64 log-sum-exp. Run before any kernel
-change goes to the GPU; it needs no GPU.
+Every load and store of pack_cloud_kernel, lse_partial_kernel (global loads, LDS staging and reads, partial
+slots) and lse_finalize_kernel is replayed in numpy with the kernels' own formulas (workgroup renumbering,
+stream-K ranges, partial slots, the three-piece bf16 packing, the v_mfma_f32_32x32x16_bf16 operand and
+accumulator lane mapping, the product order of both row roles), asserting that every index is inside its
+buffer and that the emulated result equals a direct float64 log-sum-exp. It needs no GPU.
 """
 
 import numpy as np
 import pytest
 from scipy.special import logsumexp
 
-TILE, WAVES, XCDS = 32, 4, 8
+TILE, WAVES, XCDS, RB, PIECES, BLOCK = 32, 4, 8, 2, 3, 256
+ROWS_PER_GROUP = TILE * RB * WAVES
 EMPTY = -1.0e30
+FIRST = [0, 0, 1, 0, 1, 2]     # (first-cloud piece, second-cloud piece) of the six products
+SECOND = [0, 1, 0, 2, 1, 0]
 
 
 def pad_points(n):
@@ -20,28 +23,51 @@ def pad_points(n):
 
 
 def pad_dim(d):
-    return -(-d // 8) * 8
+    return -(-d // 16) * 16
 
 
-def pack(src, n, d, kp):
-    """pack_cloud_kernel: dst[idx] for every idx < npad * kp."""
+def bf16_rne(v):
+    """float32 -> nearest bfloat16 (ties to even), returned as float32."""
+    u = np.asarray(v, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    return u.astype(np.uint32).view(np.float32)
+
+
+def split3(v):
+    v = np.asarray(v, dtype=np.float32)
+    a0 = bf16_rne(v)
+    r1 = (v - a0).astype(np.float32)
+    a1 = bf16_rne(r1)
+    a2 = bf16_rne((r1 - a1).astype(np.float32))
+    return a0, a1, a2
+
+
+def pack(src, n, d):
+    """pack_cloud_kernel: the (npad / 32 * nc * 3 * 64, 8) array of 16-byte units (as 8 float32 values)."""
+    kp = pad_dim(d)
+    nc = kp // 16
     npad = pad_points(n)
-    kq = kp // 8
-    idx = np.arange(npad * kp)
-    e = idx & 3
-    t = idx >> 2
-    r = t % 32
-    t //= 32
-    h = t % 2
-    t //= 2
-    q = t % kq
-    T = t // kq
-    row = T * 32 + r
-    k = h * (kp // 2) + q * 4 + e
-    ok = (row < n) & (k < d)
-    src_idx = np.where(ok, row * d + k, 0)
-    assert src_idx.max() < src.size
-    return np.where(ok, src.ravel()[src_idx], 0.0)
+    out = np.full((npad // TILE * nc * PIECES * 64, 8), np.nan, dtype=np.float32)
+    idx = np.arange(npad // TILE * nc * 64)                  # one thread per (tile, chunk, lane)
+    lane = idx % 64
+    cc = (idx // 64) % nc
+    T = idx // (64 * nc)
+    r, h = lane & 31, lane >> 5
+    row = T * TILE + r
+    e = np.arange(8)
+    k = 16 * cc[:, None] + 8 * h[:, None] + e[None, :]
+    ok = (row[:, None] < n) & (k < d)
+    flat = np.where(ok, row[:, None] * d + k, 0)
+    assert flat.max() < src.size
+    v = np.where(ok, src.ravel()[flat], 0.0).astype(np.float32)
+    pieces = split3(v)
+    base = (T * nc + cc) * (PIECES * 64) + lane
+    for p in range(PIECES):
+        dst = base + 64 * p
+        assert dst.max() < out.shape[0]
+        out[dst] = pieces[p]
+    assert not np.isnan(out).any(), "every unit written"
+    return out
 
 
 class Split:
@@ -58,9 +84,9 @@ class Split:
         return self.owner((g + 1) * self.nt - 1)
 
 
-def plan(rows_pad, m_pad, kp, rb, ncu=256, per_cu=2):
+def plan(rows_pad, m_pad, ncu=256, per_cu=1):
     nrb, nt = rows_pad // TILE, m_pad // TILE
-    ngroups = -(-nrb // (WAVES * rb))
+    ngroups = -(-rows_pad // ROWS_PER_GROUP)
     work = ngroups * nt
     P = max(1, min(ncu * per_cu, work))
     s = Split(work, nt, P)
@@ -74,21 +100,40 @@ def xcd_contiguous(b, P):
     return xcd * q + min(xcd, r) + i
 
 
-def emulate_lse(xa, ya, rb=1, ncu=256, per_cu=2, colterm=None, c=np.log2(np.e)):
-    """Row LSE (plain mode: alpha = 1 on a 0 / -1e30 mask, beta = 0) through the kernels' index math, with the
+def mfma_32x32x16(Aop, Bop):
+    """v_mfma_f32_32x32x16_bf16 on per-lane operands (64, 8): lane l holds A[m = l % 32][k = 8 (l / 32) + e] and
+    B[k = 8 (l / 32) + e][n = l % 32]. Returns the (64, 16) accumulator: lane l, register r holds
+    D[m = 8 (r / 4) + 4 (l / 32) + r % 4][n = l % 32]."""
+    A = np.concatenate([Aop[:32], Aop[32:]], axis=1).astype(np.float64)    # (m, k)
+    B = np.concatenate([Bop[:32], Bop[32:]], axis=1).astype(np.float64)    # (n, k)
+    D = A @ B.T                                                             # (m, n); bf16 products exact
+    lane = np.arange(64)
+    r = np.arange(16)
+    m = 8 * (r[None, :] // 4) + 4 * (lane[:, None] // 32) + r[None, :] % 4
+    return D[m, (lane % 32)[:, None]]
+
+
+def emulate_lse(xa, ya, role=0, ncu=256, per_cu=1, c=np.log2(np.e)):
+    """Row LSE (plain mode: alpha = 1 on a 0 / -1e30 mask, beta = 0) through the kernels' index math, the
     score / max / sum arithmetic in float32 as on the GPU (overflow or NaN raises)."""
     rows, K = xa.shape
     m = ya.shape[0]
     kp, rp, mp = pad_dim(K), pad_points(rows), pad_points(m)
-    kq = kp // 8
-    xr = pack(xa, rows, K, kp)
-    yc = pack(ya, m, K, kp)
-    u = np.where(np.arange(mp) < m, 0.0, -1.0e30) if colterm is None else colterm
-    nrb, nt, ngroups, s, slots = plan(rp, mp, kp, rb, ncu, per_cu)
+    nc = kp // 16
+    tile16 = nc * PIECES * 64
+    per_thread = -(-tile16 // BLOCK)
+    xr = pack(xa, rows, K)
+    yc = pack(ya, m, K)
+    u = np.where(np.arange(mp) < m, 0.0, -1.0e30).astype(np.float32)
+    nrb, nt, ngroups, s, slots = plan(rp, mp, ncu, per_cu)
     part = np.full((slots, rp, 2), np.nan)
     lane = np.arange(64)
     h = lane >> 5
+    tid = np.arange(BLOCK)
+    cj = tid & 31
     seen = np.zeros((ngroups, nt), dtype=int)
+    cf = np.float32(c)
+    ra, ca = (FIRST, SECOND) if role == 0 else (SECOND, FIRST)
     for b in range(s.P):
         p = xcd_contiguous(b, s.P)
         u1 = (p + 1) * s.work // s.P
@@ -100,41 +145,49 @@ def emulate_lse(xa, ya, rb=1, ncu=256, per_cu=2, colterm=None, c=np.log2(np.e)):
             slot = p - s.first(g)
             assert 0 <= slot < slots
             seen[g, tb:te] += 1
+            # LDS staging of every tile of the segment (both buffers), as the workgroup does it
+            lds_y = np.full((2 * tile16, 8), np.nan, dtype=np.float32)
+            lds_col = np.full(64, np.nan, dtype=np.float32)
+            staged = {}
+            for t in list(range(tb, te)) + [te - 1]:
+                buf = (t - tb) & 1
+                for k in range(per_thread):
+                    idx = np.where(tid + k * BLOCK < tile16, tid + k * BLOCK, tile16 - 1)
+                    gsrc = t * tile16 + idx
+                    assert gsrc.max() < yc.shape[0]
+                    dst = buf * tile16 + idx
+                    assert dst.max() < lds_y.shape[0]
+                    lds_y[dst] = yc[gsrc]
+                assert (t * 32 + cj).max() < mp
+                lds_col[buf * 32 + cj] = u[t * 32 + cj]
+                staged[t] = (lds_y[buf * tile16:(buf + 1) * tile16].copy(), lds_col[buf * 32:buf * 32 + 32].copy())
             for wv in range(WAVES):
-                rb0 = (g * WAVES + wv) * rb
-                if rb0 >= nrb:
-                    continue
-                for bb in range(rb):
-                    blk = rb0 + bb if rb0 + bb < nrb else rb0
+                rb0 = (g * WAVES + wv) * RB
+                for bb in range(RB):
+                    blk = rb0 + bb if rb0 + bb < nrb else nrb - 1
+                    xi = blk * tile16 + (np.arange(nc)[:, None, None] * PIECES + np.arange(PIECES)[None, :, None]) * 64 \
+                        + lane[None, None, :]
+                    assert xi.max() < xr.shape[0]
+                    xv = xr[xi]                                    # (nc, 3, 64, 8)
                     M = np.full(64, EMPTY, dtype=np.float32)
                     S = np.zeros(64, dtype=np.float32)
-                    cf = np.float32(c)
-                    # xv[q][e] of lane l: xr[blk * 32 * kp + (q * 64 + l) * 4 + e]
-                    xi = blk * 32 * kp + (np.arange(kq)[:, None, None] * 64 + lane[None, :, None]) * 4 \
-                        + np.arange(4)[None, None, :]
-                    assert xi.max() < xr.size
-                    xv = xr[xi]                                    # (kq, 64, 4)
                     for t in range(tb, te):
-                        yi = t * 64 * kq * 4 + (np.arange(kq)[:, None, None] * 64 + lane[None, :, None]) * 4 \
-                            + np.arange(4)[None, None, :]
-                        assert yi.max() < yc.size
-                        yv = yc[yi]                                # (kq, 64, 4)
-                        ui = t * 32 + 8 * np.arange(4)[None, :, None] + 4 * h[:, None, None] + np.arange(4)[None, None, :]
-                        assert ui.max() < mp
-                        init = u[ui].reshape(64, 16)               # lane, reg = 4 q + e
-                        # MFMA: D[mrow][ncol] += sum_k A[mrow][k] B[k][ncol]; A[mrow][k] = yv of lane mrow + 32 k,
-                        # B[k][ncol] = xv of lane ncol + 32 k; lane l reg r holds D[8 (r/4) + 4 (l/32) + r%4][l%32]
-                        A = yv.transpose(1, 0, 2).reshape(64, kq * 4)       # lane -> its kp/2 operand values
-                        Bm = xv.transpose(1, 0, 2).reshape(64, kq * 4)
-                        D = A[:32] @ Bm[:32].T + A[32:] @ Bm[32:].T          # (mrow, ncol)
-                        r = np.arange(16)
-                        mrow = 8 * (r[None, :] // 4) + 4 * (lane[:, None] // 32) + (r[None, :] % 4)
-                        # zero-initialised MFMA chain, then the column term on the VALU (accumulator units)
-                        acc = D[mrow, (lane % 32)[:, None]].astype(np.float32) + init.astype(np.float32)
-                        Mn = np.maximum(M, acc.max(axis=1))
-                        cf = np.float32(c)
+                        ybuf, cbuf = staged[t]
+                        yi = (np.arange(nc)[:, None, None] * PIECES + np.arange(PIECES)[None, :, None]) * 64 \
+                            + lane[None, None, :]
+                        assert yi.max() < tile16
+                        yv = ybuf[yi]
+                        ci = 8 * np.arange(4)[None, :, None] + 4 * h[:, None, None] + np.arange(4)[None, None, :]
+                        assert ci.max() < 32
+                        col = cbuf[ci].reshape(64, 16)
+                        acc = np.zeros((64, 16))
+                        for cc in range(nc):
+                            for pp in range(6):
+                                acc += mfma_32x32x16(yv[cc, ca[pp]], xv[cc, ra[pp]])
+                        a = (acc.astype(np.float32) + col).astype(np.float32)
+                        Mn = np.maximum(M, a.max(axis=1))
                         with np.errstate(over="raise", invalid="raise"):
-                            S = S * np.exp2(cf * (M - Mn)) + np.exp2(cf * (acc - Mn[:, None])).sum(axis=1)
+                            S = S * np.exp2(cf * (M - Mn)) + np.exp2(cf * (a - Mn[:, None])).sum(axis=1)
                         M = Mn
                     Mo, So = M[lane ^ 32], S[lane ^ 32]
                     Mn = np.maximum(M, Mo)
@@ -146,11 +199,9 @@ def emulate_lse(xa, ya, rb=1, ncu=256, per_cu=2, colterm=None, c=np.log2(np.e)):
                         part[slot, idx, 0], part[slot, idx, 1] = Mn[:32], Sn[:32]
             uu += te - tb
     assert np.all(seen == 1), "every (row group, tile) unit exactly once"
-    # finalisation
     out = np.empty(rp)
-    rows_per_group = 32 * rb * WAVES
     for i in range(rp):
-        g = i // rows_per_group
+        g = i // ROWS_PER_GROUP
         p0, p1 = s.first(g), s.last(g)
         assert p1 - p0 + 1 <= slots
         v = part[: p1 - p0 + 1, i]
@@ -160,27 +211,27 @@ def emulate_lse(xa, ya, rb=1, ncu=256, per_cu=2, colterm=None, c=np.log2(np.e)):
     return out[:rows], dict(slots=slots, P=s.P, work=s.work)
 
 
-@pytest.mark.parametrize("rows,m,K,rb,ncu", [(1, 1, 1, 1, 256), (1, 1, 1, 2, 256), (2, 5, 3, 1, 256), (33, 31, 8, 1, 256), (64, 300, 65, 1, 256),
-                                             (300, 100, 5, 2, 256), (257, 1000, 17, 2, 4), (500, 70, 30, 1, 3),
-                                             (129, 4097, 12, 1, 8), (1000, 40, 64, 2, 256)])
-def test_emulated_partial_and_finalize_match_logsumexp(rows, m, K, rb, ncu):
+@pytest.mark.parametrize("rows,m,K,ncu,role", [(1, 1, 1, 256, 0), (1, 1, 1, 256, 1), (2, 5, 3, 256, 0),
+                                               (33, 31, 8, 256, 1), (64, 300, 65, 256, 0), (300, 100, 5, 3, 1),
+                                               (257, 1000, 17, 4, 0), (500, 70, 30, 3, 0), (129, 1500, 12, 8, 1),
+                                               (600, 40, 128, 256, 0)])
+def test_emulated_partial_and_finalize_match_logsumexp(rows, m, K, ncu, role):
     rng = np.random.default_rng(rows + m + K)
-    xa = rng.normal(size=(rows, K))
-    ya = rng.normal(size=(m, K)) * 0.5
-    out, info = emulate_lse(xa, ya, rb=rb, ncu=ncu)
-    # float32 score arithmetic as on the GPU (float64 contraction): rounding-level agreement
-    np.testing.assert_allclose(out, logsumexp(xa @ ya.T, axis=1), rtol=0, atol=2e-5)
+    xa = rng.normal(size=(rows, K)).astype(np.float32)
+    ya = (rng.normal(size=(m, K)) * 0.5).astype(np.float32)
+    out, info = emulate_lse(xa, ya, role=role, ncu=ncu)
+    np.testing.assert_allclose(out, logsumexp(xa.astype(np.float64) @ ya.astype(np.float64).T, axis=1),
+                               rtol=0, atol=2e-5)
 
 
 @pytest.mark.parametrize("n,m", [(10_000, 10_000), (7355, 8962), (8962, 7355), (65_536, 65_536), (32, 100_000),
                                  (100_000, 32), (2048, 2048), (1, 5)])
-@pytest.mark.parametrize("rb", [1, 2])
-@pytest.mark.parametrize("ncu", [256, 304, 80])
-def test_split_covers_work_and_slot_bounds(n, m, rb, ncu):
+@pytest.mark.parametrize("ncu,per_cu", [(256, 1), (304, 1), (80, 1), (256, 2)])
+def test_split_covers_work_and_slot_bounds(n, m, ncu, per_cu):
     """The stream-K split at full sizes: units covered once, slot indexes below the planned slot count,
     workgroup renumbering a bijection."""
     rp, mp = pad_points(n), pad_points(m)
-    nrb, nt, ngroups, s, slots = plan(rp, mp, 64, rb, ncu)
+    nrb, nt, ngroups, s, slots = plan(rp, mp, ncu, per_cu)
     P = s.P
     ids = sorted(xcd_contiguous(b, P) for b in range(P))
     assert ids == list(range(P))
@@ -190,29 +241,65 @@ def test_split_covers_work_and_slot_bounds(n, m, rb, ncu):
         p0, p1 = s.first(g), s.last(g)
         assert starts[p0] <= g * nt < starts[p0 + 1] or starts[p0] == starts[p0 + 1] == g * nt
         assert p1 - p0 + 1 <= slots
-        # every workgroup that owns a unit of group g is in [p0, p1]
         lo, hi = g * nt, (g + 1) * nt
         owners = [p for p in range(P) if starts[p] < hi and starts[p + 1] > lo]
         assert owners[0] >= p0 and owners[-1] <= p1
-    # workspace the host allocates for the partials is slots * rows_pad float2
     assert slots * rp * 8 < 2 ** 31 * 8
+
+
+def test_split3_is_exact():
+    rng = np.random.default_rng(1)
+    for scale in (1.0, 1e-3, 7.3e4, 1e-20, 3e30):
+        v = (rng.normal(size=100_000) * scale).astype(np.float32)
+        a0, a1, a2 = split3(v)
+        for a in (a0, a1, a2):                    # each piece is a bfloat16 value
+            assert np.all((a.view(np.uint32) & 0xFFFF) == 0)
+        np.testing.assert_array_equal(a0.astype(np.float64) + a1 + a2, v.astype(np.float64))
+
+
+def test_six_products_are_fp32_accurate_and_symmetric():
+    """The six leading piece products reproduce x.y to fp32 accuracy, and the transposed product order of the
+    other row role adds the same terms in the same order."""
+    rng = np.random.default_rng(2)
+    x = rng.normal(size=(50, 64)).astype(np.float32)
+    y = (rng.normal(size=(40, 64)) + 0.5).astype(np.float32)
+    xs, ys = split3(x), split3(y)
+    exact = x.astype(np.float64) @ y.astype(np.float64).T
+    bound = np.abs(x.astype(np.float64)) @ np.abs(y.astype(np.float64)).T
+    approx = sum(xs[FIRST[p]].astype(np.float64) @ ys[SECOND[p]].astype(np.float64).T for p in range(6))
+    assert np.max(np.abs(approx - exact) / bound) < 2.0 ** -22
+
+    def accumulate(role, rows, cols, swap_rule=True):
+        """float32 sum of the six products in issue order, with the kernel's piece choice for `role`."""
+        ra, ca = (FIRST, SECOND) if (role == 0 or not swap_rule) else (SECOND, FIRST)
+        acc = np.zeros((rows[0].shape[0], cols[0].shape[0]), dtype=np.float32)
+        for p in range(6):
+            acc = (acc + (rows[ra[p]].astype(np.float64) @ cols[ca[p]].astype(np.float64).T).astype(np.float32))
+        return acc
+
+    f = accumulate(0, xs, ys)            # f update: rows x (role 0)
+    g = accumulate(1, ys, xs)            # g update: rows y (role 1)
+    np.testing.assert_array_equal(f, g.T)
+    # a rule that does not transpose the piece order for role 1 adds the cross terms in another order
+    g_wrong = accumulate(1, ys, xs, swap_rule=False)
+    assert np.abs(f - g_wrong.T).max() > 0
 
 
 def test_pack_layout_roundtrip():
     rng = np.random.default_rng(1)
     for n, d in [(1, 1), (31, 7), (33, 64), (100, 65), (64, 128)]:
-        x = rng.normal(size=(n, d))
+        x = rng.normal(size=(n, d)).astype(np.float32)
         kp = pad_dim(d)
-        pk = pack(x, n, d, kp)
+        nc = kp // 16
+        pk = pack(x, n, d)
         npad = pad_points(n)
-        # invert: point T*32 + r, coordinate h*kp/2 + 4q + e at ((T*kq + q)*2 + h)*32 + r)*4 + e
-        kq = kp // 8
         back = np.zeros((npad, kp))
-        for T in range(npad // 32):
-            for q in range(kq):
-                for h in range(2):
-                    for r in range(32):
-                        base = (((T * kq + q) * 2 + h) * 32 + r) * 4
-                        back[T * 32 + r, h * kp // 2 + 4 * q: h * kp // 2 + 4 * q + 4] = pk[base: base + 4]
-        np.testing.assert_array_equal(back[:n, :d], x)
+        for T in range(npad // TILE):
+            for cc in range(nc):
+                for p in range(PIECES):
+                    for lane in range(64):
+                        r, h = lane & 31, lane >> 5
+                        unit = pk[((T * nc + cc) * PIECES + p) * 64 + lane]
+                        back[T * TILE + r, 16 * cc + 8 * h:16 * cc + 8 * h + 8] += unit
+        np.testing.assert_array_equal(back[:n, :d], x.astype(np.float64))
         assert np.all(back[n:] == 0) and np.all(back[:, d:] == 0)

@@ -9,14 +9,17 @@ namespace sk {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 constexpr float kLog2e = 1.44269504088896340736f;
 constexpr float kLn2 = 0.69314718055994530942f;
 constexpr float kEmpty = -1.0e30f;     // running max of a row before its first column (finite on purpose)
 constexpr int kWaves = 4;              // waves per workgroup of the partial kernel (one per SIMD)
 constexpr int kBlock = kWaves * 64;
+constexpr int kRowBlocks = 2;          // 32-row blocks per wave (independent MFMA accumulator chains)
 constexpr int kXcds = 8;
-constexpr int kMaxKq = 16;             // kp = 8 * kq <= 128
+constexpr int kMaxChunks = 8;          // K chunks of 16 coordinates: kp = 16 * nc <= 128
+constexpr int kPieces = 3;             // bf16 pieces per fp32 coordinate
 
 enum Mode { kHalfStep = 0, kPlainLse = 1 };
 
@@ -40,8 +43,8 @@ __host__ __device__ inline int last_wg(int g, const Split& s) {
 }
 
 struct PartialArgs {
-    const float* xr;    // packed rows
-    const float* yc;    // packed columns
+    const bf16x8* xr;   // packed rows (three bf16 pieces per coordinate)
+    const bf16x8* yc;   // packed columns
     const float* u;     // column term = alpha * u + beta * v  (m_pad each)
     const float* v;
     const float* sc;    // {2/eps, 1/eps, eps, kappa} (half-step mode)
@@ -50,10 +53,11 @@ struct PartialArgs {
     int nrb;            // row blocks of 32
     int rows_pad;
     int mode;
+    int rows_role;      // 0: the rows are the first cloud of the pair, 1: the second (piece order)
     Split s;
 };
 
-// Launch the partial kernel for kp = 8 * kq and RB = rb row blocks per wave on P workgroups.
-hipError_t launch_partial(const PartialArgs& a, int kq, int rb, hipStream_t stream);
+// Launch the partial kernel for kp = 16 * nc on P workgroups.
+hipError_t launch_partial(const PartialArgs& a, int nc, hipStream_t stream);
 
 }  // namespace sk

@@ -9,31 +9,26 @@
 //
 //     a_ij = x_i . y_j + (gh_j + eps * log b_j) / 2           ("accumulator units")
 //
-// the score is c a_ij in log2 units. x_i . y_j is a fp32 MFMA contraction from zero over the padded
-// dimension kp (bit-identical in the f and g updates, so a dominant pair's rounding cannot drive the two
-// potentials apart); the column term is added on the VALU. The running (max, sum) of a row is kept as
+// the score is c a_ij in log2 units. x_i . y_j is accumulated by bf16 MFMAs from an exact three-way bf16
+// split of the fp32 coordinates (sk_lse_partial.hip), bit-identical in the f and g updates; the column term
+// is added on the VALU. The running (max, sum) of a row is kept as
 //
 //     eps * lse_i = 2 M_i + eps ln(2) log2 S_i,   S_i = sum_j exp2(c (a_ij - M_i)),  M_i = max_j a_ij.
 //
-// MFMA orientation. v_mfma_f32_32x32x2_f32 computes D(32x32) += A(32x2) * B(2x32). A holds 32 columns j
-// (the "y" side), B holds 32 rows i (the "x" side), so lane l's 16 accumulators all belong to row
-// i = l % 32 and to 16 different columns j. Row reductions therefore stay inside a lane; lanes l and
-// l + 32 (the two K halves of the operand layout) are merged once per work segment.
+// Packed cloud layout. Points are padded to a multiple of 32 (one tile), coordinates to kp = 16 * nc, and
+// every coordinate v is stored as three bf16 pieces (v0 = bf16(v), v1 = bf16(v - v0), v2 = v - v0 - v1, all
+// exact). Within tile T, the 16-byte unit ((T * nc + c) * 3 + p) * 64 + 32 h + r holds piece p of coordinates
+// [16 c + 8 h, 16 c + 8 h + 8) of point 32 T + r: lane l = 32 h + r reads its v_mfma_f32_32x32x16_bf16
+// operand for K chunk c with one coalesced 16-byte load (a wave reads 1 KB contiguous). The same layout
+// serves a cloud as rows (one half-step) and as columns (the other). 6 kp bytes per point.
 //
-// Packed cloud layout ("tile-interleaved"). Points are padded to a multiple of 32 (one tile) and
-// coordinates to kp = 8 * KQ. Within tile T the float4 number (q * 64 + h * 32 + r) holds
-// coordinates [h * kp/2 + 4q, h * kp/2 + 4q + 4) of point T * 32 + r. Lane l = h * 32 + r then reads its
-// operand for MFMA steps s = 4q .. 4q+3 with ONE coalesced 16-byte load per q (the wave reads 1 KB
-// contiguous), and MFMA step s contracts coordinates s and kp/2 + s. The same layout serves a cloud in
-// either role (rows in one half-step, columns in the other).
-//
-// Work decomposition ("stream-K" over row groups x column tiles). A workgroup is 4 waves; wave w of a
-// workgroup owns RB row blocks of 32 rows of a row group (4 * RB blocks) and all 4 waves walk the same
-// column tiles, so a column tile is fetched from L2 once per workgroup and hit in L1 by the other waves.
-// The (row group, column tile) units are split into equal contiguous ranges, one per workgroup, so every
-// workgroup does the same amount of MFMA work whatever n and m are. A range may end inside a row group;
-// each (workgroup, row group) segment writes a partial (M, S) per row into its own slot, and a
-// finalisation pass merges the slots of every row and applies the kappa / offset epilogue.
+// Work decomposition ("stream-K" over row groups x column tiles). A workgroup is 4 waves, one per SIMD;
+// wave w owns 2 row blocks of 32 rows of a row group (256 rows) and all 4 waves walk the same column tiles,
+// which the workgroup stages in LDS once. The (row group, column tile) units are split into equal contiguous
+// ranges, one per workgroup (one workgroup per CU), so every workgroup does the same amount of MFMA work
+// whatever n and m are. A range may end inside a row group; each (workgroup, row group) segment writes a
+// partial (M, S) per row into its own slot, and a finalisation pass merges the slots of every row and
+// applies the kappa / offset epilogue.
 //
 // The on-device loop (src/trnopt/sinkhorn.py:346-378) is three more tiny pieces: the g update's
 // finalisation also produces per-block convergence partials, and a one-wave control kernel advances
@@ -69,23 +64,34 @@ __device__ __forceinline__ float lg2(float x) { return __builtin_amdgcn_logf(x);
 // ---------------------------------------------------------------------------------------------------
 // Pack a row-major (n, d) cloud into the tile-interleaved layout.
 
-__global__ void pack_cloud_kernel(const float* __restrict__ src, int n, int d, int ld,
-                                  float* __restrict__ dst, int npad, int kp) {
+__global__ void pack_cloud_kernel(const float* __restrict__ src, int n, int d, int ld, bf16x8* __restrict__ dst,
+                                  int npad, int nc) {
+    // one thread per (tile, K chunk, lane): 8 coordinates, three pieces each
     const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    const long long total = (long long)npad * kp;
+    const long long total = (long long)(npad / SK_TILE) * nc * 64;
     if (idx >= total) return;
-    const int kq = kp / 8;
-    const int e = (int)(idx & 3);
-    long long t = idx >> 2;
-    const int r = (int)(t % 32);
-    t /= 32;
-    const int h = (int)(t % 2);
-    t /= 2;
-    const int q = (int)(t % kq);
-    const long long T = t / kq;
-    const long long row = T * 32 + r;
-    const int k = h * (kp / 2) + q * 4 + e;
-    dst[idx] = (row < n && k < d) ? src[row * ld + k] : 0.0f;
+    const int lane = (int)(idx % 64);
+    const int cc = (int)((idx / 64) % nc);
+    const long long T = idx / (64 * nc);
+    const int r = lane & 31, h = lane >> 5;
+    const long long row = T * SK_TILE + r;
+    bf16x8 p0, p1, p2;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const int k = 16 * cc + 8 * h + e;
+        const float v = (row < n && k < d) ? src[row * ld + k] : 0.0f;
+        const __bf16 a0 = (__bf16)v;
+        const float r1 = v - (float)a0;          // exact: v and a0 share the leading bits
+        const __bf16 a1 = (__bf16)r1;
+        const __bf16 a2 = (__bf16)(r1 - (float)a1);
+        p0[e] = a0;
+        p1[e] = a1;
+        p2[e] = a2;
+    }
+    bf16x8* o = dst + (T * nc + cc) * (kPieces * 64) + lane;
+    o[0] = p0;
+    o[64] = p1;
+    o[128] = p2;
 }
 
 __global__ void fill_mask_kernel(float* __restrict__ mask, int m, int mpad) {
@@ -306,25 +312,24 @@ int env_int(const char* name, int dflt) {
 }
 
 struct Plan {
-    int kq, rb;
+    int nc;
     int nrb, nt, ngroups;
     Split s;
     int slots;       // partial slots per row
 };
 
+constexpr int kRowsPerGroup = SK_TILE * kRowBlocks * kWaves;
+
 Plan make_plan(int rows_pad, int m_pad, int kp) {
     Plan pl;
-    pl.kq = kp / 8;
+    pl.nc = kp / 16;
     pl.nrb = rows_pad / SK_TILE;
     pl.nt = m_pad / SK_TILE;
-    int rb = env_int("TRNOPT_HIP_RB", 0);
-    if (rb != 1 && rb != 2) rb = 1;
-    pl.rb = rb;
-    pl.ngroups = (pl.nrb + kWaves * rb - 1) / (kWaves * rb);
+    pl.ngroups = (rows_pad + kRowsPerGroup - 1) / kRowsPerGroup;
     pl.s.nt = pl.nt;
     pl.s.work = (long long)pl.ngroups * pl.nt;
-    int per_cu = env_int("TRNOPT_HIP_WG_PER_CU", 2);
-    if (per_cu < 1 || per_cu > 8) per_cu = 2;
+    int per_cu = env_int("TRNOPT_HIP_WG_PER_CU", 1);
+    if (per_cu < 1 || per_cu > 4) per_cu = 1;
     long long P = (long long)cu_count() * per_cu;
     if (P > pl.s.work) P = pl.s.work;
     if (P < 1) P = 1;
@@ -343,9 +348,9 @@ int meas_count(int rows_pad) { return (rows_pad + kFinalBlock - 1) / kFinalBlock
 
 // One LSE pass (partial + finalisation) over packed rows and columns.
 struct Pass {
-    const float* xr;
+    const bf16x8* xr;
     int rows_pad;
-    const float* yc;
+    const bf16x8* yc;
     int m_pad;
     int kp;
     const float* u;
@@ -353,6 +358,7 @@ struct Pass {
     const float* sc;
     const int* skip;
     int mode;
+    int rows_role;
     const float* xsq;
     const float* off;
     float* out;
@@ -375,13 +381,14 @@ hipError_t run_pass(const Pass& ps, const Plan& pl, hipStream_t st) {
     a.nrb = pl.nrb;
     a.rows_pad = ps.rows_pad;
     a.mode = ps.mode;
+    a.rows_role = ps.rows_role;
     a.s = pl.s;
-    hipError_t e = launch_partial(a, pl.kq, pl.rb, st);
+    hipError_t e = launch_partial(a, pl.nc, st);
     if (e != hipSuccess) return e;
     FinalArgs f;
     f.part = ps.part;
     f.rows_pad = ps.rows_pad;
-    f.rows_per_group = SK_TILE * pl.rb * kWaves;
+    f.rows_per_group = kRowsPerGroup;
     f.s = pl.s;
     f.sc = ps.sc;
     f.skip = ps.skip;
@@ -441,7 +448,7 @@ int check_cloud(const sk_cloud_f32& c, const char* name) {
 
 extern "C" {
 
-int sk_version(void) { return 100; }
+int sk_version(void) { return 200; }
 
 const char* sk_last_error(void) { return g_err; }
 
@@ -449,16 +456,22 @@ int sk_pad_points(int n) { return n <= 0 ? 0 : (n + SK_TILE - 1) / SK_TILE * SK_
 
 int sk_pad_dim(int d) { return d <= 0 ? 0 : (d + SK_KP_ALIGN - 1) / SK_KP_ALIGN * SK_KP_ALIGN; }
 
-int sk_pack_cloud_f32(const float* pts, int n, int d, int ld, float* out, void* stream) {
+size_t sk_packed_bytes(int n, int d) {
+    if (n < 1 || d < 1 || sk_pad_dim(d) > SK_KP_MAX) return 0;
+    return (size_t)sk_pad_points(n) * sk_pad_dim(d) * SK_PACKED_BYTES_PER_COORD;
+}
+
+int sk_pack_cloud_f32(const float* pts, int n, int d, int ld, void* out, void* stream) {
     if (pts == nullptr || out == nullptr) return fail(SK_E_ARG, "sk_pack_cloud_f32: null pointer");
     if (n < 1 || ld < d) return fail(SK_E_SHAPE, "sk_pack_cloud_f32: n %d, d %d, ld %d", n, d, ld);
     if (int r = check_kp(d)) return r;
-    const int npad = sk_pad_points(n), kp = sk_pad_dim(d);
-    const long long total = (long long)npad * kp;
+    if (!aligned16(out)) return fail(SK_E_ARG, "sk_pack_cloud_f32: out must be 16-byte aligned");
+    const int npad = sk_pad_points(n), nc = sk_pad_dim(d) / 16;
+    const long long total = (long long)(npad / SK_TILE) * nc * 64;
     const int threads = 256;
     const long long blocks = (total + threads - 1) / threads;
     hipLaunchKernelGGL(pack_cloud_kernel, dim3((unsigned)blocks), dim3(threads), 0, (hipStream_t)stream, pts, n, d,
-                       ld, out, npad, kp);
+                       ld, (bf16x8*)out, npad, nc);
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? SK_OK : hip_fail(e, "sk_pack_cloud_f32");
 }
@@ -467,7 +480,7 @@ size_t sk_row_lse_workspace_bytes(int rows, int m, int K) {
     if (rows < 1 || m < 1 || K < 1 || sk_pad_dim(K) > SK_KP_MAX) return 0;
     const int rp = sk_pad_points(rows), mp = sk_pad_points(m), kp = sk_pad_dim(K);
     const Plan pl = make_plan(rp, mp, kp);
-    return align_up((size_t)rp * kp * 4) + align_up((size_t)mp * kp * 4) + align_up((size_t)mp * 4) +
+    return align_up(sk_packed_bytes(rows, K)) + align_up(sk_packed_bytes(m, K)) + align_up((size_t)mp * 4) +
            partial_bytes(pl, rp);
 }
 
@@ -483,10 +496,10 @@ int sk_row_lse_f32(const float* xa, const float* ya, float* lse, int rows, int m
     const int rp = sk_pad_points(rows), mp = sk_pad_points(m), kp = sk_pad_dim(K);
     const Plan pl = make_plan(rp, mp, kp);
     char* p = (char*)ws;
-    float* xpk = (float*)p;
-    p += align_up((size_t)rp * kp * 4);
-    float* ypk = (float*)p;
-    p += align_up((size_t)mp * kp * 4);
+    bf16x8* xpk = (bf16x8*)p;
+    p += align_up(sk_packed_bytes(rows, K));
+    bf16x8* ypk = (bf16x8*)p;
+    p += align_up(sk_packed_bytes(m, K));
     float* mask = (float*)p;
     p += align_up((size_t)mp * 4);
     float2* part = (float2*)p;
@@ -504,6 +517,7 @@ int sk_row_lse_f32(const float* xa, const float* ya, float* lse, int rows, int m
     ps.v = mask;
     ps.sc = mask;       // not read in this mode; a valid address all the same
     ps.mode = kPlainLse;
+    ps.rows_role = 0;
     ps.out = lse;
     ps.n_store = rows;
     ps.part = part;
@@ -519,9 +533,10 @@ size_t sk_half_step_workspace_bytes(int rows_pad, int m_pad, int d) {
 
 int sk_half_step_meas_count(int rows_pad) { return rows_pad < 1 ? 0 : meas_count(rows_pad); }
 
-int sk_half_step_f32(const float* x_pk, const float* xsq, const float* off, int rows_pad, const float* y_pk,
-                     const float* gh, const float* log_b, int m_pad, int d, const float* sc, const int* skip,
-                     float* fh, float* meas, const float* w, int n_real, void* ws, size_t ws_bytes, void* stream) {
+int sk_half_step_f32(const void* x_pk, const float* xsq, const float* off, int rows_pad, const void* y_pk,
+                     const float* gh, const float* log_b, int m_pad, int d, int rows_role, const float* sc,
+                     const int* skip, float* fh, float* meas, const float* w, int n_real, void* ws, size_t ws_bytes,
+                     void* stream) {
     if (x_pk == nullptr || xsq == nullptr || y_pk == nullptr || gh == nullptr || log_b == nullptr || sc == nullptr ||
         fh == nullptr || ws == nullptr)
         return fail(SK_E_ARG, "sk_half_step_f32: null pointer");
@@ -531,15 +546,16 @@ int sk_half_step_f32(const float* x_pk, const float* xsq, const float* off, int 
         return fail(SK_E_SHAPE, "sk_half_step_f32: rows_pad %d and m_pad %d must be positive multiples of %d",
                     rows_pad, m_pad, SK_TILE);
     if (int r = check_kp(d)) return r;
+    if (rows_role != 0 && rows_role != 1) return fail(SK_E_ARG, "sk_half_step_f32: rows_role %d not 0 or 1", rows_role);
     if (!aligned16(x_pk) || !aligned16(y_pk) || !aligned16(gh) || !aligned16(log_b))
         return fail(SK_E_ARG, "sk_half_step_f32: packed clouds, gh and log_b must be 16-byte aligned");
     const size_t need = sk_half_step_workspace_bytes(rows_pad, m_pad, d);
     if (ws_bytes < need) return fail(SK_E_WORKSPACE, "sk_half_step_f32: workspace %zu < %zu bytes", ws_bytes, need);
     const Plan pl = make_plan(rows_pad, m_pad, sk_pad_dim(d));
     Pass ps = {};
-    ps.xr = x_pk;
+    ps.xr = (const bf16x8*)x_pk;
     ps.rows_pad = rows_pad;
-    ps.yc = y_pk;
+    ps.yc = (const bf16x8*)y_pk;
     ps.m_pad = m_pad;
     ps.kp = sk_pad_dim(d);
     ps.u = gh;
@@ -547,6 +563,7 @@ int sk_half_step_f32(const float* x_pk, const float* xsq, const float* off, int 
     ps.sc = sc;
     ps.skip = skip;
     ps.mode = kHalfStep;
+    ps.rows_role = rows_role;
     ps.xsq = xsq;
     ps.off = off;
     ps.out = fh;
@@ -600,9 +617,9 @@ int sk_loop_run_f32(const sk_loop_f32* L, int iters, void* stream) {
     hipStream_t hs = (hipStream_t)stream;
 
     Pass f = {};
-    f.xr = L->x.pk;
+    f.xr = (const bf16x8*)L->x.pk;
     f.rows_pad = L->x.npad;
-    f.yc = L->y.pk;
+    f.yc = (const bf16x8*)L->y.pk;
     f.m_pad = L->y.npad;
     f.kp = kp;
     f.u = L->gh;
@@ -610,6 +627,7 @@ int sk_loop_run_f32(const sk_loop_f32* L, int iters, void* stream) {
     f.sc = st->sc_x;
     f.skip = skip;
     f.mode = kHalfStep;
+    f.rows_role = 0;
     f.xsq = L->x.sq;
     f.off = L->x.off;
     f.out = L->fh;
@@ -617,9 +635,9 @@ int sk_loop_run_f32(const sk_loop_f32* L, int iters, void* stream) {
     f.part = part;
 
     Pass g = {};
-    g.xr = L->y.pk;
+    g.xr = (const bf16x8*)L->y.pk;
     g.rows_pad = L->y.npad;
-    g.yc = L->x.pk;
+    g.yc = (const bf16x8*)L->x.pk;
     g.m_pad = L->x.npad;
     g.kp = kp;
     g.u = L->fh;
@@ -627,6 +645,7 @@ int sk_loop_run_f32(const sk_loop_f32* L, int iters, void* stream) {
     g.sc = st->sc_y;
     g.skip = skip;
     g.mode = kHalfStep;
+    g.rows_role = 1;
     g.xsq = L->y.sq;
     g.off = L->y.off;
     g.out = L->gh;

@@ -4,22 +4,34 @@
 // IEEE mode would first be canonicalised one by one. No value here is NaN or infinite: padding and empty
 // rows use large finite sentinels.
 //
-// Per row i and column j the kernel forms the dot product D_ij = x_i . y_j with v_mfma_f32_32x32x2_f32
-// chains that start from zero (A = 32 columns of the packed y tile, B = 32 rows of packed x held in
-// registers), then a_ij = D_ij + alpha u_j + beta v_j on the VALU, and keeps per lane a running (M, S) with
-// S = sum_j exp2(c (a_ij - M)).
+// Contraction. Every fp32 coordinate v is stored as three bf16 pieces v = v0 + v1 + v2 (exact: 8 + 8 + 8
+// significand bits; sk_kernels.hip packs them). The dot product x.y is accumulated in fp32 by
+// v_mfma_f32_32x32x16_bf16 from the six leading cross products
 //
-// Why the contraction starts from zero on unscaled coordinates: a v_mfma_f32_32x32x2_f32 chain rounds like
-// chained round-to-nearest FMAs, in the same coordinate order whichever cloud is A and which is B, so the
-// f update (rows x, columns y) and the g update (rows y, columns x) get bit-identical x_i . y_j. In the cold
-// regime (eps much smaller than the cost spread) a row's log-sum-exp is a single dominant score, and any
-// rounding that differs between the two directions pushes f_i + g_j of that pair by the difference in every
-// iteration: the potentials would drift linearly along the pair's neutral mode. (The reference's PyTorch
-// path has the same property: x @ y^T and y @ x^T round alike.) For the same reason the max is subtracted
-// before scaling, exp2(c (a - M)): the dominant term is exactly 1.
+//     x0 y0, x0 y1, x1 y0, x0 y2, x1 y1, x2 y0        (each bf16 x bf16 product is exact in fp32),
 //
-// The tile loop is a two-stage software pipeline: while the MFMAs of tile t run, the loads of tile t + 1
-// are in flight and the column term, max, exp and sum of tile t - 1 are issued between the MFMAs.
+// whose dropped terms are below 2^-24 of |x||y|: the result is as accurate as an fp32 dot product. On gfx950
+// the bf16 matrix pipe runs at ~15x the fp32 MFMA rate and, unlike the fp32 MFMA, issues alongside VALU work
+// of the same SIMD, so the exp / max / sum epilogue of one tile hides under the MFMAs of the next.
+//
+// Symmetry. The f update (rows x, columns y) and the g update (rows y, columns x) must form bit-identical
+// x_i . y_j: in the cold regime a row's log-sum-exp is one dominant score, and any rounding difference
+// between the directions would push f_i + g_j of that pair by the same amount every iteration (a linear
+// drift along the pair's neutral mode). The products are exact and the MFMA adds them in k order, so the two
+// directions agree when they issue the same (x piece, y piece) pairs in the same order: `rows_role` says
+// whether the rows are the first or the second cloud, and the pair list is transposed accordingly. The
+// contraction starts from zero and the column term is added afterwards on the VALU; the max is subtracted
+// before scaling, exp2(c (a - M)), so the dominant term is exactly 1.
+//
+// Layout of one workgroup (4 waves, one per SIMD of a CU): wave w owns kRowBlocks blocks of 32 rows of a
+// row group (its bf16 pieces stay in registers for the whole work segment), and all four waves walk the same
+// column tiles, which are staged once per workgroup in LDS (double buffered, with the tile's 32 column
+// terms). MFMA orientation: A = 32 columns, B = 32 rows, so lane l's 16 accumulators all belong to row
+// l % 32 (columns 8 (r / 4) + 4 (l / 32) + r % 4); row reductions stay inside a lane and lanes l, l + 32 are
+// merged once per segment.
+
+#include <type_traits>
+#include <utility>
 
 #include "sk_common.h"
 
@@ -29,182 +41,220 @@ namespace {
 __device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Hardware hands consecutive workgroup ids to the 8 XCDs in turn; renumber so that the workgroups of one
-// XCD own one contiguous range of the work (their column tiles then share that XCD's L2).
+// XCD own one contiguous range of the work.
 __device__ __forceinline__ int xcd_contiguous(int b, int P) {
     const int q = P / kXcds, r = P % kXcds;
     const int xcd = b % kXcds, idx = b / kXcds;
     return xcd * q + (xcd < r ? xcd : r) + idx;
 }
 
-// Online log-sum-exp update of one lane's row with 16 new scores a = D + colterm (accumulator units).
-__device__ __forceinline__ void lse_update(const f32x16& acc, const f32x16& col, float& M, float& S, float c) {
-    f32x16 a;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) a[r] = acc[r] + col[r];
-    const float m0 = fmaxf(fmaxf(a[0], a[1]), fmaxf(a[2], a[3]));
-    const float m1 = fmaxf(fmaxf(a[4], a[5]), fmaxf(a[6], a[7]));
-    const float m2 = fmaxf(fmaxf(a[8], a[9]), fmaxf(a[10], a[11]));
-    const float m3 = fmaxf(fmaxf(a[12], a[13]), fmaxf(a[14], a[15]));
-    const float Mn = fmaxf(M, fmaxf(fmaxf(m0, m1), fmaxf(m2, m3)));
-    float e[16];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) e[r] = ex2(c * (a[r] - Mn));
-    const float s0 = (e[0] + e[1]) + (e[2] + e[3]);
-    const float s1 = (e[4] + e[5]) + (e[6] + e[7]);
-    const float s2 = (e[8] + e[9]) + (e[10] + e[11]);
-    const float s3 = (e[12] + e[13]) + (e[14] + e[15]);
-    S = fmaf(S, ex2(c * (M - Mn)), (s0 + s1) + (s2 + s3));
-    M = Mn;
+// Compile-time loop: f(integral_constant<int, i>) for i in [B, E).
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(f);
+    }
 }
 
-template <int KQ>
-struct Tile {
-    const f32x4* y;   // packed columns + lane
-    const f32x4* u;   // u + 4 h
-    const f32x4* v;   // v + 4 h
-
-    __device__ __forceinline__ void load_y(int t, f32x4 (&out)[KQ]) const {
-#pragma unroll
-        for (int q = 0; q < KQ; ++q) out[q] = y[(size_t)t * (64 * KQ) + q * 64];
+// The online log-sum-exp update of one row block and one tile, as kOps elementary steps:
+//   j in [0, 16):  a_r = acc_r + col_r
+//   j in [16, 24): running max over a pair of scores
+//   j in [24, 40): s += exp2(c (a_r - m))
+//   j == 40:       S = S exp2(c (M - m)) + s, M = m
+// Steps are spread over the MFMA slots of the next tile in proportion to their cost (an exp step ~7 VALU).
+constexpr int kOps = 41;
+constexpr int op_cost(int j) { return j < 24 ? 1 : 7; }
+constexpr int block_cost() {
+    int s = 0;
+    for (int j = 0; j < kOps; ++j) s += op_cost(j);
+    return s;
+}
+// First step of slot i of NS (steps of the row blocks interleaved: step k is step k / RB of block k % RB).
+template <int RB>
+constexpr int op_begin(int i, int NS) {
+    const int target = (int)((long long)i * RB * block_cost() / NS);
+    int cost = 0, k = 0;
+    while (k < RB * kOps && cost < target) {
+        cost += op_cost(k / RB);
+        ++k;
     }
-    // Column term inputs of the lane's 16 accumulator rows: columns t * 32 + 8 q + 4 h + (0..3).
-    __device__ __forceinline__ void load_uv(int t, f32x4 (&uu)[4], f32x4 (&vv)[4]) const {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            uu[q] = u[t * 8 + q * 2];
-            vv[q] = v[t * 8 + q * 2];
+    return k;
+}
+
+template <int RB>
+struct Online {
+    float m[RB], s[RB];
+    template <int k>
+    __device__ __forceinline__ void step(f32x16 (&acc)[RB], const f32x16& col, float (&M)[RB], float (&S)[RB],
+                                         float c) {
+        constexpr int j = k / RB, b = k % RB;
+        if constexpr (j < 16) {
+            acc[b][j] = acc[b][j] + col[j];
+            if constexpr (j == 0) {
+                m[b] = M[b];
+                s[b] = 0.0f;
+            }
+        } else if constexpr (j < 24) {
+            constexpr int p = j - 16;
+            m[b] = fmaxf(m[b], fmaxf(acc[b][2 * p], acc[b][2 * p + 1]));
+        } else if constexpr (j < 40) {
+            constexpr int r = j - 24;
+            s[b] += ex2(c * (acc[b][r] - m[b]));
+        } else {
+            S[b] = fmaf(S[b], ex2(c * (M[b] - m[b])), s[b]);
+            M[b] = m[b];
         }
     }
 };
 
-// Column term of the lane's 16 accumulator rows (columns t * 32 + 8 q + 4 h + e, register 4 q + e).
-__device__ __forceinline__ void col_term(f32x16& col, const f32x4 (&uu)[4], const f32x4 (&vv)[4], float alpha,
-                                         float beta) {
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) col[4 * q + e] = fmaf(beta, vv[q][e], alpha * uu[q][e]);
-    }
-}
+// The six products as (first-cloud piece, second-cloud piece).
+constexpr int kFirstPiece[6] = {0, 0, 1, 0, 1, 2};
+constexpr int kSecondPiece[6] = {0, 1, 0, 2, 1, 0};
 
-// D = x . y for RB row blocks against one column tile, from zero.
-template <int KQ, int RB>
-__device__ __forceinline__ void tile_mfma(f32x16 (&acc)[RB], const f32x4 (&yv)[KQ], const f32x4 (&xv)[RB][KQ]) {
+template <int NC, int ROLE>
+struct Segment {
+    static constexpr int RB = kRowBlocks;
+    static constexpr int TILE16 = NC * kPieces * 64;   // 16-byte units per packed 32-point tile
+    static constexpr int PER_THREAD = (TILE16 + kBlock - 1) / kBlock;
+    static constexpr int NS = 6 * NC * RB;             // MFMA slots per tile
+
+    // Rows rb0 .. rb0 + RB - 1 against column tiles [tb, te); writes one (M, S) per row into `slot`.
+    __device__ __forceinline__ static void run(const PartialArgs& a, int rb0, int tb, int te, int slot, float alpha,
+                                               float beta, float c, bf16x8* lds_y, float* lds_col) {
+        const int tid = threadIdx.x;
+        const int lane = tid & 63;
+        const int h = lane >> 5;
+
+        bf16x8 xv[RB][NC][kPieces];
 #pragma unroll
-    for (int b = 0; b < RB; ++b) acc[b] = f32x16{};
+        for (int b = 0; b < RB; ++b) {
+            const int blk = rb0 + b < a.nrb ? rb0 + b : a.nrb - 1;   // a missing block recomputes the last one
 #pragma unroll
-    for (int q = 0; q < KQ; ++q) {
+            for (int cc = 0; cc < NC; ++cc)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
+                for (int p = 0; p < kPieces; ++p)
+                    xv[b][cc][p] = a.xr[(size_t)blk * TILE16 + (cc * kPieces + p) * 64 + lane];
+        }
+        float M[RB], S[RB];
 #pragma unroll
-            for (int b = 0; b < RB; ++b)
-                acc[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(yv[q][e], xv[b][q][e], acc[b], 0, 0, 0);
+        for (int b = 0; b < RB; ++b) {
+            M[b] = kEmpty;
+            S[b] = 0.0f;
+        }
+
+        // Staging of one column tile: every thread loads PER_THREAD 16-byte units and thread j % 32 the column
+        // term of column j. Branch-free (clamped indices; threads mapped to the same element write the same
+        // value), so that a whole tile is one basic block and the epilogue stays between the MFMAs.
+        const int cj = tid & 31;
+        bf16x8 pf[PER_THREAD];
+        float pc = 0.0f;
+        auto prefetch = [&](int t) {
+#pragma unroll
+            for (int k = 0; k < PER_THREAD; ++k) {
+                const int idx = tid + k * kBlock < TILE16 ? tid + k * kBlock : TILE16 - 1;
+                pf[k] = a.yc[(size_t)t * TILE16 + idx];
+            }
+            pc = fmaf(beta, a.v[t * 32 + cj], alpha * a.u[t * 32 + cj]);
+        };
+        auto stage = [&](int buf) {
+#pragma unroll
+            for (int k = 0; k < PER_THREAD; ++k) {
+                const int idx = tid + k * kBlock < TILE16 ? tid + k * kBlock : TILE16 - 1;
+                lds_y[buf * TILE16 + idx] = pf[k];
+            }
+            lds_col[buf * 32 + cj] = pc;
+        };
+        bf16x8 yv[NC][kPieces];
+        auto read_tile = [&](int buf, f32x16& col) {
+#pragma unroll
+            for (int cc = 0; cc < NC; ++cc)
+#pragma unroll
+                for (int p = 0; p < kPieces; ++p) yv[cc][p] = lds_y[buf * TILE16 + (cc * kPieces + p) * 64 + lane];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const f32x4 cv = *reinterpret_cast<const f32x4*>(&lds_col[buf * 32 + 8 * q + 4 * h]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) col[4 * q + e] = cv[e];
+            }
+        };
+
+        f32x16 accA[RB], accB[RB], colA, colB;
+        Online<RB> on;
+        // One tile: MFMAs into accN from zero; with `epi`, the update of the previous tile (accP, colP) is
+        // spread between them, one slot per MFMA, fenced so the compiler keeps the interleave.
+        auto tile = [&](f32x16 (&accN)[RB], f32x16 (&accP)[RB], const f32x16& colP, bool epi) {
+#pragma unroll
+            for (int b = 0; b < RB; ++b) accN[b] = f32x16{};
+            static_for<0, NS>([&](auto I) {
+                constexpr int i = decltype(I)::value;
+                constexpr int cc = i / (6 * RB), p = (i / RB) % 6, b = i % RB;
+                constexpr int rp = ROLE == 0 ? kFirstPiece[p] : kSecondPiece[p];
+                constexpr int cp = ROLE == 0 ? kSecondPiece[p] : kFirstPiece[p];
+                accN[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(yv[cc][cp], xv[b][cc][rp], accN[b], 0, 0, 0);
+                if (epi) {
+                    constexpr int k0 = op_begin<RB>(i, NS), k1 = op_begin<RB>(i + 1, NS);
+                    static_for<k0, k1>([&](auto K) { on.template step<decltype(K)::value>(accP, colP, M, S, c); });
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            });
+        };
+        auto update = [&](f32x16 (&accP)[RB], const f32x16& colP) {
+            static_for<0, RB * kOps>([&](auto K) { on.template step<decltype(K)::value>(accP, colP, M, S, c); });
+        };
+
+        // Tiles in pairs so the accumulator roles alternate without copies. Buffer (t - tb) & 1 holds tile t;
+        // every prefetch / stage is unconditional (after the last tile the last one is staged again).
+        const int last = te - 1;
+        prefetch(tb);
+        stage(0);
+        __syncthreads();
+        int t = tb;
+        read_tile(0, colA);
+        prefetch(t + 1 < te ? t + 1 : last);
+        tile(accA, accB, colB, false);
+        stage(1);
+        __syncthreads();
+        ++t;
+        while (t < te) {
+            read_tile((t - tb) & 1, colB);
+            prefetch(t + 1 < te ? t + 1 : last);
+            tile(accB, accA, colA, true);
+            stage((t + 1 - tb) & 1);
+            __syncthreads();
+            ++t;
+            if (t >= te) {
+                update(accB, colB);
+                goto done;
+            }
+            read_tile((t - tb) & 1, colA);
+            prefetch(t + 1 < te ? t + 1 : last);
+            tile(accA, accB, colB, true);
+            stage((t + 1 - tb) & 1);
+            __syncthreads();
+            ++t;
+        }
+        update(accA, colA);
+    done:
+        // Lanes l and l + 32 hold the same row over different columns: merge them, then store.
+#pragma unroll
+        for (int b = 0; b < RB; ++b) {
+            const float Mo = __shfl_xor(M[b], 32);
+            const float So = __shfl_xor(S[b], 32);
+            const float Mn = fmaxf(M[b], Mo);
+            const float Sn = S[b] * ex2(c * (M[b] - Mn)) + So * ex2(c * (Mo - Mn));
+            if (h == 0 && rb0 + b < a.nrb)
+                a.part[(size_t)slot * a.rows_pad + (size_t)(rb0 + b) * 32 + lane] = make_float2(Mn, Sn);
         }
     }
-}
+};
 
-template <int RB>
-__device__ __forceinline__ void update_all(const f32x16 (&acc)[RB], const f32x16& col, float (&M)[RB], float (&S)[RB],
-                                           float c) {
-#pragma unroll
-    for (int b = 0; b < RB; ++b) lse_update(acc[b], col, M[b], S[b], c);
-}
-
-template <int KQ, int RB>
-__device__ __forceinline__ void run_segment(const PartialArgs& a, int rb0, int tb, int te, int slot, float alpha,
-                                            float beta, float c) {
-    constexpr int KP = 8 * KQ;
-    const int lane = threadIdx.x & 63;
-    const int h = lane >> 5;
-
-    f32x4 xv[RB][KQ];
-#pragma unroll
-    for (int b = 0; b < RB; ++b) {
-        const bool ok = rb0 + b < a.nrb;
-        const f32x4* src = reinterpret_cast<const f32x4*>(a.xr + (size_t)(ok ? rb0 + b : rb0) * (32 * KP)) + lane;
-#pragma unroll
-        for (int q = 0; q < KQ; ++q) xv[b][q] = src[q * 64];
-    }
-
-    float M[RB], S[RB];
-#pragma unroll
-    for (int b = 0; b < RB; ++b) {
-        M[b] = kEmpty;
-        S[b] = 0.0f;
-    }
-
-    Tile<KQ> tl;
-    tl.y = reinterpret_cast<const f32x4*>(a.yc) + lane;
-    tl.u = reinterpret_cast<const f32x4*>(a.u + 4 * h);
-    tl.v = reinterpret_cast<const f32x4*>(a.v + 4 * h);
-
-    f32x4 ya[KQ], yb[KQ], uu[4], vv[4];
-    f32x16 accA[RB], accB[RB], colA, colB;
-    const int last = te - 1;
-
-    // Phase for tile t: (1) the column term of tile t from loads issued one phase earlier, (2) the loads of
-    // tile t + 1, then (3) the MFMAs of tile t interleaved with the update of tile t - 1. The scheduling
-    // fences keep the loads a whole MFMA chain ahead of their first use.
-    tl.load_y(tb, ya);
-    tl.load_uv(tb, uu, vv);
-    col_term(colA, uu, vv, alpha, beta);
-    {
-        const int tn = tb + 1 < te ? tb + 1 : last;
-        tl.load_y(tn, yb);
-        tl.load_uv(tn, uu, vv);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    tile_mfma<KQ, RB>(accA, ya, xv);
-    __builtin_amdgcn_sched_barrier(0);
-    int t = tb + 1;
-    while (t + 1 < te) {
-        // yb / uu / vv hold tile t; accA / colA hold tile t - 1.
-        col_term(colB, uu, vv, alpha, beta);
-        tl.load_y(t + 1, ya);
-        tl.load_uv(t + 1, uu, vv);
-        __builtin_amdgcn_sched_barrier(0);
-        tile_mfma<KQ, RB>(accB, yb, xv);
-        update_all<RB>(accA, colA, M, S, c);
-        __builtin_amdgcn_sched_barrier(0);
-        // ya / uu / vv hold tile t + 1; accB / colB hold tile t.
-        col_term(colA, uu, vv, alpha, beta);
-        {
-            const int tn = t + 2 < te ? t + 2 : last;
-            tl.load_y(tn, yb);
-            tl.load_uv(tn, uu, vv);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        tile_mfma<KQ, RB>(accA, ya, xv);
-        update_all<RB>(accB, colB, M, S, c);
-        __builtin_amdgcn_sched_barrier(0);
-        t += 2;
-    }
-    if (t < te) {
-        // yb / uu / vv hold tile t (the last); accA / colA hold tile t - 1.
-        col_term(colB, uu, vv, alpha, beta);
-        tile_mfma<KQ, RB>(accB, yb, xv);
-        update_all<RB>(accA, colA, M, S, c);
-        update_all<RB>(accB, colB, M, S, c);
-    } else {
-        update_all<RB>(accA, colA, M, S, c);
-    }
-
-    // Lanes l and l + 32 hold the same row over different columns: merge them, then store.
-#pragma unroll
-    for (int b = 0; b < RB; ++b) {
-        const float Mo = __shfl_xor(M[b], 32);
-        const float So = __shfl_xor(S[b], 32);
-        const float Mn = fmaxf(M[b], Mo);
-        const float Sn = S[b] * ex2(c * (M[b] - Mn)) + So * ex2(c * (Mo - Mn));
-        if (h == 0 && rb0 + b < a.nrb)
-            a.part[(size_t)slot * a.rows_pad + (size_t)(rb0 + b) * 32 + lane] = make_float2(Mn, Sn);
-    }
-}
-
-template <int KQ, int RB>
-__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2)))
+template <int NC, int ROLE>
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void lse_partial_kernel(PartialArgs a) {
     if (a.skip != nullptr && *a.skip != 0) return;
+    __shared__ bf16x8 lds_y[2 * NC * kPieces * 64];
+    __shared__ __attribute__((aligned(16))) float lds_col[64];
     const int wv = threadIdx.x >> 6;
     const int P = a.s.P;
     const int p = xcd_contiguous(blockIdx.x, P);
@@ -230,41 +280,35 @@ void lse_partial_kernel(PartialArgs a) {
         const long long left = u1 - u;
         const int te = left < (long long)(a.s.nt - tb) ? tb + (int)left : a.s.nt;
         const int slot = p - first_wg(g, a.s);
-        const int rb0 = (g * kWaves + wv) * RB;
-        if (rb0 < a.nrb) run_segment<KQ, RB>(a, rb0, tb, te, slot, alpha, beta, c);
+        // Waves past the last row block recompute it (their rows are not stored) so that every wave takes part
+        // in the workgroup's barriers.
+        const int rb0 = (g * kWaves + wv) * kRowBlocks;
+        Segment<NC, ROLE>::run(a, rb0, tb, te, slot, alpha, beta, c, lds_y, lds_col);
         u += te - tb;
     }
 }
 
-template <int KQ>
-hipError_t launch_kq(const PartialArgs& a, int rb, hipStream_t st) {
-    if (rb == 2)
-        hipLaunchKernelGGL((lse_partial_kernel<KQ, 2>), dim3(a.s.P), dim3(kBlock), 0, st, a);
+template <int NC>
+hipError_t launch_nc(const PartialArgs& a, hipStream_t st) {
+    if (a.rows_role == 0)
+        hipLaunchKernelGGL((lse_partial_kernel<NC, 0>), dim3(a.s.P), dim3(kBlock), 0, st, a);
     else
-        hipLaunchKernelGGL((lse_partial_kernel<KQ, 1>), dim3(a.s.P), dim3(kBlock), 0, st, a);
+        hipLaunchKernelGGL((lse_partial_kernel<NC, 1>), dim3(a.s.P), dim3(kBlock), 0, st, a);
     return hipGetLastError();
 }
 
 }  // namespace
 
-hipError_t launch_partial(const PartialArgs& a, int kq, int rb, hipStream_t st) {
-    switch (kq) {
-        case 1: return launch_kq<1>(a, rb, st);
-        case 2: return launch_kq<2>(a, rb, st);
-        case 3: return launch_kq<3>(a, rb, st);
-        case 4: return launch_kq<4>(a, rb, st);
-        case 5: return launch_kq<5>(a, rb, st);
-        case 6: return launch_kq<6>(a, rb, st);
-        case 7: return launch_kq<7>(a, rb, st);
-        case 8: return launch_kq<8>(a, rb, st);
-        case 9: return launch_kq<9>(a, rb, st);
-        case 10: return launch_kq<10>(a, rb, st);
-        case 11: return launch_kq<11>(a, rb, st);
-        case 12: return launch_kq<12>(a, rb, st);
-        case 13: return launch_kq<13>(a, rb, st);
-        case 14: return launch_kq<14>(a, rb, st);
-        case 15: return launch_kq<15>(a, rb, st);
-        case 16: return launch_kq<16>(a, rb, st);
+hipError_t launch_partial(const PartialArgs& a, int nc, hipStream_t st) {
+    switch (nc) {
+        case 1: return launch_nc<1>(a, st);
+        case 2: return launch_nc<2>(a, st);
+        case 3: return launch_nc<3>(a, st);
+        case 4: return launch_nc<4>(a, st);
+        case 5: return launch_nc<5>(a, st);
+        case 6: return launch_nc<6>(a, st);
+        case 7: return launch_nc<7>(a, st);
+        case 8: return launch_nc<8>(a, st);
         default: return hipErrorInvalidValue;
     }
 }

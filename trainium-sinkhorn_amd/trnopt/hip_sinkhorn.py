@@ -30,8 +30,9 @@ import torch
 
 PAD_LOG_WEIGHT = -1e9                    # src/trnopt/sinkhorn.py:59
 TILE = 32                                 # SK_TILE
-KP_ALIGN = 8                              # SK_KP_ALIGN
+KP_ALIGN = 16                             # SK_KP_ALIGN
 KP_MAX = 128                              # SK_KP_MAX
+PACKED_BYTES_PER_COORD = 6                # SK_PACKED_BYTES_PER_COORD: three bf16 pieces
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libtrnopt_hip.so"
 
 _c_float_p = ctypes.c_void_p             # device pointers travel as integers
@@ -67,17 +68,18 @@ _SIGS = {
     "sk_last_error": (ctypes.c_char_p, []),
     "sk_pad_points": (ctypes.c_int, [ctypes.c_int]),
     "sk_pad_dim": (ctypes.c_int, [ctypes.c_int]),
-    "sk_pack_cloud_f32": (ctypes.c_int, [_c_float_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, _c_float_p,
+    "sk_packed_bytes": (ctypes.c_size_t, [ctypes.c_int, ctypes.c_int]),
+    "sk_pack_cloud_f32": (ctypes.c_int, [_c_float_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
                                          ctypes.c_void_p]),
     "sk_row_lse_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int, ctypes.c_int, ctypes.c_int]),
     "sk_row_lse_f32": (ctypes.c_int, [_c_float_p, _c_float_p, _c_float_p, ctypes.c_int, ctypes.c_int,
                                       ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
     "sk_half_step_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int, ctypes.c_int, ctypes.c_int]),
     "sk_half_step_meas_count": (ctypes.c_int, [ctypes.c_int]),
-    "sk_half_step_f32": (ctypes.c_int, [_c_float_p, _c_float_p, _c_float_p, ctypes.c_int, _c_float_p, _c_float_p,
-                                        _c_float_p, ctypes.c_int, ctypes.c_int, _c_float_p, ctypes.c_void_p,
-                                        _c_float_p, _c_float_p, _c_float_p, ctypes.c_int, ctypes.c_void_p,
-                                        ctypes.c_size_t, ctypes.c_void_p]),
+    "sk_half_step_f32": (ctypes.c_int, [ctypes.c_void_p, _c_float_p, _c_float_p, ctypes.c_int, ctypes.c_void_p,
+                                        _c_float_p, _c_float_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, _c_float_p,
+                                        ctypes.c_void_p, _c_float_p, _c_float_p, _c_float_p, ctypes.c_int,
+                                        ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
     "sk_loop_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int, ctypes.c_int, ctypes.c_int]),
     "sk_loop_init_f32": (ctypes.c_int, [ctypes.POINTER(SkLoop), ctypes.c_void_p]),
     "sk_loop_run_f32": (ctypes.c_int, [ctypes.POINTER(SkLoop), ctypes.c_int, ctypes.c_void_p]),
@@ -160,15 +162,20 @@ def _workspace(nbytes: int, device) -> torch.Tensor:
 # ---------------------------------------------------------------------------------------------------------
 # Kernel-level entry points (the NKI module's make_row_lse_kernel / make_half_step_kernel)
 
+def packed_bytes(n: int, d: int) -> int:
+    return pad_points(n) * pad_dim(d) * PACKED_BYTES_PER_COORD
+
+
 def pack_cloud(pts: torch.Tensor) -> torch.Tensor:
-    """(n, d) float32 device points -> the packed tile layout (pad_points(n) * pad_dim(d),)."""
+    """(n, d) float32 device points -> the packed tile layout: each coordinate as three bf16 pieces, as bytes
+    (packed_bytes(n, d),)."""
     _require_device_f32("pts", pts)
     if pts.dim() != 2:
         raise ValueError("pts must be (n, d)")
     n, d = pts.shape
     if pad_dim(d) > KP_MAX:
         raise ValueError(f"d = {d} is above the kernels' limit ({KP_MAX})")
-    out = torch.empty(pad_points(n) * pad_dim(d), dtype=torch.float32, device=pts.device)
+    out = torch.empty(packed_bytes(n, d), dtype=torch.uint8, device=pts.device)
     _check(lib().sk_pack_cloud_f32(pts.data_ptr(), n, d, pts.stride(0), out.data_ptr(), _stream()),
            "sk_pack_cloud_f32")
     return out
@@ -203,9 +210,11 @@ class HipCloud:
     """One point cloud on the GPU in the kernels' layout: the counterpart of _Cloud (src/trnopt/sinkhorn.py:131-167).
 
     Padded to a multiple of 32 points with log weight PAD_LOG_WEIGHT (weight exactly 0) and zero coordinates,
-    |p|^2 summed in float64 and cast, coordinates packed once (they never change during a solve)."""
+    |p|^2 summed in float64 and cast, coordinates packed once (they never change during a solve). `role` is 0
+    for the first cloud of a solve (x) and 1 for the second (y): a half-step with this cloud as rows passes it
+    to the kernel, so that the f and g updates form bit-identical x_i . y_j."""
 
-    def __init__(self, pts: np.ndarray, log_w: np.ndarray, device, off: np.ndarray | None = None):
+    def __init__(self, pts: np.ndarray, log_w: np.ndarray, device, off: np.ndarray | None = None, role: int = 0):
         n, d = pts.shape
         if pad_dim(d) > KP_MAX:
             raise ValueError(f"d = {d} is above the HIP kernels' limit (d <= {KP_MAX})")
@@ -215,7 +224,9 @@ class HipCloud:
         L = np.full(npad, PAD_LOG_WEIGHT)
         L[:n] = log_w
         f32 = dict(dtype=torch.float32, device=device)
-        self.n, self.npad, self.d, self.device = n, npad, d, device
+        if role not in (0, 1):
+            raise ValueError("role must be 0 (first cloud) or 1 (second cloud)")
+        self.n, self.npad, self.d, self.device, self.role = n, npad, d, device, role
         self.sq = torch.as_tensor((P * P).sum(axis=1), dtype=torch.float32).to(device)
         self.log_w = torch.as_tensor(L, dtype=torch.float32).to(device)
         self.w = torch.as_tensor(np.exp(L), dtype=torch.float32).to(device)
@@ -244,15 +255,17 @@ def half_step(side: HipCloud, other: HipCloud, other_h: torch.Tensor, sc: torch.
     _require_device_f32("sc", sc, 4)
     if side.d != other.d:
         raise ValueError("clouds of different dimension")
+    if side.role == other.role:
+        raise ValueError("a half-step pairs a first cloud (role 0) with a second (role 1)")
     lb = lib()
     ws = _workspace(lb.sk_half_step_workspace_bytes(side.npad, other.npad, side.d), side.device)
     if out is None:
         out = torch.empty(side.npad, dtype=torch.float32, device=side.device)
     off = side.off if use_off else None
     _check(lb.sk_half_step_f32(side.pk.data_ptr(), side.sq.data_ptr(), _ptr(off), side.npad, other.pk.data_ptr(),
-                               other_h.data_ptr(), other.log_w.data_ptr(), other.npad, side.d, sc.data_ptr(), None,
-                               out.data_ptr(), None, None, side.n, ws.data_ptr(), ws.numel(), _stream()),
-           "sk_half_step_f32")
+                               other_h.data_ptr(), other.log_w.data_ptr(), other.npad, side.d, side.role,
+                               sc.data_ptr(), None, out.data_ptr(), None, None, side.n, ws.data_ptr(), ws.numel(),
+                               _stream()), "sk_half_step_f32")
     return out
 
 

@@ -196,8 +196,8 @@ def _solve_hip(p, opts: SinkhornOptions):
     if dev.index is None:
         dev = torch.device("cuda", torch.cuda.current_device())
     with torch.cuda.device(dev):
-        X = hk.HipCloud(p.xs, p.log_a, dev, p.off_x)
-        Y = hk.HipCloud(p.ys, p.log_b, dev, p.off_y)
+        X = hk.HipCloud(p.xs, p.log_a, dev, p.off_x, role=0)
+        Y = hk.HipCloud(p.ys, p.log_b, dev, p.off_y, role=1)
         loop = hk.DeviceLoop(X, Y, eps=opts.eps, rho_x=p.rho_x, rho_y=p.rho_y, sched=p.sched, stages=p.stages,
                              tol=p.tol, stage_tol=p.stage_tol, max_iters=opts.max_iters,
                              check_every=opts.check_every, stage_max_iters=opts.stage_max_iters,

@@ -12,6 +12,7 @@ import pytest
 from scipy.special import logsumexp
 
 TILE, WAVES, XCDS, RB, PIECES, BLOCK = 32, 4, 8, 2, 3, 256
+STREAM_MAX_CHUNKS, COL_TILES = 4, 256        # streamed variant: nc <= 4; column terms staged per 256 tiles
 ROWS_PER_GROUP = TILE * RB * WAVES
 EMPTY = -1.0e30
 FIRST = [0, 0, 1, 0, 1, 2]     # (first-cloud piece, second-cloud piece) of the six products
@@ -145,11 +146,26 @@ def emulate_lse(xa, ya, role=0, ncu=256, per_cu=1, c=np.log2(np.e)):
             slot = p - s.first(g)
             assert 0 <= slot < slots
             seen[g, tb:te] += 1
-            # LDS staging of every tile of the segment (both buffers), as the workgroup does it
+            staged = {}
+            if nc <= STREAM_MAX_CHUNKS:
+                # streamed: column terms of runs of COL_TILES tiles into LDS; operands straight from memory
+                lds_col = np.full(COL_TILES * 32, np.nan, dtype=np.float32)
+                for t0 in range(tb, te, COL_TILES):
+                    t1 = min(t0 + COL_TILES, te)
+                    k = np.arange((t1 - t0) * 32)
+                    assert k.max() < lds_col.size and (t0 * 32 + k).max() < mp
+                    lds_col[k] = u[t0 * 32 + k]
+                    for t in range(t0, t1):
+                        rd = (t - t0) * 32 + np.arange(32)
+                        assert rd.max() < lds_col.size
+                        gi = t * tile16 + np.arange(tile16)
+                        assert gi.max() < yc.shape[0]
+                        staged[t] = (yc[gi].copy(), lds_col[rd].copy())
+                loads = [min(t + 1, te - 1) for t in range(tb, te)]      # the one-ahead operand loads
+                assert max(loads) * tile16 + tile16 - 1 < yc.shape[0]
             lds_y = np.full((2 * tile16, 8), np.nan, dtype=np.float32)
             lds_col = np.full(64, np.nan, dtype=np.float32)
-            staged = {}
-            for t in list(range(tb, te)) + [te - 1]:
+            for t in (list(range(tb, te)) + [te - 1]) if nc > STREAM_MAX_CHUNKS else []:
                 buf = (t - tb) & 1
                 for k in range(per_thread):
                     idx = np.where(tid + k * BLOCK < tile16, tid + k * BLOCK, tile16 - 1)
@@ -214,7 +230,7 @@ def emulate_lse(xa, ya, role=0, ncu=256, per_cu=1, c=np.log2(np.e)):
 @pytest.mark.parametrize("rows,m,K,ncu,role", [(1, 1, 1, 256, 0), (1, 1, 1, 256, 1), (2, 5, 3, 256, 0),
                                                (33, 31, 8, 256, 1), (64, 300, 65, 256, 0), (300, 100, 5, 3, 1),
                                                (257, 1000, 17, 4, 0), (500, 70, 30, 3, 0), (129, 1500, 12, 8, 1),
-                                               (600, 40, 128, 256, 0)])
+                                               (600, 40, 128, 256, 0), (40, 9000, 64, 1, 1), (70, 300, 100, 1, 0)])
 def test_emulated_partial_and_finalize_match_logsumexp(rows, m, K, ncu, role):
     rng = np.random.default_rng(rows + m + K)
     xa = rng.normal(size=(rows, K)).astype(np.float32)

@@ -57,7 +57,12 @@ struct PartialArgs {
     Split s;
 };
 
-// Launch the partial kernel for kp = 16 * nc on P workgroups.
-hipError_t launch_partial(const PartialArgs& a, int nc, hipStream_t stream);
+// Launch the partial kernel for kp = 16 * nc on P workgroups (nc <= 4: launch_partial_small, else
+// launch_partial_large; the two are separate objects built from sk_lse_partial.hip).
+hipError_t launch_partial_small(const PartialArgs& a, int nc, hipStream_t stream);
+hipError_t launch_partial_large(const PartialArgs& a, int nc, hipStream_t stream);
+inline hipError_t launch_partial(const PartialArgs& a, int nc, hipStream_t stream) {
+    return nc <= 4 ? launch_partial_small(a, nc, stream) : launch_partial_large(a, nc, stream);
+}
 
 }  // namespace sk

@@ -25,15 +25,28 @@
 //
 // Layout of one workgroup (4 waves, one per SIMD of a CU): wave w owns kRowBlocks blocks of 32 rows of a
 // row group (its bf16 pieces stay in registers for the whole work segment), and all four waves walk the same
-// column tiles, which are staged once per workgroup in LDS (double buffered, with the tile's 32 column
-// terms). MFMA orientation: A = 32 columns, B = 32 rows, so lane l's 16 accumulators all belong to row
-// l % 32 (columns 8 (r / 4) + 4 (l / 32) + r % 4); row reductions stay inside a lane and lanes l, l + 32 are
-// merged once per segment.
+// column tiles. Two ways to feed the column tiles, chosen by size:
+//   - streamed (kp <= 64): every wave loads the tile's pieces straight into registers one tile ahead; the
+//     four waves of the CU read the same addresses at about the same time and share them through L1. The
+//     column terms of the whole segment are computed once into LDS. No per-tile barrier.
+//   - staged (kp > 64, where a register double buffer no longer fits): the workgroup stages each tile and
+//     its 32 column terms once in LDS (double buffered, one barrier per tile).
+// MFMA orientation: A = 32 columns, B = 32 rows, so lane l's 16 accumulators all belong to row l % 32
+// (columns 8 (r / 4) + 4 (l / 32) + r % 4); row reductions stay inside a lane and lanes l, l + 32 are merged
+// once per segment.
+//
+// This file is compiled twice: SK_PARTIAL_LARGE = 0 builds the streamed instantiations (nc <= 4) with MFMA
+// results forced into VGPRs (-mllvm -amdgpu-mfma-vgpr-form: the epilogue reads them without copies),
+// SK_PARTIAL_LARGE = 1 the staged ones (nc > 4) with the compiler's default register classes.
 
 #include <type_traits>
 #include <utility>
 
 #include "sk_common.h"
+
+#ifndef SK_PARTIAL_LARGE
+#define SK_PARTIAL_LARGE 0
+#endif
 
 namespace sk {
 namespace {
@@ -60,8 +73,9 @@ __device__ __forceinline__ void static_for(F&& f) {
 // The online log-sum-exp update of one row block and one tile, as kOps elementary steps:
 //   j in [0, 16):  a_r = acc_r + col_r
 //   j in [16, 24): running max over a pair of scores
-//   j in [24, 40): s += exp2(c (a_r - m))
-//   j == 40:       S = S exp2(c (M - m)) + s, M = m
+//   j in [24, 40): e_r = exp2(c (a_r - m)); s += e_(r-1)   (each exp is consumed one step later, so no
+//                  instruction waits on the transcendental unit)
+//   j == 40:       S = S exp2(c (M - m)) + s + e_15, M = m
 // Steps are spread over the MFMA slots of the next tile in proportion to their cost (an exp step ~7 VALU).
 constexpr int kOps = 41;
 constexpr int op_cost(int j) { return j < 24 ? 1 : 7; }
@@ -84,25 +98,27 @@ constexpr int op_begin(int i, int NS) {
 
 template <int RB>
 struct Online {
-    float m[RB], s[RB];
+    float m[RB], s[RB], pend[RB];
     template <int k>
     __device__ __forceinline__ void step(f32x16 (&acc)[RB], const f32x16& col, float (&M)[RB], float (&S)[RB],
                                          float c) {
         constexpr int j = k / RB, b = k % RB;
         if constexpr (j < 16) {
             acc[b][j] = acc[b][j] + col[j];
-            if constexpr (j == 0) {
-                m[b] = M[b];
-                s[b] = 0.0f;
-            }
+            if constexpr (j == 0) m[b] = M[b];
         } else if constexpr (j < 24) {
             constexpr int p = j - 16;
             m[b] = fmaxf(m[b], fmaxf(acc[b][2 * p], acc[b][2 * p + 1]));
         } else if constexpr (j < 40) {
             constexpr int r = j - 24;
-            s[b] += ex2(c * (acc[b][r] - m[b]));
+            const float e = ex2(c * (acc[b][r] - m[b]));
+            if constexpr (r == 0)
+                s[b] = 0.0f;
+            else
+                s[b] += pend[b];
+            pend[b] = e;
         } else {
-            S[b] = fmaf(S[b], ex2(c * (M[b] - m[b])), s[b]);
+            S[b] = fmaf(S[b], ex2(c * (M[b] - m[b])), s[b] + pend[b]);
             M[b] = m[b];
         }
     }
@@ -113,7 +129,7 @@ constexpr int kFirstPiece[6] = {0, 0, 1, 0, 1, 2};
 constexpr int kSecondPiece[6] = {0, 1, 0, 2, 1, 0};
 
 template <int NC, int ROLE>
-struct Segment {
+struct Staged {
     static constexpr int RB = kRowBlocks;
     static constexpr int TILE16 = NC * kPieces * 64;   // 16-byte units per packed 32-point tile
     static constexpr int PER_THREAD = (TILE16 + kBlock - 1) / kBlock;
@@ -249,12 +265,144 @@ struct Segment {
     }
 };
 
+// Column terms computed into LDS once per run of kColTiles tiles (streamed variant).
+constexpr int kColTiles = 256;
+constexpr int kStreamMaxChunks = 4;
+
+template <int NC, int ROLE>
+struct Streamed {
+    static constexpr int RB = kRowBlocks;
+    static constexpr int TILE16 = NC * kPieces * 64;
+    static constexpr int NS = 6 * NC * RB;
+
+    __device__ __forceinline__ static void run(const PartialArgs& a, int rb0, int tb, int te, int slot, float alpha,
+                                               float beta, float c, float* lds_col) {
+        const int tid = threadIdx.x;
+        const int lane = tid & 63;
+        const int h = lane >> 5;
+
+        bf16x8 xv[RB][NC][kPieces];
+#pragma unroll
+        for (int b = 0; b < RB; ++b) {
+            const int blk = rb0 + b < a.nrb ? rb0 + b : a.nrb - 1;   // a missing block recomputes the last one
+#pragma unroll
+            for (int cc = 0; cc < NC; ++cc)
+#pragma unroll
+                for (int p = 0; p < kPieces; ++p)
+                    xv[b][cc][p] = a.xr[(size_t)blk * TILE16 + (cc * kPieces + p) * 64 + lane];
+        }
+        float M[RB], S[RB];
+#pragma unroll
+        for (int b = 0; b < RB; ++b) {
+            M[b] = kEmpty;
+            S[b] = 0.0f;
+        }
+
+        int cbase = tb;
+        auto stage_cols = [&](int t0, int t1) {       // column terms of tiles [t0, t1) into LDS
+            __syncthreads();
+            for (int k = tid; k < (t1 - t0) * 32; k += kBlock) {
+                const int j = t0 * 32 + k;
+                lds_col[k] = fmaf(beta, a.v[j], alpha * a.u[j]);
+            }
+            __syncthreads();
+            cbase = t0;
+        };
+        bf16x8 yA[NC][kPieces], yB[NC][kPieces];
+        auto load_y = [&](int t, bf16x8 (&yv)[NC][kPieces]) {
+#pragma unroll
+            for (int cc = 0; cc < NC; ++cc)
+#pragma unroll
+                for (int p = 0; p < kPieces; ++p) yv[cc][p] = a.yc[(size_t)t * TILE16 + (cc * kPieces + p) * 64 + lane];
+        };
+        auto read_col = [&](int t, f32x16& col) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const f32x4 cv = *reinterpret_cast<const f32x4*>(&lds_col[(t - cbase) * 32 + 8 * q + 4 * h]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) col[4 * q + e] = cv[e];
+            }
+        };
+
+        f32x16 accA[RB], accB[RB], colA, colB;
+        Online<RB> on;
+        auto tile = [&](f32x16 (&accN)[RB], f32x16 (&accP)[RB], const f32x16& colP, const bf16x8 (&yv)[NC][kPieces],
+                        bool epi) {
+#pragma unroll
+            for (int b = 0; b < RB; ++b) accN[b] = f32x16{};
+            static_for<0, NS>([&](auto I) {
+                constexpr int i = decltype(I)::value;
+                constexpr int cc = i / (6 * RB), p = (i / RB) % 6, b = i % RB;
+                constexpr int rp = ROLE == 0 ? kFirstPiece[p] : kSecondPiece[p];
+                constexpr int cp = ROLE == 0 ? kSecondPiece[p] : kFirstPiece[p];
+                accN[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(yv[cc][cp], xv[b][cc][rp], accN[b], 0, 0, 0);
+                if (epi) {
+                    constexpr int k0 = op_begin<RB>(i, NS), k1 = op_begin<RB>(i + 1, NS);
+                    static_for<k0, k1>([&](auto K) { on.template step<decltype(K)::value>(accP, colP, M, S, c); });
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            });
+        };
+        auto update = [&](f32x16 (&accP)[RB], const f32x16& colP) {
+            static_for<0, RB * kOps>([&](auto K) { on.template step<decltype(K)::value>(accP, colP, M, S, c); });
+        };
+
+        // Tiles in pairs so the accumulator and operand buffers alternate without copies; the operand load of
+        // the tile after the last is the last tile again (in bounds, unused).
+        const int last = te - 1;
+        int cend = tb + kColTiles < te ? tb + kColTiles : te;
+        stage_cols(tb, cend);
+        int t = tb;
+        load_y(t, yA);
+        read_col(t, colA);
+        load_y(t + 1 < te ? t + 1 : last, yB);
+        tile(accA, accB, colB, yA, false);
+        ++t;
+        while (t < te) {
+            if (t >= cend) {
+                cend = t + kColTiles < te ? t + kColTiles : te;
+                stage_cols(t, cend);
+            }
+            read_col(t, colB);
+            load_y(t + 1 < te ? t + 1 : last, yA);
+            tile(accB, accA, colA, yB, true);
+            ++t;
+            if (t >= te) {
+                update(accB, colB);
+                goto done;
+            }
+            if (t >= cend) {
+                cend = t + kColTiles < te ? t + kColTiles : te;
+                stage_cols(t, cend);
+            }
+            read_col(t, colA);
+            load_y(t + 1 < te ? t + 1 : last, yB);
+            tile(accA, accB, colB, yA, true);
+            ++t;
+        }
+        update(accA, colA);
+    done:
+#pragma unroll
+        for (int b = 0; b < RB; ++b) {
+            const float Mo = __shfl_xor(M[b], 32);
+            const float So = __shfl_xor(S[b], 32);
+            const float Mn = fmaxf(M[b], Mo);
+            const float Sn = S[b] * ex2(c * (M[b] - Mn)) + So * ex2(c * (Mo - Mn));
+            if (h == 0 && rb0 + b < a.nrb)
+                a.part[(size_t)slot * a.rows_pad + (size_t)(rb0 + b) * 32 + lane] = make_float2(Mn, Sn);
+        }
+    }
+};
+
 template <int NC, int ROLE>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void lse_partial_kernel(PartialArgs a) {
     if (a.skip != nullptr && *a.skip != 0) return;
-    __shared__ bf16x8 lds_y[2 * NC * kPieces * 64];
-    __shared__ __attribute__((aligned(16))) float lds_col[64];
+    constexpr bool kStream = NC <= kStreamMaxChunks;
+    constexpr int kLdsY = kStream ? 1 : 2 * NC * kPieces * 64;
+    constexpr int kLdsCol = kStream ? kColTiles * 32 : 64;
+    __shared__ bf16x8 lds_y[kLdsY];
+    __shared__ __attribute__((aligned(16))) float lds_col[kLdsCol];
     const int wv = threadIdx.x >> 6;
     const int P = a.s.P;
     const int p = xcd_contiguous(blockIdx.x, P);
@@ -283,7 +431,10 @@ void lse_partial_kernel(PartialArgs a) {
         // Waves past the last row block recompute it (their rows are not stored) so that every wave takes part
         // in the workgroup's barriers.
         const int rb0 = (g * kWaves + wv) * kRowBlocks;
-        Segment<NC, ROLE>::run(a, rb0, tb, te, slot, alpha, beta, c, lds_y, lds_col);
+        if constexpr (kStream)
+            Streamed<NC, ROLE>::run(a, rb0, tb, te, slot, alpha, beta, c, lds_col);
+        else
+            Staged<NC, ROLE>::run(a, rb0, tb, te, slot, alpha, beta, c, lds_y, lds_col);
         u += te - tb;
     }
 }
@@ -299,12 +450,9 @@ hipError_t launch_nc(const PartialArgs& a, hipStream_t st) {
 
 }  // namespace
 
-hipError_t launch_partial(const PartialArgs& a, int nc, hipStream_t st) {
+#if SK_PARTIAL_LARGE
+hipError_t launch_partial_large(const PartialArgs& a, int nc, hipStream_t st) {
     switch (nc) {
-        case 1: return launch_nc<1>(a, st);
-        case 2: return launch_nc<2>(a, st);
-        case 3: return launch_nc<3>(a, st);
-        case 4: return launch_nc<4>(a, st);
         case 5: return launch_nc<5>(a, st);
         case 6: return launch_nc<6>(a, st);
         case 7: return launch_nc<7>(a, st);
@@ -312,5 +460,16 @@ hipError_t launch_partial(const PartialArgs& a, int nc, hipStream_t st) {
         default: return hipErrorInvalidValue;
     }
 }
+#else
+hipError_t launch_partial_small(const PartialArgs& a, int nc, hipStream_t st) {
+    switch (nc) {
+        case 1: return launch_nc<1>(a, st);
+        case 2: return launch_nc<2>(a, st);
+        case 3: return launch_nc<3>(a, st);
+        case 4: return launch_nc<4>(a, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+#endif
 
 }  // namespace sk

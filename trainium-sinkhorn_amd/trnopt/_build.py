@@ -6,7 +6,9 @@ The library lands in trnopt/_lib/ next to this file (in the source tree, so it s
 directory); nothing is compiled at import time. Two translation units:
 
 * sk_lse_partial.hip -- the MFMA partial (max, sum) kernel, built with -fno-honor-nans -mno-amdgpu-ieee
-  (no NaN ever reaches it; this drops the IEEE canonicalisation of every MFMA result before a max);
+  (no NaN ever reaches it; this drops the IEEE canonicalisation of every MFMA result before a max), twice:
+  the streamed instantiations (kp <= 64) with MFMA results in VGPRs (-amdgpu-mfma-vgpr-form), and the staged
+  ones (kp > 64) with the compiler's default register classes;
 * sk_kernels.hip -- packing, finalisation, the on-device loop and the C ABI, built with default NaN
   semantics (the loop state stores NaN for "not checked yet").
 
@@ -32,9 +34,11 @@ ARCH = os.environ.get("TRNOPT_HIP_ARCH", "gfx950")
 
 COMMON = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", f"-I{INCLUDE}", f"-I{CSRC}",
           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-Wno-unused-command-line-argument"]
-UNITS = [
-    ("sk_lse_partial.hip", ["-fno-honor-nans", "-mno-amdgpu-ieee"]),
-    ("sk_kernels.hip", []),
+UNITS = [   # (source, object name, extra flags)
+    ("sk_lse_partial.hip", "sk_lse_partial_small", ["-fno-honor-nans", "-mno-amdgpu-ieee", "-DSK_PARTIAL_LARGE=0",
+                                                    "-mllvm", "-amdgpu-mfma-vgpr-form"]),
+    ("sk_lse_partial.hip", "sk_lse_partial_large", ["-fno-honor-nans", "-mno-amdgpu-ieee", "-DSK_PARTIAL_LARGE=1"]),
+    ("sk_kernels.hip", "sk_kernels", []),
 ]
 
 
@@ -55,8 +59,8 @@ def build(verbose: bool = False) -> Path:
     LIB_DIR.mkdir(parents=True, exist_ok=True)
     with tempfile.TemporaryDirectory(prefix="trnopt_build_") as tmp:
         objs = []
-        for src, extra in UNITS:
-            obj = Path(tmp) / (Path(src).stem + ".o")
+        for src, name, extra in UNITS:
+            obj = Path(tmp) / (name + ".o")
             cmd = [cc, *COMMON, *extra, "-c", str(CSRC / src), "-o", str(obj)]
             _run(cmd, verbose)
             objs.append(str(obj))

@@ -15,13 +15,15 @@
  *   - Every entry point returns 0 on success, a negative SK_E* code for a rejected argument, or a
  *     positive hipError_t for a runtime failure. sk_last_error() describes the last failure on the
  *     calling thread. Nothing aborts the process.
- *   - Point clouds are "packed": padded to a multiple of SK_TILE points and SK_KP_ALIGN coordinates,
- *     every fp32 coordinate split exactly into three bf16 pieces (v = v0 + v1 + v2), and stored in the
- *     tile-interleaved order that the bf16 MFMA kernels read with one coalesced 16-byte load per lane
+ *   - Point clouds are "packed": a header holding the cloud's power-of-two scale s (max |coordinate| * s
+ *     in [2^13, 2^14)), then the points padded to a multiple of SK_TILE and the coordinates to
+ *     SK_KP_ALIGN, every scaled coordinate s x split into two fp16 pieces (within 2^-23 of s x), in the
+ *     tile-interleaved order that the fp16 MFMA kernels read with one coalesced 16-byte load per lane
  *     (sk_pack_cloud_f32 builds it from a row-major (n, d) fp32 array; sk_packed_bytes gives its size).
- *     The kernels form x.y from the six leading cross products of the pieces, accumulated in fp32: as
- *     accurate as an fp32 dot product, and bit-identical in the two directions of a pair of half-steps
- *     (rows_role 0 and 1) over the same two clouds.
+ *     The kernels form x.y from the four products of the pieces, accumulated in fp32: as accurate as an
+ *     fp32 dot product, and bit-identical in the two directions of a pair of half-steps (rows_role 0
+ *     and 1) over the same two clouds. Coordinates must satisfy max |x| <= 7e13; the precision is that of
+ *     fp32 for max |x| >= 2^-26 (1.5e-8) and degrades gracefully below.
  *   - Shifted potentials follow the reference (src/trnopt/sinkhorn.py:28-33): fh = f - |x|^2.
  */
 #ifndef TRNOPT_HIP_H
@@ -34,8 +36,9 @@ extern "C" {
 #endif
 
 #define SK_TILE 32            /* points per packed tile (one 32x32 MFMA output block) */
-#define SK_KP_ALIGN 16        /* coordinates are padded to a multiple of this (one bf16 MFMA K chunk) */
-#define SK_PACKED_BYTES_PER_COORD 6   /* three bf16 pieces per padded coordinate */
+#define SK_KP_ALIGN 16        /* coordinates are padded to a multiple of this (one fp16 MFMA K chunk) */
+#define SK_PACKED_BYTES_PER_COORD 4   /* two fp16 pieces per padded coordinate */
+#define SK_PACKED_HEADER_BYTES 256    /* before the tiles: max |coordinate| and the scale */
 #define SK_KP_MAX 128         /* largest padded dimension the kernels are built for */
 #define SK_PAD_LOG_WEIGHT (-1e9)  /* log weight of a padding point (src/trnopt/sinkhorn.py:59) */
 
@@ -57,8 +60,9 @@ int sk_pad_dim(int d);         /* d rounded up to a multiple of SK_KP_ALIGN */
 
 /*
  * Pack a row-major cloud pts (n, d), leading dimension ld >= d (device, fp32), into the tile layout
- * out (sk_packed_bytes(n, d) bytes, device, 16-byte aligned): npad = sk_pad_points(n) points,
- * kp = sk_pad_dim(d) coordinates, three bf16 pieces each. Padding is zero.
+ * out (sk_packed_bytes(n, d) bytes, device, 16-byte aligned): a header, then npad = sk_pad_points(n)
+ * points of kp = sk_pad_dim(d) coordinates, two fp16 pieces each. Padding is zero. Three launches on
+ * `stream` (header, max |coordinate|, pieces).
  * Replaces the per-block [x^T ; 1] copies of _Cloud (src/trnopt/sinkhorn.py:159-165); the augmented
  * "1" is not stored, the column term enters the accumulator instead.
  */

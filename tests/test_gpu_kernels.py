@@ -158,3 +158,22 @@ def test_f_and_g_updates_form_bit_identical_dots(hip, d):
         exact = x.astype(np.float64) @ y[j].astype(np.float64)
         bound = np.abs(x.astype(np.float64)) @ np.abs(y[j].astype(np.float64))
         assert np.all(np.abs(f_side - exact) <= 4e-7 * bound + 1e-30)
+
+
+@pytest.mark.parametrize("mx,my", [(1e-5, 1e5), (3e-8, 1e4), (1e3, 1e-3), (1.0, 1.0)])
+def test_row_lse_with_badly_scaled_clouds(hip, mx, my):
+    """Each packed cloud carries its own power-of-two scale: clouds far from unit magnitude keep the row-LSE's
+    accuracy (scores x.y of order 1 here)."""
+    rng = np.random.default_rng(int(-np.log10(mx) * 10 + 100))
+    xa = (rng.normal(size=(300, 40)) * mx).astype(np.float32)
+    ya = (rng.normal(size=(700, 40)) * my).astype(np.float32)
+    out = hip.row_lse(torch.from_numpy(xa).to(DEV), torch.from_numpy(ya).to(DEV)).cpu().numpy()
+    want = brute.row_lse(xa, ya)
+    assert np.all(np.abs(out - want) <= _lse_tol(xa, ya)), np.abs(out - want).max()
+
+
+def test_out_of_range_coordinates_are_rejected(hip):
+    with pytest.raises(ValueError, match="coordinates"):
+        hip.row_lse(torch.full((4, 3), 1e15, device=DEV), torch.ones(5, 3, device=DEV))
+    with pytest.raises(ValueError, match="coordinates"):
+        hip.HipCloud(np.full((4, 3), np.inf), np.zeros(4), DEV)

@@ -2,21 +2,26 @@
 
 Every load and store of pack_cloud_kernel, lse_partial_kernel (global loads, LDS staging and reads, partial
 slots) and lse_finalize_kernel is replayed in numpy with the kernels' own formulas (workgroup renumbering,
-stream-K ranges, partial slots, the three-piece bf16 packing, the v_mfma_f32_32x32x16_bf16 operand and
-accumulator lane mapping, the product order of both row roles), asserting that every index is inside its
-buffer and that the emulated result equals a direct float64 log-sum-exp. It needs no GPU.
+stream-K ranges, partial slots, the power-of-two scale and two-piece fp16 packing, the
+v_mfma_f32_32x32x16_f16 operand and accumulator lane mapping, the product order of both row roles, the
+scaled accumulator units), asserting that every index is inside its buffer and that the emulated result
+equals a direct float64 log-sum-exp. It needs no GPU.
 """
 
 import numpy as np
 import pytest
 from scipy.special import logsumexp
 
-TILE, WAVES, XCDS, RB, PIECES, BLOCK = 32, 4, 8, 2, 3, 256
+TILE, WAVES, XCDS, RB, BLOCK = 32, 4, 8, 2, 256
 STREAM_MAX_CHUNKS, COL_TILES = 4, 256        # streamed variant: nc <= 4; column terms staged per 256 tiles
 ROWS_PER_GROUP = TILE * RB * WAVES
 EMPTY = -1.0e30
-FIRST = [0, 0, 1, 0, 1, 2]     # (first-cloud piece, second-cloud piece) of the six products
-SECOND = [0, 1, 0, 2, 1, 0]
+FIRST = [0, 0, 1, 1]           # fp16x2 (half-steps): (first-cloud piece, second-cloud piece) of the products
+SECOND = [0, 1, 0, 1]
+FIRST3 = [0, 0, 1, 0, 1, 2]    # bf16x3 (general row log-sum-exp)
+SECOND3 = [0, 1, 0, 2, 1, 0]
+CONTRACTIONS = {"f16x2": (2, FIRST, SECOND), "bf16x3": (3, FIRST3, SECOND3)}
+PAD_SCORE = np.float32(-1.0e30)
 
 
 def pad_points(n):
@@ -25,6 +30,23 @@ def pad_points(n):
 
 def pad_dim(d):
     return -(-d // 16) * 16
+
+
+def pack_scale(m):
+    """The power-of-two scale of a cloud with max |coordinate| m: m * s in [2^13, 2^14), clamped."""
+    if not m > 0:
+        return np.float32(1.0)
+    e = np.frexp(np.float32(m))[1]                      # m in [2^(e-1), 2^e)
+    k = -32 if e > 46 else (40 if e < -26 else 14 - e)
+    return np.float32(np.ldexp(1.0, k))
+
+
+def split2(v):
+    """float32 (already scaled) -> two fp16 pieces, as float32."""
+    v = np.asarray(v, dtype=np.float32)
+    a0 = v.astype(np.float16).astype(np.float32)
+    a1 = (v - a0).astype(np.float32).astype(np.float16).astype(np.float32)
+    return a0, a1
 
 
 def bf16_rne(v):
@@ -43,11 +65,18 @@ def split3(v):
     return a0, a1, a2
 
 
-def pack(src, n, d):
-    """pack_cloud_kernel: the (npad / 32 * nc * 3 * 64, 8) array of 16-byte units (as 8 float32 values)."""
+def pack(src, n, d, contraction="f16x2"):
+    """pack_cloud_kernel (f16x2: header, max |x|, scaled two fp16 pieces) or pack_cloud_bf3_kernel (bf16x3:
+    three exact bf16 pieces, scale 1): (scale, the (npad / 32 * nc * pieces * 64, 8) array of 16-byte units as
+    8 float32 values)."""
+    PIECES = CONTRACTIONS[contraction][0]
     kp = pad_dim(d)
     nc = kp // 16
     npad = pad_points(n)
+    if contraction == "f16x2":
+        s = pack_scale(np.abs(src[:n, :d]).max() if n * d else 0.0)
+    else:
+        s = np.float32(1.0)
     out = np.full((npad // TILE * nc * PIECES * 64, 8), np.nan, dtype=np.float32)
     idx = np.arange(npad // TILE * nc * 64)                  # one thread per (tile, chunk, lane)
     lane = idx % 64
@@ -60,15 +89,15 @@ def pack(src, n, d):
     ok = (row[:, None] < n) & (k < d)
     flat = np.where(ok, row[:, None] * d + k, 0)
     assert flat.max() < src.size
-    v = np.where(ok, src.ravel()[flat], 0.0).astype(np.float32)
-    pieces = split3(v)
+    v = (np.where(ok, src.ravel()[flat], 0.0).astype(np.float32) * s).astype(np.float32)
+    pieces = split2(v) if contraction == "f16x2" else split3(v)
     base = (T * nc + cc) * (PIECES * 64) + lane
     for p in range(PIECES):
         dst = base + 64 * p
         assert dst.max() < out.shape[0]
         out[dst] = pieces[p]
     assert not np.isnan(out).any(), "every unit written"
-    return out
+    return s, out
 
 
 class Split:
@@ -102,30 +131,35 @@ def xcd_contiguous(b, P):
 
 
 def mfma_32x32x16(Aop, Bop):
-    """v_mfma_f32_32x32x16_bf16 on per-lane operands (64, 8): lane l holds A[m = l % 32][k = 8 (l / 32) + e] and
+    """v_mfma_f32_32x32x16_f16 on per-lane operands (64, 8): lane l holds A[m = l % 32][k = 8 (l / 32) + e] and
     B[k = 8 (l / 32) + e][n = l % 32]. Returns the (64, 16) accumulator: lane l, register r holds
     D[m = 8 (r / 4) + 4 (l / 32) + r % 4][n = l % 32]."""
     A = np.concatenate([Aop[:32], Aop[32:]], axis=1).astype(np.float64)    # (m, k)
     B = np.concatenate([Bop[:32], Bop[32:]], axis=1).astype(np.float64)    # (n, k)
-    D = A @ B.T                                                             # (m, n); bf16 products exact
+    D = A @ B.T                                                             # (m, n); fp16 products exact
     lane = np.arange(64)
     r = np.arange(16)
     m = 8 * (r[None, :] // 4) + 4 * (lane[:, None] // 32) + r[None, :] % 4
     return D[m, (lane % 32)[:, None]]
 
 
-def emulate_lse(xa, ya, role=0, ncu=256, per_cu=1, c=np.log2(np.e)):
+def emulate_lse(xa, ya, role=0, ncu=256, per_cu=1, c=np.log2(np.e), contraction="bf16x3"):
     """Row LSE (plain mode: alpha = 1 on a 0 / -1e30 mask, beta = 0) through the kernels' index math, the
-    score / max / sum arithmetic in float32 as on the GPU (overflow or NaN raises)."""
+    score / max / sum arithmetic in float32 as on the GPU (overflow or NaN raises). The product's row-LSE entry
+    point uses bf16x3; f16x2 (the half-steps' packing) runs through the same index math here."""
+    PIECES, FIRST_, SECOND_ = CONTRACTIONS[contraction]
     rows, K = xa.shape
     m = ya.shape[0]
     kp, rp, mp = pad_dim(K), pad_points(rows), pad_points(m)
     nc = kp // 16
     tile16 = nc * PIECES * 64
     per_thread = -(-tile16 // BLOCK)
-    xr = pack(xa, rows, K)
-    yc = pack(ya, m, K)
-    u = np.where(np.arange(mp) < m, 0.0, -1.0e30).astype(np.float32)
+    sx, xr = pack(xa, rows, K, contraction)
+    sy, yc = pack(ya, m, K, contraction)
+    sigma, inv_sigma = np.float32(sx * sy), np.float32((1 / sx) * (1 / sy))
+    u_raw = np.where(np.arange(mp) < m, 0.0, -1.0e30).astype(np.float32)
+    with np.errstate(over="ignore"):
+        u = np.maximum((u_raw * sigma).astype(np.float32), PAD_SCORE)     # scaled column term, floored
     nrb, nt, ngroups, s, slots = plan(rp, mp, ncu, per_cu)
     part = np.full((slots, rp, 2), np.nan)
     lane = np.arange(64)
@@ -133,8 +167,8 @@ def emulate_lse(xa, ya, role=0, ncu=256, per_cu=1, c=np.log2(np.e)):
     tid = np.arange(BLOCK)
     cj = tid & 31
     seen = np.zeros((ngroups, nt), dtype=int)
-    cf = np.float32(c)
-    ra, ca = (FIRST, SECOND) if role == 0 else (SECOND, FIRST)
+    cf = np.float32(np.float32(c) * inv_sigma)
+    ra, ca = (FIRST_, SECOND_) if role == 0 else (SECOND_, FIRST_)
     for b in range(s.P):
         p = xcd_contiguous(b, s.P)
         u1 = (p + 1) * s.work // s.P
@@ -198,7 +232,7 @@ def emulate_lse(xa, ya, role=0, ncu=256, per_cu=1, c=np.log2(np.e)):
                         col = cbuf[ci].reshape(64, 16)
                         acc = np.zeros((64, 16))
                         for cc in range(nc):
-                            for pp in range(6):
+                            for pp in range(len(FIRST_)):
                                 acc += mfma_32x32x16(yv[cc, ca[pp]], xv[cc, ra[pp]])
                         a = (acc.astype(np.float32) + col).astype(np.float32)
                         Mn = np.maximum(M, a.max(axis=1))
@@ -212,7 +246,7 @@ def emulate_lse(xa, ya, role=0, ncu=256, per_cu=1, c=np.log2(np.e)):
                     if rb0 + bb < nrb:
                         idx = (rb0 + bb) * 32 + lane[:32]
                         assert idx.max() < rp
-                        part[slot, idx, 0], part[slot, idx, 1] = Mn[:32], Sn[:32]
+                        part[slot, idx, 0], part[slot, idx, 1] = Mn[:32] * inv_sigma, Sn[:32]
             uu += te - tb
     assert np.all(seen == 1), "every (row group, tile) unit exactly once"
     out = np.empty(rp)
@@ -227,15 +261,17 @@ def emulate_lse(xa, ya, role=0, ncu=256, per_cu=1, c=np.log2(np.e)):
     return out[:rows], dict(slots=slots, P=s.P, work=s.work)
 
 
-@pytest.mark.parametrize("rows,m,K,ncu,role", [(1, 1, 1, 256, 0), (1, 1, 1, 256, 1), (2, 5, 3, 256, 0),
-                                               (33, 31, 8, 256, 1), (64, 300, 65, 256, 0), (300, 100, 5, 3, 1),
-                                               (257, 1000, 17, 4, 0), (500, 70, 30, 3, 0), (129, 1500, 12, 8, 1),
-                                               (600, 40, 128, 256, 0), (40, 9000, 64, 1, 1), (70, 300, 100, 1, 0)])
-def test_emulated_partial_and_finalize_match_logsumexp(rows, m, K, ncu, role):
+@pytest.mark.parametrize("rows,m,K,ncu,role,ct", [(1, 1, 1, 256, 0, "bf16x3"), (1, 1, 1, 256, 1, "f16x2"),
+                                                  (2, 5, 3, 256, 0, "f16x2"), (33, 31, 8, 256, 1, "f16x2"),
+                                                  (64, 300, 65, 256, 0, "bf16x3"), (300, 100, 5, 3, 1, "f16x2"),
+                                                  (257, 1000, 17, 4, 0, "bf16x3"), (500, 70, 30, 3, 0, "f16x2"),
+                                                  (129, 1500, 12, 8, 1, "f16x2"), (600, 40, 128, 256, 0, "f16x2"),
+                                                  (40, 9000, 64, 1, 1, "f16x2"), (70, 300, 100, 1, 0, "bf16x3")])
+def test_emulated_partial_and_finalize_match_logsumexp(rows, m, K, ncu, role, ct):
     rng = np.random.default_rng(rows + m + K)
     xa = rng.normal(size=(rows, K)).astype(np.float32)
     ya = (rng.normal(size=(m, K)) * 0.5).astype(np.float32)
-    out, info = emulate_lse(xa, ya, role=role, ncu=ncu)
+    out, info = emulate_lse(xa, ya, role=role, ncu=ncu, contraction=ct)
     np.testing.assert_allclose(out, logsumexp(xa.astype(np.float64) @ ya.astype(np.float64).T, axis=1),
                                rtol=0, atol=2e-5)
 
@@ -263,33 +299,48 @@ def test_split_covers_work_and_slot_bounds(n, m, ncu, per_cu):
     assert slots * rp * 8 < 2 ** 31 * 8
 
 
-def test_split3_is_exact():
+def test_scale_and_split2_error_bound():
     rng = np.random.default_rng(1)
-    for scale in (1.0, 1e-3, 7.3e4, 1e-20, 3e30):
-        v = (rng.normal(size=100_000) * scale).astype(np.float32)
-        a0, a1, a2 = split3(v)
-        for a in (a0, a1, a2):                    # each piece is a bfloat16 value
-            assert np.all((a.view(np.uint32) & 0xFFFF) == 0)
-        np.testing.assert_array_equal(a0.astype(np.float64) + a1 + a2, v.astype(np.float64))
+    for mag in (1.0, 1e-3, 7.3e4, 1e-7, 3e12):        # the full-precision range: max |x| in [2^-26, 7e13]
+        x = (rng.normal(size=100_000) * mag).astype(np.float32)
+        s = pack_scale(np.abs(x).max())
+        scaled_max = np.abs(x).max() * s
+        assert (2.0 ** 13 <= scaled_max < 2.0 ** 14) or (s == 2.0 ** 40 and scaled_max < 2.0 ** 13)
+        v = (x * s).astype(np.float32)
+        np.testing.assert_array_equal(v.astype(np.float64), x.astype(np.float64) * float(s))   # exact scaling
+        a0, a1 = split2(v)
+        for a in (a0, a1):                          # each piece is an fp16 value
+            np.testing.assert_array_equal(a, a.astype(np.float16).astype(np.float32))
+        err = np.abs(a0.astype(np.float64) + a1 - v)
+        assert np.all(err <= 2.0 ** -23 * np.abs(v) + 2.0 ** -25)
+        assert err.max() <= 2.0 ** -22 * scaled_max                    # relative to the cloud's largest value
+    assert pack_scale(7.0e13) * 7.0e13 <= 2.0 ** 14 and pack_scale(0.0) == 1.0
+    # below 2^-26 the scale is clamped and the smallest pieces are fp16 subnormals: precision degrades
+    x = (rng.normal(size=10_000) * 1e-14).astype(np.float32)
+    s = pack_scale(np.abs(x).max())
+    a0, a1 = split2((x * s).astype(np.float32))
+    assert s == 2.0 ** 40 and np.abs(a0.astype(np.float64) + a1 - x * float(s)).max() <= 2.0 ** -18 * np.abs(x).max() * s
 
 
-def test_six_products_are_fp32_accurate_and_symmetric():
-    """The six leading piece products reproduce x.y to fp32 accuracy, and the transposed product order of the
-    other row role adds the same terms in the same order."""
+def test_four_products_are_fp32_accurate_and_symmetric():
+    """The four piece products reproduce x.y to fp32 accuracy, and the transposed product order of the other
+    row role adds the same terms in the same order."""
     rng = np.random.default_rng(2)
     x = rng.normal(size=(50, 64)).astype(np.float32)
     y = (rng.normal(size=(40, 64)) + 0.5).astype(np.float32)
-    xs, ys = split3(x), split3(y)
+    sx, sy = pack_scale(np.abs(x).max()), pack_scale(np.abs(y).max())
+    xs, ys = split2(x * sx), split2(y * sy)
     exact = x.astype(np.float64) @ y.astype(np.float64).T
     bound = np.abs(x.astype(np.float64)) @ np.abs(y.astype(np.float64)).T
-    approx = sum(xs[FIRST[p]].astype(np.float64) @ ys[SECOND[p]].astype(np.float64).T for p in range(6))
-    assert np.max(np.abs(approx - exact) / bound) < 2.0 ** -22
+    approx = sum(xs[FIRST[p]].astype(np.float64) @ ys[SECOND[p]].astype(np.float64).T for p in range(4))
+    approx /= float(sx) * float(sy)
+    assert np.max(np.abs(approx - exact) / bound) < 2.0 ** -21
 
     def accumulate(role, rows, cols, swap_rule=True):
-        """float32 sum of the six products in issue order, with the kernel's piece choice for `role`."""
+        """float32 sum of the four products in issue order, with the kernel's piece choice for `role`."""
         ra, ca = (FIRST, SECOND) if (role == 0 or not swap_rule) else (SECOND, FIRST)
         acc = np.zeros((rows[0].shape[0], cols[0].shape[0]), dtype=np.float32)
-        for p in range(6):
+        for p in range(4):
             acc = (acc + (rows[ra[p]].astype(np.float64) @ cols[ca[p]].astype(np.float64).T).astype(np.float32))
         return acc
 
@@ -301,13 +352,15 @@ def test_six_products_are_fp32_accurate_and_symmetric():
     assert np.abs(f - g_wrong.T).max() > 0
 
 
-def test_pack_layout_roundtrip():
+@pytest.mark.parametrize("ct", ["f16x2", "bf16x3"])
+def test_pack_layout_roundtrip(ct):
     rng = np.random.default_rng(1)
+    PIECES = CONTRACTIONS[ct][0]
     for n, d in [(1, 1), (31, 7), (33, 64), (100, 65), (64, 128)]:
         x = rng.normal(size=(n, d)).astype(np.float32)
         kp = pad_dim(d)
         nc = kp // 16
-        pk = pack(x, n, d)
+        s, pk = pack(x, n, d, ct)
         npad = pad_points(n)
         back = np.zeros((npad, kp))
         for T in range(npad // TILE):
@@ -317,5 +370,21 @@ def test_pack_layout_roundtrip():
                         r, h = lane & 31, lane >> 5
                         unit = pk[((T * nc + cc) * PIECES + p) * 64 + lane]
                         back[T * TILE + r, 16 * cc + 8 * h:16 * cc + 8 * h + 8] += unit
-        np.testing.assert_array_equal(back[:n, :d], x.astype(np.float64))
+        v = x.astype(np.float64) * float(s)
+        if ct == "bf16x3":
+            np.testing.assert_array_equal(back[:n, :d], v)                  # exact
+        else:
+            assert np.all(np.abs(back[:n, :d] - v) <= 2.0 ** -23 * np.abs(v) + 2.0 ** -25)
         assert np.all(back[n:] == 0) and np.all(back[:, d:] == 0)
+
+
+def test_split3_is_exact_over_the_fp32_range():
+    """The row-LSE packing: three bf16 pieces reproduce any fp32 value exactly, whatever its magnitude (the
+    augmented padding rows hold -1e9 next to values of order 1)."""
+    rng = np.random.default_rng(1)
+    for scale in (1.0, 1e-3, 7.3e4, 1e-20, 3e30, 1e9):
+        v = (rng.normal(size=100_000) * scale).astype(np.float32)
+        a0, a1, a2 = split3(v)
+        for a in (a0, a1, a2):
+            assert np.all((a.view(np.uint32) & 0xFFFF) == 0)
+        np.testing.assert_array_equal(a0.astype(np.float64) + a1 + a2, v.astype(np.float64))

@@ -9,6 +9,7 @@ namespace sk {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 constexpr float kLog2e = 1.44269504088896340736f;
@@ -19,7 +20,17 @@ constexpr int kBlock = kWaves * 64;
 constexpr int kRowBlocks = 2;          // 32-row blocks per wave (independent MFMA accumulator chains)
 constexpr int kXcds = 8;
 constexpr int kMaxChunks = 8;          // K chunks of 16 coordinates: kp = 16 * nc <= 128
-constexpr int kPieces = 3;             // bf16 pieces per fp32 coordinate
+// The contraction x.y on the matrix cores:
+//   kF16x2  -- the half-steps: the cloud's power-of-two scaled coordinates as two fp16 pieces, four products
+//              (fp32 accuracy for coordinates within 2^26 of the cloud's largest; 4 bytes per coordinate);
+//   kBF16x3 -- the general row log-sum-exp of arbitrary fp32 matrices: each coordinate as three bf16 pieces
+//              (exact over the whole fp32 range), six products (6 bytes per coordinate).
+enum Contraction { kF16x2 = 0, kBF16x3 = 1 };
+constexpr int pieces_of(int ct) { return ct == kF16x2 ? 2 : 3; }
+constexpr int kHeaderBytes = 256;      // packed cloud header: [0] max |coordinate| (as uint), [1] scale (float)
+constexpr float kScaleTarget = 16384.0f;   // the scale puts max |coordinate| in [2^13, 2^14)
+constexpr float kMaxAbsCoordinate = 7.0e13f; // above this the scaled coordinates would not fit fp16
+constexpr float kPadScore = -1.0e30f;  // floor of a (scaled) column term: padding, never -inf
 
 enum Mode { kHalfStep = 0, kPlainLse = 1 };
 
@@ -42,9 +53,16 @@ __host__ __device__ inline int last_wg(int g, const Split& s) {
     return owner_of((long long)(g + 1) * s.nt - 1, s);
 }
 
+// Tiles of a packed cloud (after its header) and its scale (1 for kBF16x3).
+template <class T>
+__host__ __device__ inline const T* packed_tiles(const void* pk) {
+    return reinterpret_cast<const T*>(reinterpret_cast<const char*>(pk) + kHeaderBytes);
+}
+__device__ inline float packed_scale(const void* pk) { return reinterpret_cast<const float*>(pk)[1]; }
+
 struct PartialArgs {
-    const bf16x8* xr;   // packed rows (three bf16 pieces per coordinate)
-    const bf16x8* yc;   // packed columns
+    const void* xr;     // packed rows (header, then two fp16 pieces per scaled coordinate)
+    const void* yc;     // packed columns
     const float* u;     // column term = alpha * u + beta * v  (m_pad each)
     const float* v;
     const float* sc;    // {2/eps, 1/eps, eps, kappa} (half-step mode)
@@ -54,11 +72,13 @@ struct PartialArgs {
     int rows_pad;
     int mode;
     int rows_role;      // 0: the rows are the first cloud of the pair, 1: the second (piece order)
+    int contraction;    // kF16x2 or kBF16x3 (the packing of both clouds)
     Split s;
 };
 
 // Launch the partial kernel for kp = 16 * nc on P workgroups (nc <= 4: launch_partial_small, else
-// launch_partial_large; the two are separate objects built from sk_lse_partial.hip).
+// launch_partial_large; the two are separate objects built from sk_lse_partial.hip). kBF16x3 exists for
+// rows_role 0 only.
 hipError_t launch_partial_small(const PartialArgs& a, int nc, hipStream_t stream);
 hipError_t launch_partial_large(const PartialArgs& a, int nc, hipStream_t stream);
 inline hipError_t launch_partial(const PartialArgs& a, int nc, hipStream_t stream) {

@@ -9,18 +9,20 @@
 //
 //     a_ij = x_i . y_j + (gh_j + eps * log b_j) / 2           ("accumulator units")
 //
-// the score is c a_ij in log2 units. x_i . y_j is accumulated by bf16 MFMAs from an exact three-way bf16
-// split of the fp32 coordinates (sk_lse_partial.hip), bit-identical in the f and g updates; the column term
-// is added on the VALU. The running (max, sum) of a row is kept as
+// the score is c a_ij in log2 units. x_i . y_j is accumulated by fp16 MFMAs from a two-piece fp16 split of
+// the power-of-two scaled fp32 coordinates (sk_lse_partial.hip), bit-identical in the f and g updates; the
+// column term is added on the VALU. The running (max, sum) of a row is kept as
 //
 //     eps * lse_i = 2 M_i + eps ln(2) log2 S_i,   S_i = sum_j exp2(c (a_ij - M_i)),  M_i = max_j a_ij.
 //
-// Packed cloud layout. Points are padded to a multiple of 32 (one tile), coordinates to kp = 16 * nc, and
-// every coordinate v is stored as three bf16 pieces (v0 = bf16(v), v1 = bf16(v - v0), v2 = v - v0 - v1, all
-// exact). Within tile T, the 16-byte unit ((T * nc + c) * 3 + p) * 64 + 32 h + r holds piece p of coordinates
-// [16 c + 8 h, 16 c + 8 h + 8) of point 32 T + r: lane l = 32 h + r reads its v_mfma_f32_32x32x16_bf16
-// operand for K chunk c with one coalesced 16-byte load (a wave reads 1 KB contiguous). The same layout
-// serves a cloud as rows (one half-step) and as columns (the other). 6 kp bytes per point.
+// Packed cloud layout. A 256-byte header ([0] max |coordinate| as float bits, [1] the scale s, a power of
+// two with max |coordinate| * s in [2^13, 2^14)), then the tiles: points padded to a multiple of 32,
+// coordinates to kp = 16 * nc, every scaled coordinate v = s x stored as two fp16 pieces (v0 = fp16(v),
+// v1 = fp16(v - v0)). Within tile T, the 16-byte unit ((T * nc + c) * 2 + p) * 64 + 32 h + r holds piece p
+// of coordinates [16 c + 8 h, 16 c + 8 h + 8) of point 32 T + r: lane l = 32 h + r reads its
+// v_mfma_f32_32x32x16_f16 operand for K chunk c with one coalesced 16-byte load (a wave reads 1 KB
+// contiguous). The same layout serves a cloud as rows (one half-step) and as columns (the other).
+// 4 kp bytes per point.
 //
 // Work decomposition ("stream-K" over row groups x column tiles). A workgroup is 4 waves, one per SIMD;
 // wave w owns 2 row blocks of 32 rows of a row group (256 rows) and all 4 waves walk the same column tiles,
@@ -64,9 +66,73 @@ __device__ __forceinline__ float lg2(float x) { return __builtin_amdgcn_logf(x);
 // ---------------------------------------------------------------------------------------------------
 // Pack a row-major (n, d) cloud into the tile-interleaved layout.
 
-__global__ void pack_cloud_kernel(const float* __restrict__ src, int n, int d, int ld, bf16x8* __restrict__ dst,
+// Packing is three launches: clear the header, max |coordinate| (one atomic max per block on the float
+// bits, which order like the values for non-negative floats), then the pieces.
+__global__ void pack_header_kernel(unsigned* __restrict__ header) {
+    if (threadIdx.x == 0) {
+        header[0] = 0u;
+        header[1] = __float_as_uint(1.0f);
+    }
+}
+
+__global__ __launch_bounds__(256) void absmax_kernel(const float* __restrict__ src, int n, int d, int ld,
+                                                     unsigned* __restrict__ header) {
+    float mx = 0.0f;
+    const long long total = (long long)n * d;
+    for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (long long)gridDim.x * blockDim.x)
+        mx = fmaxf(mx, fabsf(src[(i / d) * ld + i % d]));
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    __shared__ float red[4];
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+        atomicMax(&header[0], __float_as_uint(mx));
+    }
+}
+
+// The power-of-two scale for a max |coordinate| m: m * s in [2^13, 2^14), clamped to [2^-32, 2^40] so that
+// s_x s_y and the scaled column terms stay well inside the fp32 range (m <= 7e13 < 2^46 keeps m s <= 2^14).
+__device__ __forceinline__ float pack_scale(float m) {
+    if (!(m > 0.0f)) return 1.0f;
+    int e;
+    frexpf(m, &e);                          // m in [2^(e-1), 2^e)
+    const int k = e > 46 ? -32 : (e < -26 ? 40 : 14 - e);
+    return ldexpf(1.0f, k);
+}
+
+__global__ void pack_cloud_kernel(const float* __restrict__ src, int n, int d, int ld, char* __restrict__ dst,
                                   int npad, int nc) {
-    // one thread per (tile, K chunk, lane): 8 coordinates, three pieces each
+    // one thread per (tile, K chunk, lane): 8 coordinates, two pieces each
+    const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long long total = (long long)(npad / SK_TILE) * nc * 64;
+    const float s = pack_scale(__uint_as_float(reinterpret_cast<const unsigned*>(dst)[0]));
+    if (idx == 0) reinterpret_cast<float*>(dst)[1] = s;
+    if (idx >= total) return;
+    const int lane = (int)(idx % 64);
+    const int cc = (int)((idx / 64) % nc);
+    const long long T = idx / (64 * nc);
+    const int r = lane & 31, h = lane >> 5;
+    const long long row = T * SK_TILE + r;
+    f16x8 p0, p1;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const int k = 16 * cc + 8 * h + e;
+        const float v = (row < n && k < d) ? src[row * ld + k] * s : 0.0f;   // exact: s is a power of two
+        const _Float16 a0 = (_Float16)v;
+        p0[e] = a0;
+        p1[e] = (_Float16)(v - (float)a0);       // v - a0 is exact in fp32
+    }
+    f16x8* o = reinterpret_cast<f16x8*>(dst + kHeaderBytes) + (T * nc + cc) * (2 * 64) + lane;
+    o[0] = p0;
+    o[64] = p1;
+}
+
+// The general row log-sum-exp's packing: three bf16 pieces per coordinate (exact), no scale (the header
+// keeps the scale 1 written by pack_header_kernel).
+__global__ void pack_cloud_bf3_kernel(const float* __restrict__ src, int n, int d, int ld, char* __restrict__ dst,
+                                      int npad, int nc) {
     const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     const long long total = (long long)(npad / SK_TILE) * nc * 64;
     if (idx >= total) return;
@@ -83,15 +149,19 @@ __global__ void pack_cloud_kernel(const float* __restrict__ src, int n, int d, i
         const __bf16 a0 = (__bf16)v;
         const float r1 = v - (float)a0;          // exact: v and a0 share the leading bits
         const __bf16 a1 = (__bf16)r1;
-        const __bf16 a2 = (__bf16)(r1 - (float)a1);
         p0[e] = a0;
         p1[e] = a1;
-        p2[e] = a2;
+        p2[e] = (__bf16)(r1 - (float)a1);        // exact: at most 8 significant bits remain
     }
-    bf16x8* o = dst + (T * nc + cc) * (kPieces * 64) + lane;
+    bf16x8* o = reinterpret_cast<bf16x8*>(dst + kHeaderBytes) + (T * nc + cc) * (3 * 64) + lane;
     o[0] = p0;
     o[64] = p1;
     o[128] = p2;
+}
+
+size_t packed_bf3_bytes(int n, int d) {
+    return (size_t)kHeaderBytes + (size_t)((n + SK_TILE - 1) / SK_TILE * SK_TILE) *
+                                      ((d + SK_KP_ALIGN - 1) / SK_KP_ALIGN * SK_KP_ALIGN) * 6;
 }
 
 __global__ void fill_mask_kernel(float* __restrict__ mask, int m, int mpad) {
@@ -348,9 +418,9 @@ int meas_count(int rows_pad) { return (rows_pad + kFinalBlock - 1) / kFinalBlock
 
 // One LSE pass (partial + finalisation) over packed rows and columns.
 struct Pass {
-    const bf16x8* xr;
+    const void* xr;
     int rows_pad;
-    const bf16x8* yc;
+    const void* yc;
     int m_pad;
     int kp;
     const float* u;
@@ -359,6 +429,7 @@ struct Pass {
     const int* skip;
     int mode;
     int rows_role;
+    int contraction;
     const float* xsq;
     const float* off;
     float* out;
@@ -382,6 +453,7 @@ hipError_t run_pass(const Pass& ps, const Plan& pl, hipStream_t st) {
     a.rows_pad = ps.rows_pad;
     a.mode = ps.mode;
     a.rows_role = ps.rows_role;
+    a.contraction = ps.contraction;
     a.s = pl.s;
     hipError_t e = launch_partial(a, pl.nc, st);
     if (e != hipSuccess) return e;
@@ -448,7 +520,7 @@ int check_cloud(const sk_cloud_f32& c, const char* name) {
 
 extern "C" {
 
-int sk_version(void) { return 200; }
+int sk_version(void) { return 300; }
 
 const char* sk_last_error(void) { return g_err; }
 
@@ -458,7 +530,7 @@ int sk_pad_dim(int d) { return d <= 0 ? 0 : (d + SK_KP_ALIGN - 1) / SK_KP_ALIGN 
 
 size_t sk_packed_bytes(int n, int d) {
     if (n < 1 || d < 1 || sk_pad_dim(d) > SK_KP_MAX) return 0;
-    return (size_t)sk_pad_points(n) * sk_pad_dim(d) * SK_PACKED_BYTES_PER_COORD;
+    return SK_PACKED_HEADER_BYTES + (size_t)sk_pad_points(n) * sk_pad_dim(d) * SK_PACKED_BYTES_PER_COORD;
 }
 
 int sk_pack_cloud_f32(const float* pts, int n, int d, int ld, void* out, void* stream) {
@@ -470,8 +542,13 @@ int sk_pack_cloud_f32(const float* pts, int n, int d, int ld, void* out, void* s
     const long long total = (long long)(npad / SK_TILE) * nc * 64;
     const int threads = 256;
     const long long blocks = (total + threads - 1) / threads;
-    hipLaunchKernelGGL(pack_cloud_kernel, dim3((unsigned)blocks), dim3(threads), 0, (hipStream_t)stream, pts, n, d,
-                       ld, (bf16x8*)out, npad, nc);
+    hipStream_t st = (hipStream_t)stream;
+    const long long elems = (long long)n * d;
+    const long long mblocks = std::min<long long>((elems + threads - 1) / threads, 1024);
+    hipLaunchKernelGGL(pack_header_kernel, dim3(1), dim3(64), 0, st, (unsigned*)out);
+    hipLaunchKernelGGL(absmax_kernel, dim3((unsigned)mblocks), dim3(threads), 0, st, pts, n, d, ld, (unsigned*)out);
+    hipLaunchKernelGGL(pack_cloud_kernel, dim3((unsigned)blocks), dim3(threads), 0, st, pts, n, d, ld, (char*)out,
+                       npad, nc);
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? SK_OK : hip_fail(e, "sk_pack_cloud_f32");
 }
@@ -480,7 +557,7 @@ size_t sk_row_lse_workspace_bytes(int rows, int m, int K) {
     if (rows < 1 || m < 1 || K < 1 || sk_pad_dim(K) > SK_KP_MAX) return 0;
     const int rp = sk_pad_points(rows), mp = sk_pad_points(m), kp = sk_pad_dim(K);
     const Plan pl = make_plan(rp, mp, kp);
-    return align_up(sk_packed_bytes(rows, K)) + align_up(sk_packed_bytes(m, K)) + align_up((size_t)mp * 4) +
+    return align_up(packed_bf3_bytes(rows, K)) + align_up(packed_bf3_bytes(m, K)) + align_up((size_t)mp * 4) +
            partial_bytes(pl, rp);
 }
 
@@ -496,16 +573,24 @@ int sk_row_lse_f32(const float* xa, const float* ya, float* lse, int rows, int m
     const int rp = sk_pad_points(rows), mp = sk_pad_points(m), kp = sk_pad_dim(K);
     const Plan pl = make_plan(rp, mp, kp);
     char* p = (char*)ws;
-    bf16x8* xpk = (bf16x8*)p;
-    p += align_up(sk_packed_bytes(rows, K));
-    bf16x8* ypk = (bf16x8*)p;
-    p += align_up(sk_packed_bytes(m, K));
+    void* xpk = p;
+    p += align_up(packed_bf3_bytes(rows, K));
+    void* ypk = p;
+    p += align_up(packed_bf3_bytes(m, K));
     float* mask = (float*)p;
     p += align_up((size_t)mp * 4);
     float2* part = (float2*)p;
     hipStream_t st = (hipStream_t)stream;
-    if (int r = sk_pack_cloud_f32(xa, rows, K, K, xpk, stream)) return r;
-    if (int r = sk_pack_cloud_f32(ya, m, K, K, ypk, stream)) return r;
+    {
+        const int nc = kp / 16;
+        const long long ux = (long long)(rp / SK_TILE) * nc * 64, uy = (long long)(mp / SK_TILE) * nc * 64;
+        hipLaunchKernelGGL(pack_header_kernel, dim3(1), dim3(64), 0, st, (unsigned*)xpk);
+        hipLaunchKernelGGL(pack_header_kernel, dim3(1), dim3(64), 0, st, (unsigned*)ypk);
+        hipLaunchKernelGGL(pack_cloud_bf3_kernel, dim3((unsigned)((ux + 255) / 256)), dim3(256), 0, st, xa, rows, K, K,
+                           (char*)xpk, rp, nc);
+        hipLaunchKernelGGL(pack_cloud_bf3_kernel, dim3((unsigned)((uy + 255) / 256)), dim3(256), 0, st, ya, m, K, K,
+                           (char*)ypk, mp, nc);
+    }
     hipLaunchKernelGGL(fill_mask_kernel, dim3((mp + 255) / 256), dim3(256), 0, st, mask, m, mp);
     Pass ps = {};
     ps.xr = xpk;
@@ -518,6 +603,7 @@ int sk_row_lse_f32(const float* xa, const float* ya, float* lse, int rows, int m
     ps.sc = mask;       // not read in this mode; a valid address all the same
     ps.mode = kPlainLse;
     ps.rows_role = 0;
+    ps.contraction = kBF16x3;
     ps.out = lse;
     ps.n_store = rows;
     ps.part = part;
@@ -553,9 +639,9 @@ int sk_half_step_f32(const void* x_pk, const float* xsq, const float* off, int r
     if (ws_bytes < need) return fail(SK_E_WORKSPACE, "sk_half_step_f32: workspace %zu < %zu bytes", ws_bytes, need);
     const Plan pl = make_plan(rows_pad, m_pad, sk_pad_dim(d));
     Pass ps = {};
-    ps.xr = (const bf16x8*)x_pk;
+    ps.xr = x_pk;
     ps.rows_pad = rows_pad;
-    ps.yc = (const bf16x8*)y_pk;
+    ps.yc = y_pk;
     ps.m_pad = m_pad;
     ps.kp = sk_pad_dim(d);
     ps.u = gh;
@@ -564,6 +650,7 @@ int sk_half_step_f32(const void* x_pk, const float* xsq, const float* off, int r
     ps.skip = skip;
     ps.mode = kHalfStep;
     ps.rows_role = rows_role;
+    ps.contraction = kF16x2;
     ps.xsq = xsq;
     ps.off = off;
     ps.out = fh;
@@ -617,9 +704,9 @@ int sk_loop_run_f32(const sk_loop_f32* L, int iters, void* stream) {
     hipStream_t hs = (hipStream_t)stream;
 
     Pass f = {};
-    f.xr = (const bf16x8*)L->x.pk;
+    f.xr = L->x.pk;
     f.rows_pad = L->x.npad;
-    f.yc = (const bf16x8*)L->y.pk;
+    f.yc = L->y.pk;
     f.m_pad = L->y.npad;
     f.kp = kp;
     f.u = L->gh;
@@ -628,6 +715,7 @@ int sk_loop_run_f32(const sk_loop_f32* L, int iters, void* stream) {
     f.skip = skip;
     f.mode = kHalfStep;
     f.rows_role = 0;
+    f.contraction = kF16x2;
     f.xsq = L->x.sq;
     f.off = L->x.off;
     f.out = L->fh;
@@ -635,9 +723,9 @@ int sk_loop_run_f32(const sk_loop_f32* L, int iters, void* stream) {
     f.part = part;
 
     Pass g = {};
-    g.xr = (const bf16x8*)L->y.pk;
+    g.xr = L->y.pk;
     g.rows_pad = L->y.npad;
-    g.yc = (const bf16x8*)L->x.pk;
+    g.yc = L->x.pk;
     g.m_pad = L->x.npad;
     g.kp = kp;
     g.u = L->fh;
@@ -646,6 +734,7 @@ int sk_loop_run_f32(const sk_loop_f32* L, int iters, void* stream) {
     g.skip = skip;
     g.mode = kHalfStep;
     g.rows_role = 1;
+    g.contraction = kF16x2;
     g.xsq = L->y.sq;
     g.off = L->y.off;
     g.out = L->gh;

@@ -4,27 +4,34 @@
 // IEEE mode would first be canonicalised one by one. No value here is NaN or infinite: padding and empty
 // rows use large finite sentinels.
 //
-// Contraction. Every fp32 coordinate v is stored as three bf16 pieces v = v0 + v1 + v2 (exact: 8 + 8 + 8
-// significand bits; sk_kernels.hip packs them). The dot product x.y is accumulated in fp32 by
-// v_mfma_f32_32x32x16_bf16 from the six leading cross products
+// Contraction. Every packed cloud carries a power-of-two scale s (max |coordinate| * s in [2^13, 2^14)),
+// and every scaled coordinate v = s x is stored as two fp16 pieces v = v0 + v1 (22 significand bits: within
+// 2^-23 of v, about one fp32 ulp; sk_kernels.hip packs them). The dot product of two scaled points is
+// accumulated in fp32 by v_mfma_f32_32x32x16_f16 from the four products
 //
-//     x0 y0, x0 y1, x1 y0, x0 y2, x1 y1, x2 y0        (each bf16 x bf16 product is exact in fp32),
+//     x0 y0, x0 y1, x1 y0, x1 y1                   (each fp16 x fp16 product is exact in fp32),
 //
-// whose dropped terms are below 2^-24 of |x||y|: the result is as accurate as an fp32 dot product. On gfx950
-// the bf16 matrix pipe runs at ~15x the fp32 MFMA rate and, unlike the fp32 MFMA, issues alongside VALU work
-// of the same SIMD, so the exp / max / sum epilogue of one tile hides under the MFMAs of the next.
+// which reproduces x.y as accurately as an fp32 dot product (measured error <= 2.1e-7 of sum |x_k y_k|, the
+// fp32 MFMA chain gives 3.2e-7). With sigma = s_x s_y, the kernel works in scaled accumulator units
+// sigma a = D + sigma (column term) and c / sigma, all exact power-of-two rescalings, and stores M / sigma.
+// On gfx950 the fp16 matrix pipe runs at ~15x the fp32 MFMA rate and, unlike the fp32 MFMA, issues alongside
+// VALU work of the same SIMD, so the exp / max / sum epilogue of one tile hides under the MFMAs of the next.
+// The general row log-sum-exp of arbitrary fp32 matrices (whose columns may mix magnitudes 1e9 apart, as the
+// augmented padding rows do) uses the exact three-way bf16 split instead: v = v0 + v1 + v2, six products
+// x0 y0, x0 y1, x1 y0, x0 y2, x1 y1, x2 y0 on v_mfma_f32_32x32x16_bf16, scale 1.
 //
 // Symmetry. The f update (rows x, columns y) and the g update (rows y, columns x) must form bit-identical
 // x_i . y_j: in the cold regime a row's log-sum-exp is one dominant score, and any rounding difference
 // between the directions would push f_i + g_j of that pair by the same amount every iteration (a linear
 // drift along the pair's neutral mode). The products are exact and the MFMA adds them in k order, so the two
-// directions agree when they issue the same (x piece, y piece) pairs in the same order: `rows_role` says
+// directions agree when they issue the same (x piece, y piece) pairs in the same order (sigma is the same
+// product of the two scales in both directions): `rows_role` says
 // whether the rows are the first or the second cloud, and the pair list is transposed accordingly. The
 // contraction starts from zero and the column term is added afterwards on the VALU; the max is subtracted
 // before scaling, exp2(c (a - M)), so the dominant term is exactly 1.
 //
 // Layout of one workgroup (4 waves, one per SIMD of a CU): wave w owns kRowBlocks blocks of 32 rows of a
-// row group (its bf16 pieces stay in registers for the whole work segment), and all four waves walk the same
+// row group (its fp16 pieces stay in registers for the whole work segment), and all four waves walk the same
 // column tiles. Two ways to feed the column tiles, chosen by size:
 //   - streamed (kp <= 64): every wave loads the tile's pieces straight into registers one tile ahead; the
 //     four waves of the CU read the same addresses at about the same time and share them through L1. The
@@ -124,25 +131,54 @@ struct Online {
     }
 };
 
-// The six products as (first-cloud piece, second-cloud piece).
-constexpr int kFirstPiece[6] = {0, 0, 1, 0, 1, 2};
-constexpr int kSecondPiece[6] = {0, 1, 0, 2, 1, 0};
+// The contractions: operand type, pieces per coordinate, the products as (first-cloud piece, second-cloud
+// piece) in issue order, and the MFMA.
+template <int CT>
+struct Contract;
 
-template <int NC, int ROLE>
+template <>
+struct Contract<kF16x2> {
+    using T = f16x8;
+    static constexpr int pieces = 2, products = 4;
+    static constexpr int first[4] = {0, 0, 1, 1};
+    static constexpr int second[4] = {0, 1, 0, 1};
+    static __device__ __forceinline__ f32x16 mfma(const T& a, const T& b, const f32x16& c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+    }
+};
+
+template <>
+struct Contract<kBF16x3> {
+    using T = bf16x8;
+    static constexpr int pieces = 3, products = 6;
+    static constexpr int first[6] = {0, 0, 1, 0, 1, 2};     // x0 y0, x0 y1, x1 y0, x0 y2, x1 y1, x2 y0
+    static constexpr int second[6] = {0, 1, 0, 2, 1, 0};
+    static __device__ __forceinline__ f32x16 mfma(const T& a, const T& b, const f32x16& c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+    }
+};
+
+template <int NC, int ROLE, int CT>
 struct Staged {
+    using C = Contract<CT>;
+    using T = typename C::T;
+    static constexpr int kPieces = C::pieces;
+    static constexpr int kProducts = C::products;
     static constexpr int RB = kRowBlocks;
     static constexpr int TILE16 = NC * kPieces * 64;   // 16-byte units per packed 32-point tile
     static constexpr int PER_THREAD = (TILE16 + kBlock - 1) / kBlock;
-    static constexpr int NS = 6 * NC * RB;             // MFMA slots per tile
+    static constexpr int NS = kProducts * NC * RB;     // MFMA slots per tile
 
     // Rows rb0 .. rb0 + RB - 1 against column tiles [tb, te); writes one (M, S) per row into `slot`.
     __device__ __forceinline__ static void run(const PartialArgs& a, int rb0, int tb, int te, int slot, float alpha,
-                                               float beta, float c, bf16x8* lds_y, float* lds_col) {
+                                               float beta, float c, float inv_sigma, T* lds_y, float* lds_col) {
         const int tid = threadIdx.x;
         const int lane = tid & 63;
         const int h = lane >> 5;
+        const T* xt = packed_tiles<T>(a.xr);
+        const T* yt = packed_tiles<T>(a.yc);
 
-        bf16x8 xv[RB][NC][kPieces];
+        T xv[RB][NC][kPieces];
 #pragma unroll
         for (int b = 0; b < RB; ++b) {
             const int blk = rb0 + b < a.nrb ? rb0 + b : a.nrb - 1;   // a missing block recomputes the last one
@@ -150,7 +186,7 @@ struct Staged {
             for (int cc = 0; cc < NC; ++cc)
 #pragma unroll
                 for (int p = 0; p < kPieces; ++p)
-                    xv[b][cc][p] = a.xr[(size_t)blk * TILE16 + (cc * kPieces + p) * 64 + lane];
+                    xv[b][cc][p] = xt[(size_t)blk * TILE16 + (cc * kPieces + p) * 64 + lane];
         }
         float M[RB], S[RB];
 #pragma unroll
@@ -163,15 +199,15 @@ struct Staged {
         // term of column j. Branch-free (clamped indices; threads mapped to the same element write the same
         // value), so that a whole tile is one basic block and the epilogue stays between the MFMAs.
         const int cj = tid & 31;
-        bf16x8 pf[PER_THREAD];
+        T pf[PER_THREAD];
         float pc = 0.0f;
         auto prefetch = [&](int t) {
 #pragma unroll
             for (int k = 0; k < PER_THREAD; ++k) {
                 const int idx = tid + k * kBlock < TILE16 ? tid + k * kBlock : TILE16 - 1;
-                pf[k] = a.yc[(size_t)t * TILE16 + idx];
+                pf[k] = yt[(size_t)t * TILE16 + idx];
             }
-            pc = fmaf(beta, a.v[t * 32 + cj], alpha * a.u[t * 32 + cj]);
+            pc = fmaxf(fmaf(beta, a.v[t * 32 + cj], alpha * a.u[t * 32 + cj]), kPadScore);
         };
         auto stage = [&](int buf) {
 #pragma unroll
@@ -181,7 +217,7 @@ struct Staged {
             }
             lds_col[buf * 32 + cj] = pc;
         };
-        bf16x8 yv[NC][kPieces];
+        T yv[NC][kPieces];
         auto read_tile = [&](int buf, f32x16& col) {
 #pragma unroll
             for (int cc = 0; cc < NC; ++cc)
@@ -204,10 +240,10 @@ struct Staged {
             for (int b = 0; b < RB; ++b) accN[b] = f32x16{};
             static_for<0, NS>([&](auto I) {
                 constexpr int i = decltype(I)::value;
-                constexpr int cc = i / (6 * RB), p = (i / RB) % 6, b = i % RB;
-                constexpr int rp = ROLE == 0 ? kFirstPiece[p] : kSecondPiece[p];
-                constexpr int cp = ROLE == 0 ? kSecondPiece[p] : kFirstPiece[p];
-                accN[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(yv[cc][cp], xv[b][cc][rp], accN[b], 0, 0, 0);
+                constexpr int cc = i / (kProducts * RB), p = (i / RB) % kProducts, b = i % RB;
+                constexpr int rp = ROLE == 0 ? C::first[p] : C::second[p];
+                constexpr int cp = ROLE == 0 ? C::second[p] : C::first[p];
+                accN[b] = C::mfma(yv[cc][cp], xv[b][cc][rp], accN[b]);
                 if (epi) {
                     constexpr int k0 = op_begin<RB>(i, NS), k1 = op_begin<RB>(i + 1, NS);
                     static_for<k0, k1>([&](auto K) { on.template step<decltype(K)::value>(accP, colP, M, S, c); });
@@ -260,7 +296,7 @@ struct Staged {
             const float Mn = fmaxf(M[b], Mo);
             const float Sn = S[b] * ex2(c * (M[b] - Mn)) + So * ex2(c * (Mo - Mn));
             if (h == 0 && rb0 + b < a.nrb)
-                a.part[(size_t)slot * a.rows_pad + (size_t)(rb0 + b) * 32 + lane] = make_float2(Mn, Sn);
+                a.part[(size_t)slot * a.rows_pad + (size_t)(rb0 + b) * 32 + lane] = make_float2(Mn * inv_sigma, Sn);
         }
     }
 };
@@ -269,19 +305,25 @@ struct Staged {
 constexpr int kColTiles = 256;
 constexpr int kStreamMaxChunks = 4;
 
-template <int NC, int ROLE>
+template <int NC, int ROLE, int CT>
 struct Streamed {
+    using C = Contract<CT>;
+    using T = typename C::T;
+    static constexpr int kPieces = C::pieces;
+    static constexpr int kProducts = C::products;
     static constexpr int RB = kRowBlocks;
     static constexpr int TILE16 = NC * kPieces * 64;
-    static constexpr int NS = 6 * NC * RB;
+    static constexpr int NS = kProducts * NC * RB;
 
     __device__ __forceinline__ static void run(const PartialArgs& a, int rb0, int tb, int te, int slot, float alpha,
-                                               float beta, float c, float* lds_col) {
+                                               float beta, float c, float inv_sigma, float* lds_col) {
         const int tid = threadIdx.x;
         const int lane = tid & 63;
         const int h = lane >> 5;
+        const T* xt = packed_tiles<T>(a.xr);
+        const T* yt = packed_tiles<T>(a.yc);
 
-        bf16x8 xv[RB][NC][kPieces];
+        T xv[RB][NC][kPieces];
 #pragma unroll
         for (int b = 0; b < RB; ++b) {
             const int blk = rb0 + b < a.nrb ? rb0 + b : a.nrb - 1;   // a missing block recomputes the last one
@@ -289,7 +331,7 @@ struct Streamed {
             for (int cc = 0; cc < NC; ++cc)
 #pragma unroll
                 for (int p = 0; p < kPieces; ++p)
-                    xv[b][cc][p] = a.xr[(size_t)blk * TILE16 + (cc * kPieces + p) * 64 + lane];
+                    xv[b][cc][p] = xt[(size_t)blk * TILE16 + (cc * kPieces + p) * 64 + lane];
         }
         float M[RB], S[RB];
 #pragma unroll
@@ -303,17 +345,17 @@ struct Streamed {
             __syncthreads();
             for (int k = tid; k < (t1 - t0) * 32; k += kBlock) {
                 const int j = t0 * 32 + k;
-                lds_col[k] = fmaf(beta, a.v[j], alpha * a.u[j]);
+                lds_col[k] = fmaxf(fmaf(beta, a.v[j], alpha * a.u[j]), kPadScore);
             }
             __syncthreads();
             cbase = t0;
         };
-        bf16x8 yA[NC][kPieces], yB[NC][kPieces];
-        auto load_y = [&](int t, bf16x8 (&yv)[NC][kPieces]) {
+        T yA[NC][kPieces], yB[NC][kPieces];
+        auto load_y = [&](int t, T (&yv)[NC][kPieces]) {
 #pragma unroll
             for (int cc = 0; cc < NC; ++cc)
 #pragma unroll
-                for (int p = 0; p < kPieces; ++p) yv[cc][p] = a.yc[(size_t)t * TILE16 + (cc * kPieces + p) * 64 + lane];
+                for (int p = 0; p < kPieces; ++p) yv[cc][p] = yt[(size_t)t * TILE16 + (cc * kPieces + p) * 64 + lane];
         };
         auto read_col = [&](int t, f32x16& col) {
 #pragma unroll
@@ -326,16 +368,16 @@ struct Streamed {
 
         f32x16 accA[RB], accB[RB], colA, colB;
         Online<RB> on;
-        auto tile = [&](f32x16 (&accN)[RB], f32x16 (&accP)[RB], const f32x16& colP, const bf16x8 (&yv)[NC][kPieces],
+        auto tile = [&](f32x16 (&accN)[RB], f32x16 (&accP)[RB], const f32x16& colP, const T (&yv)[NC][kPieces],
                         bool epi) {
 #pragma unroll
             for (int b = 0; b < RB; ++b) accN[b] = f32x16{};
             static_for<0, NS>([&](auto I) {
                 constexpr int i = decltype(I)::value;
-                constexpr int cc = i / (6 * RB), p = (i / RB) % 6, b = i % RB;
-                constexpr int rp = ROLE == 0 ? kFirstPiece[p] : kSecondPiece[p];
-                constexpr int cp = ROLE == 0 ? kSecondPiece[p] : kFirstPiece[p];
-                accN[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(yv[cc][cp], xv[b][cc][rp], accN[b], 0, 0, 0);
+                constexpr int cc = i / (kProducts * RB), p = (i / RB) % kProducts, b = i % RB;
+                constexpr int rp = ROLE == 0 ? C::first[p] : C::second[p];
+                constexpr int cp = ROLE == 0 ? C::second[p] : C::first[p];
+                accN[b] = C::mfma(yv[cc][cp], xv[b][cc][rp], accN[b]);
                 if (epi) {
                     constexpr int k0 = op_begin<RB>(i, NS), k1 = op_begin<RB>(i + 1, NS);
                     static_for<k0, k1>([&](auto K) { on.template step<decltype(K)::value>(accP, colP, M, S, c); });
@@ -389,19 +431,19 @@ struct Streamed {
             const float Mn = fmaxf(M[b], Mo);
             const float Sn = S[b] * ex2(c * (M[b] - Mn)) + So * ex2(c * (Mo - Mn));
             if (h == 0 && rb0 + b < a.nrb)
-                a.part[(size_t)slot * a.rows_pad + (size_t)(rb0 + b) * 32 + lane] = make_float2(Mn, Sn);
+                a.part[(size_t)slot * a.rows_pad + (size_t)(rb0 + b) * 32 + lane] = make_float2(Mn * inv_sigma, Sn);
         }
     }
 };
 
-template <int NC, int ROLE>
+template <int NC, int ROLE, int CT>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void lse_partial_kernel(PartialArgs a) {
     if (a.skip != nullptr && *a.skip != 0) return;
     constexpr bool kStream = NC <= kStreamMaxChunks;
-    constexpr int kLdsY = kStream ? 1 : 2 * NC * kPieces * 64;
+    constexpr int kLdsY = kStream ? 1 : 2 * NC * Contract<CT>::pieces * 64;
     constexpr int kLdsCol = kStream ? kColTiles * 32 : 64;
-    __shared__ bf16x8 lds_y[kLdsY];
+    __shared__ typename Contract<CT>::T lds_y[kLdsY];
     __shared__ __attribute__((aligned(16))) float lds_col[kLdsCol];
     const int wv = threadIdx.x >> 6;
     const int P = a.s.P;
@@ -409,7 +451,8 @@ void lse_partial_kernel(PartialArgs a) {
 
     // a_ij = x_i . y_j + alpha u_j + beta v_j in accumulator units, scores exp2(c (a - M)):
     // half-step: a = x . y + (gh + eps log b) / 2, c = (2 / eps) log2(e); plain row-LSE: a = xa . ya + mask,
-    // c = log2(e).
+    // c = log2(e). The kernel works in units scaled by sigma = s_rows s_cols (a power of two): alpha, beta
+    // times sigma, c divided by it.
     float alpha, beta, c;
     if (a.mode == kHalfStep) {
         alpha = 0.5f;
@@ -420,6 +463,11 @@ void lse_partial_kernel(PartialArgs a) {
         beta = 0.0f;
         c = kLog2e;
     }
+    const float sx = packed_scale(a.xr), sy = packed_scale(a.yc);   // 1 for kBF16x3
+    const float sigma = sx * sy, inv_sigma = (1.0f / sx) * (1.0f / sy);
+    alpha *= sigma;
+    beta *= sigma;
+    c *= inv_sigma;
 
     const long long u1 = (long long)(p + 1) * a.s.work / P;
     for (long long u = (long long)p * a.s.work / P; u < u1;) {
@@ -432,19 +480,23 @@ void lse_partial_kernel(PartialArgs a) {
         // in the workgroup's barriers.
         const int rb0 = (g * kWaves + wv) * kRowBlocks;
         if constexpr (kStream)
-            Streamed<NC, ROLE>::run(a, rb0, tb, te, slot, alpha, beta, c, lds_col);
+            Streamed<NC, ROLE, CT>::run(a, rb0, tb, te, slot, alpha, beta, c, inv_sigma, lds_col);
         else
-            Staged<NC, ROLE>::run(a, rb0, tb, te, slot, alpha, beta, c, lds_y, lds_col);
+            Staged<NC, ROLE, CT>::run(a, rb0, tb, te, slot, alpha, beta, c, inv_sigma, lds_y, lds_col);
         u += te - tb;
     }
 }
 
 template <int NC>
 hipError_t launch_nc(const PartialArgs& a, hipStream_t st) {
-    if (a.rows_role == 0)
-        hipLaunchKernelGGL((lse_partial_kernel<NC, 0>), dim3(a.s.P), dim3(kBlock), 0, st, a);
-    else
-        hipLaunchKernelGGL((lse_partial_kernel<NC, 1>), dim3(a.s.P), dim3(kBlock), 0, st, a);
+    if (a.contraction == kBF16x3) {
+        if (a.rows_role != 0) return hipErrorInvalidValue;
+        hipLaunchKernelGGL((lse_partial_kernel<NC, 0, kBF16x3>), dim3(a.s.P), dim3(kBlock), 0, st, a);
+    } else if (a.rows_role == 0) {
+        hipLaunchKernelGGL((lse_partial_kernel<NC, 0, kF16x2>), dim3(a.s.P), dim3(kBlock), 0, st, a);
+    } else {
+        hipLaunchKernelGGL((lse_partial_kernel<NC, 1, kF16x2>), dim3(a.s.P), dim3(kBlock), 0, st, a);
+    }
     return hipGetLastError();
 }
 

@@ -32,7 +32,9 @@ PAD_LOG_WEIGHT = -1e9                    # src/trnopt/sinkhorn.py:59
 TILE = 32                                 # SK_TILE
 KP_ALIGN = 16                             # SK_KP_ALIGN
 KP_MAX = 128                              # SK_KP_MAX
-PACKED_BYTES_PER_COORD = 6                # SK_PACKED_BYTES_PER_COORD: three bf16 pieces
+PACKED_BYTES_PER_COORD = 4                # SK_PACKED_BYTES_PER_COORD: two fp16 pieces
+PACKED_HEADER_BYTES = 256                 # SK_PACKED_HEADER_BYTES
+MAX_ABS_COORDINATE = 7.0e13               # larger coordinates do not fit the kernels' scaled fp16 pieces
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libtrnopt_hip.so"
 
 _c_float_p = ctypes.c_void_p             # device pointers travel as integers
@@ -163,12 +165,18 @@ def _workspace(nbytes: int, device) -> torch.Tensor:
 # Kernel-level entry points (the NKI module's make_row_lse_kernel / make_half_step_kernel)
 
 def packed_bytes(n: int, d: int) -> int:
-    return pad_points(n) * pad_dim(d) * PACKED_BYTES_PER_COORD
+    return PACKED_HEADER_BYTES + pad_points(n) * pad_dim(d) * PACKED_BYTES_PER_COORD
+
+
+def _check_range(name: str, max_abs: float) -> None:
+    if not np.isfinite(max_abs) or max_abs > MAX_ABS_COORDINATE:
+        raise ValueError(f"{name}: coordinates must be finite with |x| <= {MAX_ABS_COORDINATE:g} "
+                         f"(max |x| = {max_abs:g})")
 
 
 def pack_cloud(pts: torch.Tensor) -> torch.Tensor:
-    """(n, d) float32 device points -> the packed tile layout: each coordinate as three bf16 pieces, as bytes
-    (packed_bytes(n, d),)."""
+    """(n, d) float32 device points -> the packed layout as bytes (packed_bytes(n, d),): a header with the
+    cloud's power-of-two scale, then each scaled coordinate as two fp16 pieces."""
     _require_device_f32("pts", pts)
     if pts.dim() != 2:
         raise ValueError("pts must be (n, d)")
@@ -192,6 +200,9 @@ def row_lse(xa: torch.Tensor, ya: torch.Tensor) -> torch.Tensor:
         raise ValueError("xa (rows, K) and ya (m, K) must share K")
     rows, K = xa.shape
     m = ya.shape[0]
+    if rows and m:
+        _check_range("xa", float(xa.abs().max()))
+        _check_range("ya", float(ya.abs().max()))
     lb = lib()
     ws = _workspace(lb.sk_row_lse_workspace_bytes(rows, m, K), xa.device)
     out = torch.empty(rows, dtype=torch.float32, device=xa.device)
@@ -226,6 +237,7 @@ class HipCloud:
         f32 = dict(dtype=torch.float32, device=device)
         if role not in (0, 1):
             raise ValueError("role must be 0 (first cloud) or 1 (second cloud)")
+        _check_range("points", float(np.abs(pts).max()) if pts.size else 0.0)
         self.n, self.npad, self.d, self.device, self.role = n, npad, d, device, role
         self.sq = torch.as_tensor((P * P).sum(axis=1), dtype=torch.float32).to(device)
         self.log_w = torch.as_tensor(L, dtype=torch.float32).to(device)

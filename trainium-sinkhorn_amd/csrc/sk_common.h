@@ -1,9 +1,11 @@
 // Definitions shared by the two translation units of libtrnopt_hip.so: the MFMA partial kernel
 // (sk_lse_partial.hip, built without NaN semantics so row maxima need no canonicalisation) and the rest
-// (sk_kernels.hip: packing, finalisation, loop control, C ABI).
+// (sk_kernels.hip: packing, the merge pass and loop control of sk_epilogue.h, C ABI).
 #pragma once
 
 #include <hip/hip_runtime.h>
+
+#include "trnopt_hip.h"
 
 namespace sk {
 
@@ -18,6 +20,7 @@ constexpr float kEmpty = -1.0e30f;     // running max of a row before its first 
 constexpr int kWaves = 4;              // waves per workgroup of the partial kernel (one per SIMD)
 constexpr int kBlock = kWaves * 64;
 constexpr int kRowBlocks = 2;          // 32-row blocks per wave (independent MFMA accumulator chains)
+constexpr int kRowsPerGroup = 32 * kRowBlocks * kWaves;   // rows of a row group: one row per thread
 constexpr int kXcds = 8;
 constexpr int kMaxChunks = 8;          // K chunks of 16 coordinates: kp = 16 * nc <= 128
 // The contraction x.y on the matrix cores:
@@ -60,6 +63,15 @@ __host__ __device__ inline const T* packed_tiles(const void* pk) {
 }
 __device__ inline float packed_scale(const void* pk) { return reinterpret_cast<const float*>(pk)[1]; }
 
+// The on-device loop's configuration (src/trnopt/sinkhorn.py:313-320, 340-344).
+struct LoopCfg {
+    const double* sched;
+    const double* stages;
+    int n_sched, n_stages;
+    double eps, rho_x, rho_y, tol, stage_tol;
+    int max_iters, check_every, stage_max_iters, fixed_iters, balanced;
+};
+
 struct PartialArgs {
     const void* xr;     // packed rows (header, then two fp16 pieces per scaled coordinate)
     const void* yc;     // packed columns
@@ -74,6 +86,19 @@ struct PartialArgs {
     int rows_role;      // 0: the rows are the first cloud of the pair, 1: the second (piece order)
     int contraction;    // kF16x2 or kBF16x3 (the packing of both clouds)
     Split s;
+    // The merge pass (one workgroup per row group):
+    const float* xsq;   // |x|^2 (half-step epilogue)
+    const float* off;   // log(target / weight) or null
+    float* out;         // merged result (fh, or the plain row-LSE)
+    int n_store;        // rows of out written
+    float2* meas;       // per-group convergence partials (g update of the loop), or null
+    const float* w;     // row weights, with meas
+    int n_real;         // real rows, with meas
+    int* counters;      // with state: one arrival counter, zero on entry and left zero
+    int ngroups;
+    // ... and, in the last merge workgroup of a g update, the loop control (null: none).
+    sk_state* state;
+    LoopCfg cfg;
 };
 
 // Launch the partial kernel for kp = 16 * nc on P workgroups (nc <= 4: launch_partial_small, else

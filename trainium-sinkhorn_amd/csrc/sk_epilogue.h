@@ -1,0 +1,178 @@
+// Device code of the merge pass: the merge of a row group's partial (max, sum) slots with the half-step
+// epilogue, and the on-device loop control (src/trnopt/sinkhorn.py:346-378), which the merge pass of a g update
+// runs in its last workgroup. (The merge is a launch of its own: run inside the MFMA kernel, its device-scope
+// fences write back and invalidate each XCD's L2 under the tiles the other workgroups are streaming.)
+#pragma once
+
+#include "sk_common.h"
+
+namespace sk {
+
+constexpr float kDeltaCap = 50.0f;     // cap of (g_old - g_new) / eps in the balanced check (sinkhorn.py:60)
+
+__device__ __forceinline__ float ep_ex2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float ep_lg2(float x) { return __builtin_amdgcn_logf(x); }
+
+// eps of the iteration that starts with `it` iterations done (sinkhorn.py:347-350).
+__device__ inline double eps_for(const LoopCfg& c, int it, int stage) {
+    if (c.n_stages > 0) return stage < c.n_stages ? c.stages[stage] : c.eps;
+    return it < c.n_sched ? c.sched[it] : c.eps;
+}
+
+// The scalars of one eps, computed in double and rounded once, as consts() does (sinkhorn.py:323-334).
+__device__ inline void set_scalars(sk_state* st, double e, double rho_x, double rho_y) {
+    const double kx = rho_x > 0.0 ? rho_x / (rho_x + e) : 1.0;
+    const double ky = rho_y > 0.0 ? rho_y / (rho_y + e) : 1.0;
+    st->eps = e;
+    st->sc_x[0] = (float)(2.0 / e);
+    st->sc_x[1] = (float)(1.0 / e);
+    st->sc_x[2] = (float)e;
+    st->sc_x[3] = (float)kx;
+    st->sc_y[0] = (float)(2.0 / e);
+    st->sc_y[1] = (float)(1.0 / e);
+    st->sc_y[2] = (float)e;
+    st->sc_y[3] = (float)ky;
+}
+
+// Merge the slots of row i = 256 g + threadIdx.x (one row per thread of the workgroup) and apply the epilogue:
+//     lse = (2 / eps) M + ln S  (half-step, accumulator units) or M + ln S  (plain row-LSE)
+//     fh  = kappa ((|x|^2 + eps off) - eps lse) - |x|^2
+// With meas, also the group's convergence partials {max_{i<n_real} |new - old|, sum_i |w (exp(min((old -
+// new) / eps, 50)) - 1)|} (sinkhorn.py:360, 368-373), reduced in a fixed order into meas[g].
+__device__ inline void merge_group(const PartialArgs& a, int g) {
+    const int i = g * kRowsPerGroup + (int)threadIdx.x;
+    const float c = a.mode == kHalfStep ? a.sc[0] * kLog2e : kLog2e;
+    float dmax = 0.0f;
+    double derr = 0.0;
+    if (i < a.rows_pad) {
+        const int p0 = first_wg(g, a.s), p1 = last_wg(g, a.s);
+        const float2* pp = a.part + i;
+        // One pass, online: (M, S) <- (max(M, m_k), S 2^(c (M - M')) + s_k 2^(c (m_k - M'))), slots loaded eight
+        // at a time so that their latencies overlap.
+        float M = kEmpty, S = 0.0f;
+        for (int q = p0; q <= p1; q += 8) {
+            float2 v[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[k] = q + k <= p1 ? pp[(size_t)(q + k - p0) * a.rows_pad] : make_float2(kEmpty, 0.0f);
+            float Mn = M;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) Mn = fmaxf(Mn, v[k].x);
+            float Sn = S * ep_ex2(c * (M - Mn));
+#pragma unroll
+            for (int k = 0; k < 8; ++k) Sn += v[k].y * ep_ex2(c * (v[k].x - Mn));
+            M = Mn;
+            S = Sn;
+        }
+        // the max enters exactly, in accumulator units
+        const float l2s = ep_lg2(S);
+        if (a.mode == kHalfStep) {
+            const float eps = a.sc[2], kappa = a.sc[3];
+            const float x2 = a.xsq[i];
+            const float o = a.off != nullptr ? a.off[i] : 0.0f;
+            const float eps_lse = 2.0f * M + (eps * kLn2) * l2s;
+            const float val = kappa * ((x2 + eps * o) - eps_lse) - x2;
+            if (a.meas != nullptr) {
+                const float old = a.out[i];
+                if (i < a.n_real) dmax = fabsf(val - old);
+                const float delta = fminf((old - val) * a.sc[1], kDeltaCap);
+                derr = (double)fabsf(a.w[i] * (expf(delta) - 1.0f));
+            }
+            if (i < a.n_store) a.out[i] = val;
+        } else if (i < a.n_store) {
+            a.out[i] = M + kLn2 * l2s;
+        }
+    }
+    if (a.meas != nullptr) {
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            dmax = fmaxf(dmax, __shfl_xor(dmax, o));
+            derr += __shfl_xor(derr, o);
+        }
+        __shared__ float smax[kRowsPerGroup / 64];
+        __shared__ double ssum[kRowsPerGroup / 64];
+        const int wv = (int)threadIdx.x >> 6;
+        if ((threadIdx.x & 63) == 0) {
+            smax[wv] = dmax;
+            ssum[wv] = derr;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            float mx = smax[0];
+            double sm = ssum[0];
+            for (int k = 1; k < kRowsPerGroup / 64; ++k) {
+                mx = fmaxf(mx, smax[k]);
+                sm += ssum[k];
+            }
+            a.meas[g] = make_float2(mx, (float)sm);
+        }
+    }
+}
+
+// After the g update of one iteration, by one wave: the body of sinkhorn.py:356-378. Advances (it, stage,
+// stage_it), runs the balanced / unbalanced check at the reference's cadence, sets `done`, and writes the
+// next iteration's eps and {2/eps, 1/eps, eps, kappa}.
+__device__ inline void control_step(sk_state* st, const float2* meas, int nmeas, const LoopCfg& c) {
+    float mx = 0.0f;
+    double sm = 0.0;
+    for (int k = (int)threadIdx.x; k < nmeas; k += 64) {
+        const float2 v = meas[k];
+        mx = fmaxf(mx, v.x);
+        sm += (double)v.y;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        mx = fmaxf(mx, __shfl_xor(mx, o));
+        sm += __shfl_xor(sm, o);
+    }
+    if (threadIdx.x != 0) return;
+    const float inv_eps = st->sc_x[1];          // 1/eps of the iteration that just ran
+    const int it = st->it + 1;
+    int stage = st->stage;
+    int stage_it = st->stage_it + 1;
+    int conv = 0;
+    if (c.n_stages > 0 && stage < c.n_stages) {
+        // An intermediate stage: advance once the potentials settle or after stage_max_iters.
+        if (stage_it % c.check_every == 0) {
+            const double ch = (double)(mx * inv_eps);
+            if (ch < c.stage_tol || stage_it >= c.stage_max_iters) {
+                stage += 1;
+                stage_it = 0;
+            }
+        }
+    } else {
+        const bool check = c.fixed_iters == 0 && (c.n_stages > 0 || it > c.n_sched) &&
+                           (stage_it % c.check_every == 0 || it == c.max_iters);
+        if (check) {
+            const double err = c.balanced != 0 ? sm : (double)(mx * inv_eps);
+            st->err = err;
+            st->checks += 1;
+            if (err < c.tol) conv = 1;
+        }
+    }
+    const int done = (conv != 0 || it >= c.max_iters) ? 1 : 0;
+    st->it = it;
+    st->stage = stage;
+    st->stage_it = stage_it;
+    st->converged = conv;
+    if (done == 0) set_scalars(st, eps_for(c, it, stage), c.rho_x, c.rho_y);
+    st->done = done;
+}
+
+// The merge pass: one workgroup per row group. With a loop state (the g update of the on-device loop), the
+// last workgroup to finish runs the loop control; the counter is zero on entry and reset by that workgroup.
+__global__ __launch_bounds__(kRowsPerGroup) void merge_kernel(PartialArgs a) {
+    if (a.skip != nullptr && *a.skip != 0) return;
+    merge_group(a, (int)blockIdx.x);
+    if (a.state == nullptr) return;
+    __shared__ int s_last;
+    __threadfence();                       // release: this group's outputs and meas[g]
+    __syncthreads();
+    if (threadIdx.x == 0) s_last = atomicAdd(&a.counters[0], 1) == (int)gridDim.x - 1 ? 1 : 0;
+    __syncthreads();
+    if (s_last == 0) return;
+    __threadfence();                       // acquire: every group's meas
+    if (threadIdx.x < 64) control_step(a.state, a.meas, a.ngroups, a.cfg);
+    if (threadIdx.x == 0) a.counters[0] = 0;
+}
+
+}  // namespace sk

@@ -32,11 +32,13 @@
 // partial (M, S) per row into its own slot, and a finalisation pass merges the slots of every row and
 // applies the kappa / offset epilogue.
 //
-// The on-device loop (src/trnopt/sinkhorn.py:346-378) is three more tiny pieces: the g update's
-// finalisation also produces per-block convergence partials, and a one-wave control kernel advances
-// (it, stage, stage_it), runs the balanced / unbalanced checks at the reference's cadence, sets `done`,
-// and writes the next iteration's eps and {2/eps, 1/eps, eps, kappa} into the device state. Every loop
-// kernel returns immediately once `done` is set, so the host may enqueue whole batches of iterations.
+// A half-step is two launches: the partial kernel, then the merge kernel (sk_epilogue.h), one workgroup per
+// row group, which merges the group's slots and applies the epilogue. The on-device loop
+// (src/trnopt/sinkhorn.py:346-378) is four launches per iteration: in the g update the merge also produces
+// per-group convergence partials, and the last merge workgroup to finish advances (it, stage, stage_it), runs
+// the balanced / unbalanced checks at the reference's cadence, sets `done`, and writes the next iteration's
+// eps and {2/eps, 1/eps, eps, kappa} into the device state. Every loop kernel returns immediately once `done`
+// is set, so the host may enqueue whole batches of iterations.
 
 #include <hip/hip_runtime.h>
 
@@ -50,6 +52,7 @@
 #include <algorithm>
 
 #include "sk_common.h"
+#include "sk_epilogue.h"
 #include "trnopt_hip.h"
 
 namespace {
@@ -57,8 +60,6 @@ namespace {
 using namespace sk;
 
 constexpr float kMaskOut = -1.0e30f;   // column term of a padding column in the plain row-LSE mode
-constexpr float kDeltaCap = 50.0f;     // cap of (g_old - g_new) / eps in the balanced check (sinkhorn.py:60)
-constexpr int kFinalBlock = 256;
 
 __device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float lg2(float x) { return __builtin_amdgcn_logf(x); }
@@ -170,121 +171,10 @@ __global__ void fill_mask_kernel(float* __restrict__ mask, int m, int mpad) {
 }
 
 // ---------------------------------------------------------------------------------------------------
-// Finalisation: merge the partial slots of each row, then the epilogue.
-
-struct FinalArgs {
-    const float2* part;
-    int rows_pad;
-    int rows_per_group;   // 32 * RB * kWaves
-    Split s;
-    const float* sc;
-    const int* skip;
-    int mode;
-    const float* xsq;
-    const float* off;
-    float* out;
-    int n_store;          // rows written (the rest of rows_pad is computed and dropped)
-    float2* meas;         // per-block convergence partials, or null
-    const float* w;
-    int n_real;
-};
-
-__global__ __launch_bounds__(kFinalBlock) void lse_finalize_kernel(FinalArgs a) {
-    if (a.skip != nullptr && *a.skip != 0) return;
-    const int i = blockIdx.x * kFinalBlock + threadIdx.x;
-    const float c = a.mode == kHalfStep ? a.sc[0] * kLog2e : kLog2e;
-    float dmax = 0.0f;
-    double derr = 0.0;
-    if (i < a.rows_pad) {
-        const int g = i / a.rows_per_group;
-        const int p0 = first_wg(g, a.s), p1 = last_wg(g, a.s);
-        const float2* pp = a.part + i;
-        float M = kEmpty;
-        for (int p = p0; p <= p1; ++p) M = fmaxf(M, pp[(size_t)(p - p0) * a.rows_pad].x);
-        float S = 0.0f;
-        for (int p = p0; p <= p1; ++p) {
-            const float2 v = pp[(size_t)(p - p0) * a.rows_pad];
-            S += v.y * ex2(c * (v.x - M));
-        }
-        // lse = (2 / eps) M + ln S (half-step) or M + ln S (plain): the max enters exactly, in accumulator units
-        const float l2s = lg2(S);
-        if (a.mode == kHalfStep) {
-            const float eps = a.sc[2], kappa = a.sc[3];
-            const float x2 = a.xsq[i];
-            const float o = a.off != nullptr ? a.off[i] : 0.0f;
-            const float eps_lse = 2.0f * M + (eps * kLn2) * l2s;
-            const float val = kappa * ((x2 + eps * o) - eps_lse) - x2;
-            if (a.meas != nullptr) {
-                const float old = a.out[i];
-                if (i < a.n_real) dmax = fabsf(val - old);
-                const float delta = fminf((old - val) * a.sc[1], kDeltaCap);
-                derr = (double)fabsf(a.w[i] * (expf(delta) - 1.0f));
-            }
-            if (i < a.n_store) a.out[i] = val;
-        } else if (i < a.n_store) {
-            a.out[i] = M + kLn2 * l2s;
-        }
-    }
-    if (a.meas != nullptr) {
-        // Block reduction in a fixed order (deterministic for a given launch shape).
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            dmax = fmaxf(dmax, __shfl_xor(dmax, o));
-            derr += __shfl_xor(derr, o);
-        }
-        __shared__ float smax[kFinalBlock / 64];
-        __shared__ double ssum[kFinalBlock / 64];
-        const int wv = threadIdx.x >> 6;
-        if ((threadIdx.x & 63) == 0) {
-            smax[wv] = dmax;
-            ssum[wv] = derr;
-        }
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            float mx = smax[0];
-            double sm = ssum[0];
-            for (int k = 1; k < kFinalBlock / 64; ++k) {
-                mx = fmaxf(mx, smax[k]);
-                sm += ssum[k];
-            }
-            a.meas[blockIdx.x] = make_float2(mx, (float)sm);
-        }
-    }
-}
-
-// ---------------------------------------------------------------------------------------------------
 // On-device loop control.
 
-struct LoopCfg {
-    const double* sched;
-    const double* stages;
-    int n_sched, n_stages;
-    double eps, rho_x, rho_y, tol, stage_tol;
-    int max_iters, check_every, stage_max_iters, fixed_iters, balanced;
-};
-
-// eps of the iteration that starts with `it` iterations done (sinkhorn.py:347-350).
-__device__ double eps_for(const LoopCfg& c, int it, int stage) {
-    if (c.n_stages > 0) return stage < c.n_stages ? c.stages[stage] : c.eps;
-    return it < c.n_sched ? c.sched[it] : c.eps;
-}
-
-// The scalars of one eps, computed in double and rounded once, as consts() does (sinkhorn.py:323-334).
-__device__ void set_scalars(sk_state* st, double e, double rho_x, double rho_y) {
-    const double kx = rho_x > 0.0 ? rho_x / (rho_x + e) : 1.0;
-    const double ky = rho_y > 0.0 ? rho_y / (rho_y + e) : 1.0;
-    st->eps = e;
-    st->sc_x[0] = (float)(2.0 / e);
-    st->sc_x[1] = (float)(1.0 / e);
-    st->sc_x[2] = (float)e;
-    st->sc_x[3] = (float)kx;
-    st->sc_y[0] = (float)(2.0 / e);
-    st->sc_y[1] = (float)(1.0 / e);
-    st->sc_y[2] = (float)e;
-    st->sc_y[3] = (float)ky;
-}
-
-__global__ void loop_init_kernel(sk_state* st, LoopCfg c) {
+__global__ void loop_init_kernel(sk_state* st, LoopCfg c, int* __restrict__ counters, int ncounters) {
+    for (int k = threadIdx.x; k < ncounters; k += blockDim.x) counters[k] = 0;
     if (threadIdx.x != 0) return;
     st->it = 0;
     st->stage = 0;
@@ -294,56 +184,6 @@ __global__ void loop_init_kernel(sk_state* st, LoopCfg c) {
     st->checks = 0;
     st->err = __builtin_nan("");
     set_scalars(st, eps_for(c, 0, 0), c.rho_x, c.rho_y);
-}
-
-// After the g update of one iteration: the body of sinkhorn.py:356-378.
-__global__ __launch_bounds__(64) void loop_control_kernel(sk_state* st, const float2* __restrict__ meas,
-                                                          int nmeas, LoopCfg c) {
-    if (st->done != 0) return;
-    float mx = 0.0f;
-    double sm = 0.0;
-    for (int k = threadIdx.x; k < nmeas; k += 64) {
-        const float2 v = meas[k];
-        mx = fmaxf(mx, v.x);
-        sm += (double)v.y;
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        mx = fmaxf(mx, __shfl_xor(mx, o));
-        sm += __shfl_xor(sm, o);
-    }
-    if (threadIdx.x != 0) return;
-    const float inv_eps = st->sc_x[1];          // 1/eps of the iteration that just ran
-    const int it = st->it + 1;
-    int stage = st->stage;
-    int stage_it = st->stage_it + 1;
-    int conv = 0;
-    if (c.n_stages > 0 && stage < c.n_stages) {
-        // An intermediate stage: advance once the potentials settle or after stage_max_iters.
-        if (stage_it % c.check_every == 0) {
-            const double ch = (double)(mx * inv_eps);
-            if (ch < c.stage_tol || stage_it >= c.stage_max_iters) {
-                stage += 1;
-                stage_it = 0;
-            }
-        }
-    } else {
-        const bool check = c.fixed_iters == 0 && (c.n_stages > 0 || it > c.n_sched) &&
-                           (stage_it % c.check_every == 0 || it == c.max_iters);
-        if (check) {
-            const double err = c.balanced != 0 ? sm : (double)(mx * inv_eps);
-            st->err = err;
-            st->checks += 1;
-            if (err < c.tol) conv = 1;
-        }
-    }
-    const int done = (conv != 0 || it >= c.max_iters) ? 1 : 0;
-    st->it = it;
-    st->stage = stage;
-    st->stage_it = stage_it;
-    st->converged = conv;
-    if (done == 0) set_scalars(st, eps_for(c, it, stage), c.rho_x, c.rho_y);
-    st->done = done;
 }
 
 // ---------------------------------------------------------------------------------------------------
@@ -388,8 +228,6 @@ struct Plan {
     int slots;       // partial slots per row
 };
 
-constexpr int kRowsPerGroup = SK_TILE * kRowBlocks * kWaves;
-
 Plan make_plan(int rows_pad, int m_pad, int kp) {
     Plan pl;
     pl.nc = kp / 16;
@@ -414,9 +252,10 @@ size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
 
 size_t partial_bytes(const Plan& pl, int rows_pad) { return align_up((size_t)pl.slots * rows_pad * sizeof(float2)); }
 
-int meas_count(int rows_pad) { return (rows_pad + kFinalBlock - 1) / kFinalBlock; }
+// Row groups of rows_pad rows: the number of convergence partials.
+int meas_count(int rows_pad) { return (rows_pad + kRowsPerGroup - 1) / kRowsPerGroup; }
 
-// One LSE pass (partial + finalisation) over packed rows and columns.
+// One LSE pass over packed rows and columns: the partial kernel writes the slots, the merge kernel merges them.
 struct Pass {
     const void* xr;
     int rows_pad;
@@ -437,7 +276,10 @@ struct Pass {
     float2* meas;
     const float* w;
     int n_real;
-    float2* part;   // workspace
+    float2* part;   // workspace: partial slots
+    int* counters;  // with state: one arrival counter, zero on entry and left zero
+    sk_state* state;  // loop control after the merge (g update of the loop), or null
+    LoopCfg cfg;
 };
 
 hipError_t run_pass(const Pass& ps, const Plan& pl, hipStream_t st) {
@@ -455,24 +297,20 @@ hipError_t run_pass(const Pass& ps, const Plan& pl, hipStream_t st) {
     a.rows_role = ps.rows_role;
     a.contraction = ps.contraction;
     a.s = pl.s;
+    a.xsq = ps.xsq;
+    a.off = ps.off;
+    a.out = ps.out;
+    a.n_store = ps.n_store;
+    a.meas = ps.meas;
+    a.w = ps.w;
+    a.n_real = ps.n_real;
+    a.counters = ps.counters;
+    a.ngroups = pl.ngroups;
+    a.state = ps.state;
+    a.cfg = ps.cfg;
     hipError_t e = launch_partial(a, pl.nc, st);
     if (e != hipSuccess) return e;
-    FinalArgs f;
-    f.part = ps.part;
-    f.rows_pad = ps.rows_pad;
-    f.rows_per_group = kRowsPerGroup;
-    f.s = pl.s;
-    f.sc = ps.sc;
-    f.skip = ps.skip;
-    f.mode = ps.mode;
-    f.xsq = ps.xsq;
-    f.off = ps.off;
-    f.out = ps.out;
-    f.n_store = ps.n_store;
-    f.meas = ps.meas;
-    f.w = ps.w;
-    f.n_real = ps.n_real;
-    hipLaunchKernelGGL(lse_finalize_kernel, dim3(meas_count(ps.rows_pad)), dim3(kFinalBlock), 0, st, f);
+    hipLaunchKernelGGL(merge_kernel, dim3(pl.ngroups), dim3(kRowsPerGroup), 0, st, a);
     return hipGetLastError();
 }
 
@@ -607,7 +445,7 @@ int sk_row_lse_f32(const float* xa, const float* ya, float* lse, int rows, int m
     ps.out = lse;
     ps.n_store = rows;
     ps.part = part;
-    hipError_t e = run_pass(ps, pl, st);
+    const hipError_t e = run_pass(ps, pl, st);
     return e == hipSuccess ? SK_OK : hip_fail(e, "sk_row_lse_f32");
 }
 
@@ -637,6 +475,7 @@ int sk_half_step_f32(const void* x_pk, const float* xsq, const float* off, int r
         return fail(SK_E_ARG, "sk_half_step_f32: packed clouds, gh and log_b must be 16-byte aligned");
     const size_t need = sk_half_step_workspace_bytes(rows_pad, m_pad, d);
     if (ws_bytes < need) return fail(SK_E_WORKSPACE, "sk_half_step_f32: workspace %zu < %zu bytes", ws_bytes, need);
+    if (((uintptr_t)ws & 255) != 0) return fail(SK_E_ARG, "sk_half_step_f32: workspace must be 256-byte aligned");
     const Plan pl = make_plan(rows_pad, m_pad, sk_pad_dim(d));
     Pass ps = {};
     ps.xr = x_pk;
@@ -659,24 +498,57 @@ int sk_half_step_f32(const void* x_pk, const float* xsq, const float* off, int r
     ps.w = w;
     ps.n_real = n_real;
     ps.part = (float2*)ws;
-    hipError_t e = run_pass(ps, pl, (hipStream_t)stream);
+    const hipError_t e = run_pass(ps, pl, (hipStream_t)stream);
     return e == hipSuccess ? SK_OK : hip_fail(e, "sk_half_step_f32");
 }
 
 size_t sk_loop_workspace_bytes(int nx_pad, int ny_pad, int d) {
     if (nx_pad < SK_TILE || ny_pad < SK_TILE || d < 1 || sk_pad_dim(d) > SK_KP_MAX) return 0;
     const int kp = sk_pad_dim(d);
-    const size_t pf = partial_bytes(make_plan(nx_pad, ny_pad, kp), nx_pad);
-    const size_t pg = partial_bytes(make_plan(ny_pad, nx_pad, kp), ny_pad);
-    return std::max(pf, pg) + align_up((size_t)meas_count(ny_pad) * sizeof(float2));
+    const Plan pf = make_plan(nx_pad, ny_pad, kp), pg = make_plan(ny_pad, nx_pad, kp);
+    return std::max(partial_bytes(pf, nx_pad), partial_bytes(pg, ny_pad)) +
+           align_up((size_t)meas_count(ny_pad) * sizeof(float2)) + align_up(sizeof(int));
 }
 
+namespace {
+// The loop's workspace: partial slots (shared by the f and g updates), the g update's per-group convergence
+// partials, the arrival counter of the g update's merge (zeroed at init; every merge leaves it zero).
+struct LoopLayout {
+    Plan pf, pg;
+    float2* part;
+    float2* meas;
+    int* counters;
+    int ncounters;
+};
+
+LoopLayout loop_layout(const sk_loop_f32* L) {
+    LoopLayout o;
+    const int kp = sk_pad_dim(L->d);
+    o.pf = make_plan(L->x.npad, L->y.npad, kp);
+    o.pg = make_plan(L->y.npad, L->x.npad, kp);
+    const size_t part_sz = std::max(partial_bytes(o.pf, L->x.npad), partial_bytes(o.pg, L->y.npad));
+    o.part = (float2*)L->ws;
+    o.meas = (float2*)((char*)L->ws + part_sz);
+    o.counters = (int*)((char*)o.meas + align_up((size_t)meas_count(L->y.npad) * sizeof(float2)));
+    o.ncounters = 1;
+    return o;
+}
+}  // namespace
+
 int sk_loop_init_f32(const sk_loop_f32* L, void* stream) {
-    if (L == nullptr || L->state == nullptr) return fail(SK_E_ARG, "sk_loop_init_f32: null pointer");
+    if (L == nullptr || L->state == nullptr || L->ws == nullptr) return fail(SK_E_ARG, "sk_loop_init_f32: null pointer");
     if (L->n_sched > 0 && L->sched == nullptr) return fail(SK_E_ARG, "sk_loop_init_f32: n_sched without sched");
     if (L->n_stages > 0 && L->stages == nullptr) return fail(SK_E_ARG, "sk_loop_init_f32: n_stages without stages");
     if (!(L->eps > 0.0)) return fail(SK_E_ARG, "sk_loop_init_f32: eps must be > 0");
-    hipLaunchKernelGGL(loop_init_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, L->state, loop_cfg(L));
+    if (int r = check_cloud(L->x, "x")) return r;
+    if (int r = check_cloud(L->y, "y")) return r;
+    if (int r = check_kp(L->d)) return r;
+    const size_t need = sk_loop_workspace_bytes(L->x.npad, L->y.npad, L->d);
+    if (L->ws_bytes < need) return fail(SK_E_WORKSPACE, "sk_loop_init_f32: workspace %zu < %zu bytes", L->ws_bytes, need);
+    if (((uintptr_t)L->ws & 255) != 0) return fail(SK_E_ARG, "sk_loop_init_f32: workspace must be 256-byte aligned");
+    const LoopLayout lo = loop_layout(L);
+    hipLaunchKernelGGL(loop_init_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, L->state, loop_cfg(L),
+                       lo.counters, lo.ncounters);
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? SK_OK : hip_fail(e, "sk_loop_init_f32");
 }
@@ -692,12 +564,11 @@ int sk_loop_run_f32(const sk_loop_f32* L, int iters, void* stream) {
     if (L->ws_bytes < need) return fail(SK_E_WORKSPACE, "sk_loop_run_f32: workspace %zu < %zu bytes", L->ws_bytes, need);
     if (((uintptr_t)L->ws & 255) != 0) return fail(SK_E_ARG, "sk_loop_run_f32: workspace must be 256-byte aligned");
     const int kp = sk_pad_dim(L->d);
-    const Plan pf = make_plan(L->x.npad, L->y.npad, kp);
-    const Plan pg = make_plan(L->y.npad, L->x.npad, kp);
-    const size_t part_sz = std::max(partial_bytes(pf, L->x.npad), partial_bytes(pg, L->y.npad));
-    float2* part = (float2*)L->ws;
-    float2* meas = (float2*)((char*)L->ws + part_sz);
-    const int nmeas = meas_count(L->y.npad);
+    const LoopLayout lo = loop_layout(L);
+    const Plan& pf = lo.pf;
+    const Plan& pg = lo.pg;
+    float2* part = lo.part;
+    float2* meas = lo.meas;
     sk_state* st = L->state;
     const int* skip = &st->done;
     const LoopCfg cfg = loop_cfg(L);
@@ -743,14 +614,13 @@ int sk_loop_run_f32(const sk_loop_f32* L, int iters, void* stream) {
     g.w = L->y.w;
     g.n_real = L->y.n;
     g.part = part;
+    g.counters = lo.counters;
+    g.state = st;
+    g.cfg = cfg;
 
     for (int k = 0; k < iters; ++k) {
         hipError_t e = run_pass(f, pf, hs);
         if (e == hipSuccess) e = run_pass(g, pg, hs);
-        if (e == hipSuccess) {
-            hipLaunchKernelGGL(loop_control_kernel, dim3(1), dim3(64), 0, hs, st, meas, nmeas, cfg);
-            e = hipGetLastError();
-        }
         if (e != hipSuccess) return hip_fail(e, "sk_loop_run_f32");
     }
     return SK_OK;

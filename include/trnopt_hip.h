@@ -20,8 +20,8 @@
  *     SK_KP_ALIGN, every scaled coordinate s x split into two fp16 pieces (within 2^-23 of s x), in the
  *     tile-interleaved order that the fp16 MFMA kernels read with one coalesced 16-byte load per lane
  *     (sk_pack_cloud_f32 builds it from a row-major (n, d) fp32 array; sk_packed_bytes gives its size).
- *     The kernels form x.y from the four products of the pieces, accumulated in fp32: as accurate as an
- *     fp32 dot product, and bit-identical in the two directions of a pair of half-steps (rows_role 0
+ *     The kernels form x.y from three products of the pieces (x0 y0, x0 y1, x1 y0), accumulated in
+ *     fp32: at least as accurate as an fp32 dot product, and bit-identical in the two directions of a pair of half-steps (rows_role 0
  *     and 1) over the same two clouds. Coordinates must satisfy max |x| <= 7e13; the precision is that of
  *     fp32 for max |x| >= 2^-26 (1.5e-8) and degrades gracefully below.
  *   - Shifted potentials follow the reference (src/trnopt/sinkhorn.py:28-33): fh = f - |x|^2.

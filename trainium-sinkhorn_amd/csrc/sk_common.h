@@ -24,7 +24,7 @@ constexpr int kRowsPerGroup = 32 * kRowBlocks * kWaves;   // rows of a row group
 constexpr int kXcds = 8;
 constexpr int kMaxChunks = 8;          // K chunks of 16 coordinates: kp = 16 * nc <= 128
 // The contraction x.y on the matrix cores:
-//   kF16x2  -- the half-steps: the cloud's power-of-two scaled coordinates as two fp16 pieces, four products
+//   kF16x2  -- the half-steps: the cloud's power-of-two scaled coordinates as two fp16 pieces, three products
 //              (fp32 accuracy for coordinates within 2^26 of the cloud's largest; 4 bytes per coordinate);
 //   kBF16x3 -- the general row log-sum-exp of arbitrary fp32 matrices: each coordinate as three bf16 pieces
 //              (exact over the whole fp32 range), six products (6 bytes per coordinate).

@@ -7,12 +7,13 @@
 // Contraction. Every packed cloud carries a power-of-two scale s (max |coordinate| * s in [2^13, 2^14)),
 // and every scaled coordinate v = s x is stored as two fp16 pieces v = v0 + v1 (22 significand bits: within
 // 2^-23 of v, about one fp32 ulp; sk_kernels.hip packs them). The dot product of two scaled points is
-// accumulated in fp32 by v_mfma_f32_32x32x16_f16 from the four products
+// accumulated in fp32 by v_mfma_f32_32x32x16_f16 from the three products
 //
-//     x0 y0, x0 y1, x1 y0, x1 y1                   (each fp16 x fp16 product is exact in fp32),
+//     x0 y0, x0 y1, x1 y0                          (each fp16 x fp16 product is exact in fp32);
 //
-// which reproduces x.y as accurately as an fp32 dot product (measured error <= 2.1e-7 of sum |x_k y_k|, the
-// fp32 MFMA chain gives 3.2e-7). With sigma = s_x s_y, the kernel works in scaled accumulator units
+// the fourth, x1 y1, is at most 2^-22 |x_k y_k| and left out. This reproduces x.y at least as accurately as
+// an fp32 dot product (error ~1e-7 of sum |x_k y_k| on N(0, 1) data; a float32 dot product gives ~2.3e-7,
+// the fp32 MFMA chain 3.2e-7). With sigma = s_x s_y, the kernel works in scaled accumulator units
 // sigma a = D + sigma (column term) and c / sigma, all exact power-of-two rescalings, and stores M / sigma.
 // On gfx950 the fp16 matrix pipe runs at ~15x the fp32 MFMA rate and, unlike the fp32 MFMA, issues alongside
 // VALU work of the same SIMD, so the exp / max / sum epilogue of one tile hides under the MFMAs of the next.
@@ -59,6 +60,10 @@ namespace sk {
 namespace {
 
 __device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
+// exp2 of an exponent that is <= 0 up to the rounding of its offset, clamped to [0, 1] (the clamp bit of the
+// instruction): where a row's offset is a padding sentinel near -1e30 the rounding residual of fl(c m) is
+// itself huge, and exp2 of it must not reach infinity.
+__device__ __forceinline__ float ex2_unit(float x) { return __builtin_amdgcn_fmed3f(ex2(x), 0.0f, 1.0f); }
 
 // Hardware hands consecutive workgroup ids to the 8 XCDs in turn; renumber so that the workgroups of one
 // XCD own one contiguous range of the work.
@@ -78,14 +83,20 @@ __device__ __forceinline__ void static_for(F&& f) {
 }
 
 // The online log-sum-exp update of one row block and one tile, as kOps elementary steps:
-//   j in [0, 16):  a_r = acc_r + col_r
-//   j in [16, 24): running max over a pair of scores
-//   j in [24, 40): e_r = exp2(c (a_r - m)); s += e_(r-1)   (each exp is consumed one step later, so no
-//                  instruction waits on the transcendental unit)
-//   j == 40:       S = S exp2(c (M - m)) + s + e_15, M = m
-// Steps are spread over the MFMA slots of the next tile in proportion to their cost (an exp step ~7 VALU).
-constexpr int kOps = 41;
-constexpr int op_cost(int j) { return j < 24 ? 1 : 7; }
+//   j == 0:        the tile's 16 column terms of this lane from LDS (four 16-byte reads, shared by the row
+//                  blocks; costed high so that the adds land a few MFMA slots later, past the LDS latency)
+//   j in [1, 17):  a_r = acc_r + col_r
+//   j in [17, 25): running max over a pair of scores
+//   j in [25, 41): e_r = exp2(c a_r - cm) with cm = fl(c m); s += e_(r-1)   (each exp is consumed one step
+//                  later, so no instruction waits on the transcendental unit)
+//   j == 41:       S = S exp2(CM - cm) + s + e_15, M = m, CM = cm
+// The row state is (M, CM = fl(c M), S) with S relative to 2^CM: subtracting the rounded offset inside the
+// fma leaves exp2(c a - fl(c m)) = 2^(c m - fl(c m)) exp2(c (a - m)), a factor common to every term of the
+// row, so the log-sum-exp CM + log2 S is exact up to the rounding of c M itself (2^-24 relative, as if the
+// result were rounded to fp32 once).
+// Steps are spread over the MFMA slots of the next tile in proportion to their cost.
+constexpr int kOps = 42;
+constexpr int op_cost(int j) { return j == 0 ? 8 : j < 25 ? 1 : 4; }
 constexpr int block_cost() {
     int s = 0;
     for (int j = 0; j < kOps; ++j) s += op_cost(j);
@@ -103,30 +114,39 @@ constexpr int op_begin(int i, int NS) {
     return k;
 }
 
+// col4(q) returns the column terms of accumulators 4q .. 4q + 3 of the tile being updated.
 template <int RB>
 struct Online {
-    float m[RB], s[RB], pend[RB];
-    template <int k>
-    __device__ __forceinline__ void step(f32x16 (&acc)[RB], const f32x16& col, float (&M)[RB], float (&S)[RB],
-                                         float c) {
+    float m[RB], cm[RB], s[RB], pend[RB];
+    f32x4 cv[4];
+    template <int k, class ColFn>
+    __device__ __forceinline__ void step(f32x16 (&acc)[RB], ColFn&& col4, float (&M)[RB], float (&CM)[RB],
+                                         float (&S)[RB], float c) {
         constexpr int j = k / RB, b = k % RB;
-        if constexpr (j < 16) {
-            acc[b][j] = acc[b][j] + col[j];
-            if constexpr (j == 0) m[b] = M[b];
-        } else if constexpr (j < 24) {
-            constexpr int p = j - 16;
+        if constexpr (j == 0) {
+            if constexpr (b == 0)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) cv[q] = col4(q);
+            m[b] = M[b];
+        } else if constexpr (j < 17) {
+            constexpr int r = j - 1;
+            acc[b][r] = acc[b][r] + cv[r / 4][r % 4];
+        } else if constexpr (j < 25) {
+            constexpr int p = j - 17;
             m[b] = fmaxf(m[b], fmaxf(acc[b][2 * p], acc[b][2 * p + 1]));
-        } else if constexpr (j < 40) {
-            constexpr int r = j - 24;
-            const float e = ex2(c * (acc[b][r] - m[b]));
+        } else if constexpr (j < 41) {
+            constexpr int r = j - 25;
+            if constexpr (r == 0) cm[b] = c * m[b];
+            const float e = ex2_unit(fmaf(c, acc[b][r], -cm[b]));
             if constexpr (r == 0)
                 s[b] = 0.0f;
             else
                 s[b] += pend[b];
             pend[b] = e;
         } else {
-            S[b] = fmaf(S[b], ex2(c * (M[b] - m[b])), s[b] + pend[b]);
+            S[b] = fmaf(S[b], ex2(CM[b] - cm[b]), s[b] + pend[b]);
             M[b] = m[b];
+            CM[b] = cm[b];
         }
     }
 };
@@ -139,9 +159,9 @@ struct Contract;
 template <>
 struct Contract<kF16x2> {
     using T = f16x8;
-    static constexpr int pieces = 2, products = 4;
-    static constexpr int first[4] = {0, 0, 1, 1};
-    static constexpr int second[4] = {0, 1, 0, 1};
+    static constexpr int pieces = 2, products = 3;
+    static constexpr int first[3] = {0, 0, 1};               // x0 y0, x0 y1, x1 y0
+    static constexpr int second[3] = {0, 1, 0};
     static __device__ __forceinline__ f32x16 mfma(const T& a, const T& b, const f32x16& c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
     }
@@ -157,6 +177,24 @@ struct Contract<kBF16x3> {
         return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
     }
 };
+
+// End of a work segment: lanes l and l + 32 hold the same row over different columns; merge them and store
+// (M / sigma, S) of each row. fl(c M) is monotone in M, so the larger CM belongs to the larger M.
+template <int RB>
+__device__ __forceinline__ void store_rows(const PartialArgs& a, const float (&M)[RB], const float (&CM)[RB],
+                                           const float (&S)[RB], int rb0, int slot, float inv_sigma, int lane) {
+#pragma unroll
+    for (int b = 0; b < RB; ++b) {
+        const float Mo = __shfl_xor(M[b], 32);
+        const float CMo = __shfl_xor(CM[b], 32);
+        const float So = __shfl_xor(S[b], 32);
+        const float CMn = fmaxf(CM[b], CMo);
+        const float Sn = S[b] * ex2(CM[b] - CMn) + So * ex2(CMo - CMn);
+        if (lane < 32 && rb0 + b < a.nrb)
+            a.part[(size_t)slot * a.rows_pad + (size_t)(rb0 + b) * 32 + lane] =
+                make_float2(fmaxf(M[b], Mo) * inv_sigma, Sn);
+    }
+}
 
 template <int NC, int ROLE, int CT>
 struct Staged {
@@ -188,16 +226,19 @@ struct Staged {
                 for (int p = 0; p < kPieces; ++p)
                     xv[b][cc][p] = xt[(size_t)blk * TILE16 + (cc * kPieces + p) * 64 + lane];
         }
-        float M[RB], S[RB];
+        float M[RB], CM[RB], S[RB];
 #pragma unroll
         for (int b = 0; b < RB; ++b) {
             M[b] = kEmpty;
+            CM[b] = c * kEmpty;
             S[b] = 0.0f;
         }
 
         // Staging of one column tile: every thread loads PER_THREAD 16-byte units and thread j % 32 the column
         // term of column j. Branch-free (clamped indices; threads mapped to the same element write the same
-        // value), so that a whole tile is one basic block and the epilogue stays between the MFMAs.
+        // value), so that a whole tile is one basic block and the epilogue stays between the MFMAs. The
+        // operands are double buffered (read into registers before the tile's MFMAs); the column terms are
+        // triple buffered, since the update of tile t - 1 reads them while tile t + 1 is staged.
         const int cj = tid & 31;
         T pf[PER_THREAD];
         float pc = 0.0f;
@@ -209,33 +250,28 @@ struct Staged {
             }
             pc = fmaxf(fmaf(beta, a.v[t * 32 + cj], alpha * a.u[t * 32 + cj]), kPadScore);
         };
-        auto stage = [&](int buf) {
+        auto stage = [&](int buf, int cbuf) {
 #pragma unroll
             for (int k = 0; k < PER_THREAD; ++k) {
                 const int idx = tid + k * kBlock < TILE16 ? tid + k * kBlock : TILE16 - 1;
                 lds_y[buf * TILE16 + idx] = pf[k];
             }
-            lds_col[buf * 32 + cj] = pc;
+            lds_col[cbuf * 32 + cj] = pc;
         };
         T yv[NC][kPieces];
-        auto read_tile = [&](int buf, f32x16& col) {
+        auto read_tile = [&](int buf) {
 #pragma unroll
             for (int cc = 0; cc < NC; ++cc)
 #pragma unroll
                 for (int p = 0; p < kPieces; ++p) yv[cc][p] = lds_y[buf * TILE16 + (cc * kPieces + p) * 64 + lane];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const f32x4 cv = *reinterpret_cast<const f32x4*>(&lds_col[buf * 32 + 8 * q + 4 * h]);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) col[4 * q + e] = cv[e];
-            }
         };
 
-        f32x16 accA[RB], accB[RB], colA, colB;
+        f32x16 accA[RB], accB[RB];
         Online<RB> on;
-        // One tile: MFMAs into accN from zero; with `epi`, the update of the previous tile (accP, colP) is
-        // spread between them, one slot per MFMA, fenced so the compiler keeps the interleave.
-        auto tile = [&](f32x16 (&accN)[RB], f32x16 (&accP)[RB], const f32x16& colP, bool epi) {
+        // One tile: MFMAs into accN from zero; with `epi`, the update of the previous tile (accP, its column
+        // terms at colp) is spread between them, one slot per MFMA, fenced so the compiler keeps the interleave.
+        auto tile = [&](f32x16 (&accN)[RB], f32x16 (&accP)[RB], const float* colp, bool epi) {
+            auto col4 = [&](int q) { return *reinterpret_cast<const f32x4*>(colp + 8 * q); };
 #pragma unroll
             for (int b = 0; b < RB; ++b) accN[b] = f32x16{};
             static_for<0, NS>([&](auto I) {
@@ -246,58 +282,59 @@ struct Staged {
                 accN[b] = C::mfma(yv[cc][cp], xv[b][cc][rp], accN[b]);
                 if (epi) {
                     constexpr int k0 = op_begin<RB>(i, NS), k1 = op_begin<RB>(i + 1, NS);
-                    static_for<k0, k1>([&](auto K) { on.template step<decltype(K)::value>(accP, colP, M, S, c); });
+                    static_for<k0, k1>([&](auto K) { on.template step<decltype(K)::value>(accP, col4, M, CM, S, c); });
                 }
                 __builtin_amdgcn_sched_barrier(0);
             });
         };
-        auto update = [&](f32x16 (&accP)[RB], const f32x16& colP) {
-            static_for<0, RB * kOps>([&](auto K) { on.template step<decltype(K)::value>(accP, colP, M, S, c); });
+        auto update = [&](f32x16 (&accP)[RB], const float* colp) {
+            auto col4 = [&](int q) { return *reinterpret_cast<const f32x4*>(colp + 8 * q); };
+            static_for<0, RB * kOps>([&](auto K) { on.template step<decltype(K)::value>(accP, col4, M, CM, S, c); });
         };
+        auto colp_of = [&](int cbuf) { return lds_col + cbuf * 32 + 4 * h; };
 
-        // Tiles in pairs so the accumulator roles alternate without copies. Buffer (t - tb) & 1 holds tile t;
-        // every prefetch / stage is unconditional (after the last tile the last one is staged again).
+        // Tiles in pairs so the accumulator roles alternate without copies. Tile t sits in operand buffer
+        // (t - tb) & 1 and column buffer (t - tb) % 3; every prefetch / stage is unconditional (after the last
+        // tile the last one is staged again).
         const int last = te - 1;
         prefetch(tb);
-        stage(0);
+        stage(0, 0);
         __syncthreads();
         int t = tb;
-        read_tile(0, colA);
+        int cb = 0;                            // column buffer of tile t
+        read_tile(0);
         prefetch(t + 1 < te ? t + 1 : last);
-        tile(accA, accB, colB, false);
-        stage(1);
+        tile(accA, accB, nullptr, false);
+        stage(1, 1);
         __syncthreads();
         ++t;
         while (t < te) {
-            read_tile((t - tb) & 1, colB);
+            int cn = cb == 2 ? 0 : cb + 1;     // tile t
+            int cn2 = cn == 2 ? 0 : cn + 1;    // tile t + 1
+            read_tile((t - tb) & 1);
             prefetch(t + 1 < te ? t + 1 : last);
-            tile(accB, accA, colA, true);
-            stage((t + 1 - tb) & 1);
+            tile(accB, accA, colp_of(cb), true);
+            stage((t + 1 - tb) & 1, cn2);
             __syncthreads();
             ++t;
+            cb = cn;
             if (t >= te) {
-                update(accB, colB);
+                update(accB, colp_of(cb));
                 goto done;
             }
-            read_tile((t - tb) & 1, colA);
+            cn = cb == 2 ? 0 : cb + 1;
+            cn2 = cn == 2 ? 0 : cn + 1;
+            read_tile((t - tb) & 1);
             prefetch(t + 1 < te ? t + 1 : last);
-            tile(accA, accB, colB, true);
-            stage((t + 1 - tb) & 1);
+            tile(accA, accB, colp_of(cb), true);
+            stage((t + 1 - tb) & 1, cn2);
             __syncthreads();
             ++t;
+            cb = cn;
         }
-        update(accA, colA);
+        update(accA, colp_of(cb));
     done:
-        // Lanes l and l + 32 hold the same row over different columns: merge them, then store.
-#pragma unroll
-        for (int b = 0; b < RB; ++b) {
-            const float Mo = __shfl_xor(M[b], 32);
-            const float So = __shfl_xor(S[b], 32);
-            const float Mn = fmaxf(M[b], Mo);
-            const float Sn = S[b] * ex2(c * (M[b] - Mn)) + So * ex2(c * (Mo - Mn));
-            if (h == 0 && rb0 + b < a.nrb)
-                a.part[(size_t)slot * a.rows_pad + (size_t)(rb0 + b) * 32 + lane] = make_float2(Mn * inv_sigma, Sn);
-        }
+        store_rows(a, M, CM, S, rb0, slot, inv_sigma, lane);
     }
 };
 
@@ -333,22 +370,25 @@ struct Streamed {
                 for (int p = 0; p < kPieces; ++p)
                     xv[b][cc][p] = xt[(size_t)blk * TILE16 + (cc * kPieces + p) * 64 + lane];
         }
-        float M[RB], S[RB];
+        float M[RB], CM[RB], S[RB];
 #pragma unroll
         for (int b = 0; b < RB; ++b) {
             M[b] = kEmpty;
+            CM[b] = c * kEmpty;
             S[b] = 0.0f;
         }
 
-        int cbase = tb;
-        auto stage_cols = [&](int t0, int t1) {       // column terms of tiles [t0, t1) into LDS
+        // Column terms of tiles [t0 - 1, t1) into LDS (tile t at (t - cbase) * 32): the update of tile t0 - 1
+        // still runs while tile t0's MFMAs do.
+        int cbase = tb - 1;
+        auto stage_cols = [&](int t0, int t1) {
             __syncthreads();
-            for (int k = tid; k < (t1 - t0) * 32; k += kBlock) {
-                const int j = t0 * 32 + k;
-                lds_col[k] = fmaxf(fmaf(beta, a.v[j], alpha * a.u[j]), kPadScore);
+            for (int k = tid; k < (t1 - t0 + 1) * 32; k += kBlock) {
+                const int j = (t0 - 1) * 32 + k;
+                if (j >= 0) lds_col[k] = fmaxf(fmaf(beta, a.v[j], alpha * a.u[j]), kPadScore);
             }
             __syncthreads();
-            cbase = t0;
+            cbase = t0 - 1;
         };
         T yA[NC][kPieces], yB[NC][kPieces];
         auto load_y = [&](int t, T (&yv)[NC][kPieces]) {
@@ -357,19 +397,13 @@ struct Streamed {
 #pragma unroll
                 for (int p = 0; p < kPieces; ++p) yv[cc][p] = yt[(size_t)t * TILE16 + (cc * kPieces + p) * 64 + lane];
         };
-        auto read_col = [&](int t, f32x16& col) {
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const f32x4 cv = *reinterpret_cast<const f32x4*>(&lds_col[(t - cbase) * 32 + 8 * q + 4 * h]);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) col[4 * q + e] = cv[e];
-            }
-        };
+        auto colp_of = [&](int t) { return lds_col + (t - cbase) * 32 + 4 * h; };
 
-        f32x16 accA[RB], accB[RB], colA, colB;
+        f32x16 accA[RB], accB[RB];
         Online<RB> on;
-        auto tile = [&](f32x16 (&accN)[RB], f32x16 (&accP)[RB], const f32x16& colP, const T (&yv)[NC][kPieces],
+        auto tile = [&](f32x16 (&accN)[RB], f32x16 (&accP)[RB], const float* colp, const T (&yv)[NC][kPieces],
                         bool epi) {
+            auto col4 = [&](int q) { return *reinterpret_cast<const f32x4*>(colp + 8 * q); };
 #pragma unroll
             for (int b = 0; b < RB; ++b) accN[b] = f32x16{};
             static_for<0, NS>([&](auto I) {
@@ -380,13 +414,14 @@ struct Streamed {
                 accN[b] = C::mfma(yv[cc][cp], xv[b][cc][rp], accN[b]);
                 if (epi) {
                     constexpr int k0 = op_begin<RB>(i, NS), k1 = op_begin<RB>(i + 1, NS);
-                    static_for<k0, k1>([&](auto K) { on.template step<decltype(K)::value>(accP, colP, M, S, c); });
+                    static_for<k0, k1>([&](auto K) { on.template step<decltype(K)::value>(accP, col4, M, CM, S, c); });
                 }
                 __builtin_amdgcn_sched_barrier(0);
             });
         };
-        auto update = [&](f32x16 (&accP)[RB], const f32x16& colP) {
-            static_for<0, RB * kOps>([&](auto K) { on.template step<decltype(K)::value>(accP, colP, M, S, c); });
+        auto update = [&](f32x16 (&accP)[RB], const float* colp) {
+            auto col4 = [&](int q) { return *reinterpret_cast<const f32x4*>(colp + 8 * q); };
+            static_for<0, RB * kOps>([&](auto K) { on.template step<decltype(K)::value>(accP, col4, M, CM, S, c); });
         };
 
         // Tiles in pairs so the accumulator and operand buffers alternate without copies; the operand load of
@@ -396,43 +431,32 @@ struct Streamed {
         stage_cols(tb, cend);
         int t = tb;
         load_y(t, yA);
-        read_col(t, colA);
         load_y(t + 1 < te ? t + 1 : last, yB);
-        tile(accA, accB, colB, yA, false);
+        tile(accA, accB, nullptr, yA, false);
         ++t;
         while (t < te) {
             if (t >= cend) {
                 cend = t + kColTiles < te ? t + kColTiles : te;
                 stage_cols(t, cend);
             }
-            read_col(t, colB);
             load_y(t + 1 < te ? t + 1 : last, yA);
-            tile(accB, accA, colA, yB, true);
+            tile(accB, accA, colp_of(t - 1), yB, true);
             ++t;
             if (t >= te) {
-                update(accB, colB);
+                update(accB, colp_of(t - 1));
                 goto done;
             }
             if (t >= cend) {
                 cend = t + kColTiles < te ? t + kColTiles : te;
                 stage_cols(t, cend);
             }
-            read_col(t, colA);
             load_y(t + 1 < te ? t + 1 : last, yB);
-            tile(accA, accB, colB, yA, true);
+            tile(accA, accB, colp_of(t - 1), yA, true);
             ++t;
         }
-        update(accA, colA);
+        update(accA, colp_of(t - 1));
     done:
-#pragma unroll
-        for (int b = 0; b < RB; ++b) {
-            const float Mo = __shfl_xor(M[b], 32);
-            const float So = __shfl_xor(S[b], 32);
-            const float Mn = fmaxf(M[b], Mo);
-            const float Sn = S[b] * ex2(c * (M[b] - Mn)) + So * ex2(c * (Mo - Mn));
-            if (h == 0 && rb0 + b < a.nrb)
-                a.part[(size_t)slot * a.rows_pad + (size_t)(rb0 + b) * 32 + lane] = make_float2(Mn * inv_sigma, Sn);
-        }
+        store_rows(a, M, CM, S, rb0, slot, inv_sigma, lane);
     }
 };
 
@@ -442,7 +466,7 @@ void lse_partial_kernel(PartialArgs a) {
     if (a.skip != nullptr && *a.skip != 0) return;
     constexpr bool kStream = NC <= kStreamMaxChunks;
     constexpr int kLdsY = kStream ? 1 : 2 * NC * Contract<CT>::pieces * 64;
-    constexpr int kLdsCol = kStream ? kColTiles * 32 : 64;
+    constexpr int kLdsCol = kStream ? (kColTiles + 1) * 32 : 3 * 32;
     __shared__ typename Contract<CT>::T lds_y[kLdsY];
     __shared__ __attribute__((aligned(16))) float lds_col[kLdsCol];
     const int wv = threadIdx.x >> 6;

@@ -73,6 +73,21 @@ __device__ __forceinline__ int xcd_contiguous(int b, int P) {
     return xcd * q + (xcd < r ? xcd : r) + idx;
 }
 
+// max(a, b, c) as one v_max3_f32 (the compiler would pair the operands into a tree of two-operand maxima).
+// Its operands are always written by VALU instructions (the column-term adds), never directly by an MFMA.
+__device__ __forceinline__ float max3(float a, float b, float c) {
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+
+// A wave-uniform 64-bit value moved to scalar registers.
+__device__ __forceinline__ long long uniform64(long long v) {
+    const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)v);
+    const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)((unsigned long long)v >> 32));
+    return (long long)(((unsigned long long)hi << 32) | lo);
+}
+
 // Compile-time loop: f(integral_constant<int, i>) for i in [B, E).
 template <int B, int E, class F>
 __device__ __forceinline__ void static_for(F&& f) {
@@ -87,16 +102,18 @@ __device__ __forceinline__ void static_for(F&& f) {
 //                  blocks; costed high so that the adds land a few MFMA slots later, past the LDS latency)
 //   j in [1, 17):  a_r = acc_r + col_r
 //   j in [17, 25): running max over a pair of scores
-//   j in [25, 41): e_r = exp2(c a_r - cm) with cm = fl(c m); s += e_(r-1)   (each exp is consumed one step
-//                  later, so no instruction waits on the transcendental unit)
-//   j == 41:       S = S exp2(CM - cm) + s + e_15, M = m, CM = cm
+//   j == 25:       cm = fl(c m)
+//   j in [26, 42): acc_r = exp2(c a_r - cm), in place
+//   j in [42, 57): the sum of the 16 exponentials as a pairwise tree (8 + 4 + 2 + 1 adds), long after the
+//                  exponentials were issued, so no add waits on the transcendental unit
+//   j == 57:       S = S exp2(CM - cm) + sum, M = m, CM = cm
 // The row state is (M, CM = fl(c M), S) with S relative to 2^CM: subtracting the rounded offset inside the
 // fma leaves exp2(c a - fl(c m)) = 2^(c m - fl(c m)) exp2(c (a - m)), a factor common to every term of the
 // row, so the log-sum-exp CM + log2 S is exact up to the rounding of c M itself (2^-24 relative, as if the
 // result were rounded to fp32 once).
 // Steps are spread over the MFMA slots of the next tile in proportion to their cost.
-constexpr int kOps = 42;
-constexpr int op_cost(int j) { return j == 0 ? 8 : j < 25 ? 1 : 4; }
+constexpr int kOps = 58;
+constexpr int op_cost(int j) { return j == 0 ? 8 : (j >= 26 && j < 42) ? 3 : j == 57 ? 4 : 1; }
 constexpr int block_cost() {
     int s = 0;
     for (int j = 0; j < kOps; ++j) s += op_cost(j);
@@ -117,7 +134,7 @@ constexpr int op_begin(int i, int NS) {
 // col4(q) returns the column terms of accumulators 4q .. 4q + 3 of the tile being updated.
 template <int RB>
 struct Online {
-    float m[RB], cm[RB], s[RB], pend[RB];
+    float m[RB], cm[RB];
     f32x4 cv[4];
     template <int k, class ColFn>
     __device__ __forceinline__ void step(f32x16 (&acc)[RB], ColFn&& col4, float (&M)[RB], float (&CM)[RB],
@@ -133,18 +150,21 @@ struct Online {
             acc[b][r] = acc[b][r] + cv[r / 4][r % 4];
         } else if constexpr (j < 25) {
             constexpr int p = j - 17;
-            m[b] = fmaxf(m[b], fmaxf(acc[b][2 * p], acc[b][2 * p + 1]));
-        } else if constexpr (j < 41) {
-            constexpr int r = j - 25;
-            if constexpr (r == 0) cm[b] = c * m[b];
-            const float e = ex2_unit(fmaf(c, acc[b][r], -cm[b]));
-            if constexpr (r == 0)
-                s[b] = 0.0f;
-            else
-                s[b] += pend[b];
-            pend[b] = e;
+            m[b] = max3(m[b], acc[b][2 * p], acc[b][2 * p + 1]);
+        } else if constexpr (j == 25) {
+            cm[b] = c * m[b];
+        } else if constexpr (j < 42) {
+            constexpr int r = j - 26;
+            acc[b][r] = ex2_unit(fmaf(c, acc[b][r], -cm[b]));
+        } else if constexpr (j < 57) {
+            // tree level l (stride 2^l) pairs acc[2^(l+1) q] += acc[2^(l+1) q + 2^l]
+            constexpr int t = j - 42;
+            constexpr int l = t < 8 ? 0 : t < 12 ? 1 : t < 14 ? 2 : 3;
+            constexpr int q = t - (l == 0 ? 0 : l == 1 ? 8 : l == 2 ? 12 : 14);
+            constexpr int lo = q << (l + 1), hi = lo + (1 << l);
+            acc[b][lo] = acc[b][lo] + acc[b][hi];
         } else {
-            S[b] = fmaf(S[b], ex2(CM[b] - cm[b]), s[b] + pend[b]);
+            S[b] = fmaf(S[b], ex2(CM[b] - cm[b]), acc[b][0]);
             M[b] = m[b];
             CM[b] = cm[b];
         }
@@ -340,6 +360,7 @@ struct Staged {
 
 // Column terms computed into LDS once per run of kColTiles tiles (streamed variant).
 constexpr int kColTiles = 256;
+constexpr int kColBatch = 8;
 constexpr int kStreamMaxChunks = 4;
 
 template <int NC, int ROLE, int CT>
@@ -383,9 +404,23 @@ struct Streamed {
         int cbase = tb - 1;
         auto stage_cols = [&](int t0, int t1) {
             __syncthreads();
-            for (int k = tid; k < (t1 - t0 + 1) * 32; k += kBlock) {
-                const int j = (t0 - 1) * 32 + k;
-                if (j >= 0) lds_col[k] = fmaxf(fmaf(beta, a.v[j], alpha * a.u[j]), kPadScore);
+            const int n = (t1 - t0 + 1) * 32, base = (t0 - 1) * 32;
+            // Eight column terms per thread per batch, all sixteen loads in flight before the first use (a
+            // run of up to 256 tiles takes at most five batches, a typical segment one).
+            for (int k0 = 0; k0 < n; k0 += kColBatch * kBlock) {
+                float uu[kColBatch], vv[kColBatch];
+#pragma unroll
+                for (int q = 0; q < kColBatch; ++q) {
+                    const int k = k0 + q * kBlock + tid, j = base + k;
+                    const int jc = (k < n && j >= 0) ? j : 0;     // clamped in bounds; not stored
+                    uu[q] = a.u[jc];
+                    vv[q] = a.v[jc];
+                }
+#pragma unroll
+                for (int q = 0; q < kColBatch; ++q) {
+                    const int k = k0 + q * kBlock + tid, j = base + k;
+                    if (k < n && j >= 0) lds_col[k] = fmaxf(fmaf(beta, vv[q], alpha * uu[q]), kPadScore);
+                }
             }
             __syncthreads();
             cbase = t0 - 1;
@@ -427,11 +462,13 @@ struct Streamed {
         // Tiles in pairs so the accumulator and operand buffers alternate without copies; the operand load of
         // the tile after the last is the last tile again (in bounds, unused).
         const int last = te - 1;
+        // The first two operand tiles are requested before the column terms, so that the latencies of the row
+        // operands, the operands and the column terms overlap.
         int cend = tb + kColTiles < te ? tb + kColTiles : te;
-        stage_cols(tb, cend);
         int t = tb;
         load_y(t, yA);
         load_y(t + 1 < te ? t + 1 : last, yB);
+        stage_cols(tb, cend);
         tile(accA, accB, nullptr, yA, false);
         ++t;
         while (t < te) {
@@ -469,7 +506,7 @@ void lse_partial_kernel(PartialArgs a) {
     constexpr int kLdsCol = kStream ? (kColTiles + 1) * 32 : 3 * 32;
     __shared__ typename Contract<CT>::T lds_y[kLdsY];
     __shared__ __attribute__((aligned(16))) float lds_col[kLdsCol];
-    const int wv = threadIdx.x >> 6;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // one value per wave
     const int P = a.s.P;
     const int p = xcd_contiguous(blockIdx.x, P);
 
@@ -493,13 +530,16 @@ void lse_partial_kernel(PartialArgs a) {
     beta *= sigma;
     c *= inv_sigma;
 
-    const long long u1 = (long long)(p + 1) * a.s.work / P;
-    for (long long u = (long long)p * a.s.work / P; u < u1;) {
-        const int g = (int)(u / a.s.nt);
+    // The 64-bit divisions below expand to vector code; their results are the same in every lane, and
+    // readfirstlane hands them to the scalar unit, so the tile loop's counters and operand addresses stay in
+    // scalar registers.
+    const long long u1 = uniform64((long long)(p + 1) * a.s.work / P);
+    for (long long u = uniform64((long long)p * a.s.work / P); u < u1;) {
+        const int g = __builtin_amdgcn_readfirstlane((int)(u / a.s.nt));
         const int tb = (int)(u - (long long)g * a.s.nt);
         const long long left = u1 - u;
         const int te = left < (long long)(a.s.nt - tb) ? tb + (int)left : a.s.nt;
-        const int slot = p - first_wg(g, a.s);
+        const int slot = __builtin_amdgcn_readfirstlane(p - first_wg(g, a.s));
         // Waves past the last row block recompute it (their rows are not stored) so that every wave takes part
         // in the workgroup's barriers.
         const int rb0 = (g * kWaves + wv) * kRowBlocks;

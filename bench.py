@@ -1,18 +1,25 @@
 """Benchmark: ms per Sinkhorn iteration (f half-step + g half-step) on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-    python bench.py --profile [--reps R]     # for rocprofv3: R fused half-steps, then a 256 MiB copy
+    python bench.py --profile [--reps R]     # for rocprofv3: R half-steps, then a 256 MiB copy
 
 Workload: synthetic balanced 10,000 x 10,000, d = 64, fp32, x ~ N(0, 1) (seed 0), y ~ N(0, 1) + 0.5
 (seed 1), uniform weights, squared-Euclidean cost, no normalisation, eps = 0.1 (the reference's
 examples/sinkhorn_benchmark.py --flashsinkhorn setup). A "step" is one iteration of the on-device loop
-(fused f half-step, fused g half-step, loop control), inputs resident in HBM. W untimed iterations, then
+(f half-step, g half-step, loop control: four kernel launches), inputs resident in HBM. W untimed iterations, then
 exactly K timed iterations between two device synchronisations.
 
 Also reported on the same JSON line:
-* roofline -- the dominant kernel (the fused half-step, sk_half_step_f32 = MFMA partial pass + merge),
-  timed with HIP events on the stream it runs on: achieved fp32 MFMA FLOP/s on the algorithmic count
-  2 n m (d + 1) per half-step vs the 157.3 TFLOP/s peak;
+* roofline -- the dominant kernel pair, sk_half_step_f32 (lse_partial_kernel, then merge_kernel), timed with
+  HIP events on the stream it runs on. `achieved` is the algorithmic count 2 n m (d + 1) of one half-step
+  (the augmented fp32 contraction) per second, against the 157.3 TFLOP/s fp32 MFMA peak; `frac` exceeds 1
+  because the fp32-accurate contraction runs on the fp16 matrix pipe (three products of a two-piece split of
+  the coordinates). `mfma_f16` gives the executed fp16 MFMA work (3 x 2 x n_pad m_pad kp per half-step)
+  against the 2.5 PFLOP/s fp16 dense peak, `exp` the exponentials (n m per half-step) against the
+  9.83e12/s transcendental peak (quarter rate on 256 CUs x 4 SIMDs x 16 lanes at 2.4 GHz); `traffic` is the
+  fabric bytes per half-step from the committed counter summary;
+* iteration_roofline_frac -- max(4 n m (d + 1) / 157.3e12, 2 n m / 9.83e12) seconds over the measured
+  ms/iteration: the exp + fp32-MFMA roofline fraction the metric names;
 * cpu_baseline -- the reference's plain-PyTorch CPU path (the oracle's restatement, float32, block 2048,
   all host cores) on a bounded sample of the same workload;
 * end_to_end_s -- sinkhorn() wall time for 10 fixed iterations, host arrays in, float64 potentials out
@@ -33,11 +40,13 @@ sys.path.insert(0, str(ROOT / "trainium-sinkhorn_amd"))
 
 N, M, D, EPS = 10_000, 10_000, 64, 0.1
 MFMA_F32_PEAK = 157.3e12
+MFMA_F16_PEAK = 2.5e15
 EXP_PEAK = 9.83e12
+PRODUCTS = 3          # fp16 piece products per K chunk of the half-step contraction
 
 
 def profiled_traffic():
-    """Fabric bytes per fused half-step from the committed counter summary (FETCH_SIZE and WRITE_SIZE passes,
+    """Fabric bytes per half-step from the committed counter summary (FETCH_SIZE and WRITE_SIZE passes,
     scaled by the copy calibration), or None if the summary is absent."""
     import re
     p = ROOT / "profiles" / "half_step_10k_d64_counters.md"
@@ -78,7 +87,7 @@ def gpu_run(steps, warmup, kernel_reps=50):
     st = loop.read_state()
     assert st.it == warmup + steps and not st.done, (st.it, st.done)
 
-    # dominant kernel: the fused half-step (f update), HIP events on the current stream
+    # dominant kernel pair: one half-step (f update), HIP events on the current stream
     sc = hk.scalars(EPS, 1.0, dev)
     out = torch.empty(X.npad, dtype=torch.float32, device=dev)
     for _ in range(3):
@@ -93,6 +102,7 @@ def gpu_run(steps, warmup, kernel_reps=50):
     half_ms = ev0.elapsed_time(ev1) / kernel_reps
     flop = 2.0 * N * M * (D + 1)
     achieved = flop / (half_ms * 1e-3)
+    executed = PRODUCTS * 2.0 * X.npad * Y.npad * hk.pad_dim(D)
 
     # end to end: sinkhorn() with host arrays, 10 fixed iterations
     from trnopt import Backend, SinkhornOptions, sinkhorn
@@ -103,13 +113,14 @@ def gpu_run(steps, warmup, kernel_reps=50):
     te = time.perf_counter()
     r = sinkhorn(x, y, opts=o)
     e2e = time.perf_counter() - te
-    return dict(ms_per_it=ms_per_it, half_ms=half_ms, achieved=achieved, flop=flop, e2e=e2e, loop_s=r.seconds)
+    return dict(ms_per_it=ms_per_it, half_ms=half_ms, achieved=achieved, flop=flop, executed=executed, e2e=e2e,
+                loop_s=r.seconds)
 
 
 def profile_run(reps):
-    """What the rocprofv3 summaries are taken from: `reps` fused half-steps (f update) of the workload, then
-    one plain device copy of 256 MiB, whose FETCH_SIZE / WRITE_SIZE calibrate the counters (the copy reads and
-    writes exactly 262144 KiB)."""
+    """What the rocprofv3 summaries are taken from: `reps` half-steps (f update) of the workload, then one
+    plain device copy of 256 MiB (two copy dispatches of 128 MiB), whose FETCH_SIZE / WRITE_SIZE calibrate the
+    counters (each dispatch reads and writes exactly 131072 KiB)."""
     import numpy as np
     import torch
     from trnopt import hip_sinkhorn as hk
@@ -187,8 +198,13 @@ def main():
                    "d": D, "eps": EPS},
         "roofline": {"bound": "mfma", "achieved": round(g["achieved"] / 1e12, 3), "peak": MFMA_F32_PEAK / 1e12,
                      "unit": "TFLOP/s", "frac": round(g["achieved"] / MFMA_F32_PEAK, 4), "traffic": profiled_traffic(),
-                     "kernel": "fused half-step (MFMA partial pass + merge)", "kernel_ms": round(g["half_ms"], 5),
-                     "flop_per_launch": g["flop"]},
+                     "kernel": "sk_half_step_f32 (lse_partial_kernel + merge_kernel)",
+                     "kernel_ms": round(g["half_ms"], 5), "flop_per_launch": g["flop"],
+                     "mfma_f16": {"executed_flop_per_launch": g["executed"],
+                                  "achieved": round(g["executed"] / (g["half_ms"] * 1e-3) / 1e12, 1),
+                                  "peak": MFMA_F16_PEAK / 1e12,
+                                  "frac": round(g["executed"] / (g["half_ms"] * 1e-3) / MFMA_F16_PEAK, 4)},
+                     "exp": {"per_launch": N * M, "frac": round(N * M / (g["half_ms"] * 1e-3) / EXP_PEAK, 4)}},
         "iteration_roofline_frac": round(t_roof * 1e3 / g["ms_per_it"], 4),
         "end_to_end_s": round(g["e2e"], 4),
         "cpu_baseline": cpu,

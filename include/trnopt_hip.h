@@ -76,6 +76,7 @@ int sk_pack_cloud_f32(const float* pts, int n, int d, int ld, void* out, void* s
  * Replaces make_row_lse_kernel(K, rows, m)(xa_T, ya_T) (src/trnopt/nki_sinkhorn.py:150-172); unlike
  * the NKI kernel there is no constraint on rows or m and K may be up to SK_KP_MAX.
  */
+/* ws: sk_row_lse_workspace_bytes() bytes, 256-byte aligned. */
 size_t sk_row_lse_workspace_bytes(int rows, int m, int K);
 int sk_row_lse_f32(const float* xa, const float* ya, float* lse, int rows, int m, int K,
                    void* ws, size_t ws_bytes, void* stream);
@@ -96,11 +97,13 @@ int sk_row_lse_f32(const float* xa, const float* ya, float* lse, int rows, int m
  *   skip   device int or NULL: when *skip != 0 the call does nothing (the on-device loop's "done")
  *   fh     (rows_pad,) output; must not alias gh
  *   meas   NULL, or per-call convergence partials: then the previous contents of fh are the old
- *          potential, and meas receives per-block {max_{i<n_real} |fh_new - fh_old|,
+ *          potential, and meas receives, per group of 256 rows, {max_{i<n_real} |fh_new - fh_old|,
  *          sum_i |w_i (exp(min((fh_old - fh_new)/eps, 50)) - 1)|} (src/trnopt/sinkhorn.py:360, 368-373);
  *          w (rows_pad,) the row weights (padding 0) is then required. sk_half_step_meas_count()
  *          gives the number of float2 entries written.
- * rows_pad and m_pad must be multiples of SK_TILE.
+ *   ws     workspace of sk_half_step_workspace_bytes() bytes, 256-byte aligned
+ * rows_pad and m_pad must be multiples of SK_TILE. Two launches on `stream`: the MFMA partial pass, then
+ * the merge of the partial (max, sum) slots with the kappa / offset epilogue.
  */
 size_t sk_half_step_workspace_bytes(int rows_pad, int m_pad, int d);
 int sk_half_step_meas_count(int rows_pad);
@@ -162,7 +165,8 @@ typedef struct sk_loop_f32 {
 size_t sk_loop_workspace_bytes(int nx_pad, int ny_pad, int d);
 /* Write the initial state (it = 0, first eps and its scalars). */
 int sk_loop_init_f32(const sk_loop_f32* L, void* stream);
-/* Enqueue `iters` iterations (f update, g update, control); iterations after `done` do nothing. */
+/* Enqueue `iters` iterations (f update, g update with the loop control in its merge: four launches each);
+ * iterations after `done` do nothing. ws (sk_loop_workspace_bytes) must be 256-byte aligned. */
 int sk_loop_run_f32(const sk_loop_f32* L, int iters, void* stream);
 
 #ifdef __cplusplus

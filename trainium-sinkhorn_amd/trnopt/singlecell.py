@@ -11,6 +11,11 @@ The interface of the reference's src/trnopt/singlecell.py (wot, Schiebinger et a
 * growth_iters: re-solve with the row target set to the previous plan's row sums (wot's learned growth).
 
 wot's tmap is I * P, whose rows sum to the learned growth I * row_mass.
+
+save_pair / load_pair write and read the per-pair result file of the reference's pipeline
+(examples/singlecell_wot.py:112-117: f, g, eps, center, cost_scale, row_mass, col_mass, learned_growth,
+cells0, cells1, x0, x1), with the cell names stored as fixed-width strings so the file loads without pickle;
+pair_result turns a loaded file back into a SinkhornResult for trnopt.plan.
 """
 
 from __future__ import annotations
@@ -21,6 +26,9 @@ from dataclasses import dataclass, replace
 import numpy as np
 
 from .sinkhorn import SinkhornOptions, SinkhornResult, normalization, sinkhorn, transport_plan
+
+PAIR_KEYS = ("f", "g", "eps", "center", "cost_scale", "row_mass", "col_mass", "learned_growth", "cells0",
+             "cells1", "x0", "x1")
 
 
 def local_pca_coords(X0, X1, n_components: int = 30) -> tuple[np.ndarray, np.ndarray]:
@@ -80,3 +88,44 @@ def wot_tmap(x0, x1, tm: TransportMap) -> np.ndarray:
     """The dense map in wot's normalisation (I * P), small pairs only."""
     I, J = len(x0), len(x1)
     return I * transport_plan(x0, x1, tm.result, np.full(I, 1.0 / I), np.full(J, 1.0 / J))
+
+
+def save_pair(path, tm: TransportMap, x0: np.ndarray, x1: np.ndarray, cells0=None, cells1=None) -> None:
+    """Write one pair's result in the reference's format (examples/singlecell_wot.py:112-117). cells0 / cells1
+    default to the point indices; every array is numeric or a fixed-width string, so np.load needs no pickle."""
+    r = tm.result
+    I, J = len(x0), len(x1)
+    cells0 = np.arange(I) if cells0 is None else cells0
+    cells1 = np.arange(J) if cells1 is None else cells1
+    c0, c1 = np.asarray(cells0).astype(str), np.asarray(cells1).astype(str)
+    if c0.shape != (I,) or c1.shape != (J,):
+        raise ValueError("cells0 / cells1 must name every point of x0 / x1")
+    nan = lambda n: np.full(n, np.nan)                                            # noqa: E731
+    np.savez(path, f=np.asarray(r.f, np.float64), g=np.asarray(r.g, np.float64), eps=np.float64(r.eps),
+             center=np.asarray(r.center, np.float64), cost_scale=np.float64(r.cost_scale),
+             row_mass=nan(I) if r.row_mass is None else np.asarray(r.row_mass, np.float64),
+             col_mass=nan(J) if r.col_mass is None else np.asarray(r.col_mass, np.float64),
+             learned_growth=np.array(tm.learned_growth, dtype=np.float64), cells0=c0, cells1=c1,
+             x0=np.asarray(x0, np.float64), x1=np.asarray(x1, np.float64))
+
+
+def load_pair(path) -> dict:
+    """The arrays of a pair file (written by save_pair or by the reference's pipeline), scalars as floats.
+    Loads without pickle; a file whose cell names were stored as Python objects needs the reference's own
+    np.load(..., allow_pickle=True) instead and is refused here."""
+    with np.load(path, allow_pickle=False) as z:
+        missing = [k for k in PAIR_KEYS if k not in z.files]
+        if missing:
+            raise ValueError(f"{path}: not a pair file (missing {missing})")
+        out = {k: z[k] for k in PAIR_KEYS}
+    out["eps"], out["cost_scale"] = float(out["eps"]), float(out["cost_scale"])
+    return out
+
+
+def pair_result(z: dict) -> SinkhornResult:
+    """A SinkhornResult holding a loaded pair's potentials and normalisation (iterations etc. are unknown)."""
+    rm = None if np.all(np.isnan(z["row_mass"])) else z["row_mass"]
+    cm = None if np.all(np.isnan(z["col_mass"])) else z["col_mass"]
+    return SinkhornResult(f=z["f"], g=z["g"], iterations=0, error=float("nan"), converged=True, cost=float("nan"),
+                          seconds=0.0, eps=z["eps"], rho=None, center=z["center"], cost_scale=z["cost_scale"],
+                          row_mass=rm, col_mass=cm)

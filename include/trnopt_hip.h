@@ -169,6 +169,20 @@ int sk_loop_init_f32(const sk_loop_f32* L, void* stream);
  * iterations after `done` do nothing. ws (sk_loop_workspace_bytes) must be 256-byte aligned. */
 int sk_loop_run_f32(const sk_loop_f32* L, int iters, void* stream);
 
+/*
+ * Median of the squared-Euclidean cost over all pairs, the normalisation cost / median(cost) of
+ * normalization(how="median") (src/trnopt/sinkhorn.py:229-233), which the reference evaluates on the host
+ * over the materialised n x m float64 matrix:
+ *     median over i < n, j < m of max((|xc_i|^2 + |yc_j|^2) - 2 xc_i . yc_j, 0)   (float64),
+ * np.median's definition (mean of the two middle values when n m is even). xc (n, d), yc (m, d): row-major
+ * float64 device arrays, already centred; out: one device double. The cost is recomputed in each of six
+ * radix-select passes and never stored. n m < 2^32, d <= SK_MEDIAN_D_MAX; ws 256-byte aligned.
+ */
+#define SK_MEDIAN_D_MAX 128
+size_t sk_cost_median_workspace_bytes(int n, int m, int d);
+int sk_cost_median_f64(const double* xc, const double* yc, int n, int m, int d, double* out,
+                       void* ws, size_t ws_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -104,6 +104,10 @@ struct PartialArgs {
 // Launch the partial kernel for kp = 16 * nc on P workgroups (nc <= 4: launch_partial_small, else
 // launch_partial_large; the two are separate objects built from sk_lse_partial.hip). kBF16x3 exists for
 // rows_role 0 only.
+// Sets the message that sk_last_error() returns and passes `code` through.
+int fail(int code, const char* fmt, ...);
+int hip_fail(hipError_t e, const char* where);
+
 hipError_t launch_partial_small(const PartialArgs& a, int nc, hipStream_t stream);
 hipError_t launch_partial_large(const PartialArgs& a, int nc, hipStream_t stream);
 inline hipError_t launch_partial(const PartialArgs& a, int nc, hipStream_t stream) {

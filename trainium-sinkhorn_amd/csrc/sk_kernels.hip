@@ -55,6 +55,25 @@
 #include "sk_epilogue.h"
 #include "trnopt_hip.h"
 
+namespace sk {
+
+// Error reporting shared by the translation units (declared in sk_common.h).
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* where) {
+    return fail((int)e, "%s: %s", where, hipGetErrorString(e));
+}
+
+}  // namespace sk
+
 namespace {
 
 using namespace sk;
@@ -188,20 +207,6 @@ __global__ void loop_init_kernel(sk_state* st, LoopCfg c, int* __restrict__ coun
 
 // ---------------------------------------------------------------------------------------------------
 // Host side: errors, device facts, planning, dispatch.
-
-thread_local char g_err[512] = "";
-
-int fail(int code, const char* fmt, ...) {
-    va_list ap;
-    va_start(ap, fmt);
-    vsnprintf(g_err, sizeof(g_err), fmt, ap);
-    va_end(ap);
-    return code;
-}
-
-int hip_fail(hipError_t e, const char* where) {
-    return fail((int)e, "%s: %s", where, hipGetErrorString(e));
-}
 
 int cu_count() {
     static int cached[64] = {0};

@@ -1,0 +1,240 @@
+// Exact median of the squared-Euclidean cost over all pairs, on the GPU: the normalisation
+// "cost / median(cost)" of src/trnopt/sinkhorn.py:229-233 (wot's), which the reference computes on the host
+// by materialising the n x m float64 cost matrix (527 MB at 7,355 x 8,962) and calling np.median.
+//
+//     C_ij = max((|x_i|^2 + |y_j|^2) - 2 x_i . y_j, 0)        in float64, x and y already centred
+//     median = (C_(k0) + C_(k1)) / 2,   k0 = floor((N - 1) / 2), k1 = floor(N / 2),  N = n m
+//
+// (np.median's definition: the middle element for odd N, the mean of the two middle ones for even N.)
+//
+// Radix select on the fused cost stream: non-negative doubles order like their bit patterns, so the k-th
+// smallest cost is found digit by digit from the top (11, 11, 11, 11, 11, 9 bits). Each pass recomputes every
+// C_ij tile by tile (256 rows x 32 columns per step: the 32 column points in LDS, one row per thread, the
+// dot products in registers), keeps the pairs whose high bits equal the prefix found so far, and histograms
+// their next digit in LDS; a one-workgroup scan then picks the digit holding rank k and narrows the prefix.
+// The two ranks k0 and k1 share one histogram while their prefixes agree. Nothing is stored per pair: the
+// cost never reaches memory, and every launch goes on the caller's stream with no host round trip.
+
+#include <hip/hip_runtime.h>
+
+#include <stdint.h>
+
+#include "sk_common.h"
+
+namespace {
+
+using sk::fail;
+using sk::hip_fail;
+
+constexpr int kBins = 2048;                 // 11-bit digits
+constexpr int kRowsPerBlock = 256;          // one row per thread
+constexpr int kColTile = 32;                // column points per LDS tile
+constexpr int kColsPerBlock = 256;          // column points per workgroup (8 tiles)
+constexpr int kChunk = 32;                  // coordinates per register chunk of the row
+constexpr int kPasses = 6;
+constexpr int kShift[kPasses] = {53, 42, 31, 20, 9, 0};
+constexpr int kWidth[kPasses] = {11, 11, 11, 11, 11, 9};
+
+struct SelectState {
+    unsigned long long prefix[2];   // bits of the answer known so far (above the current digit)
+    unsigned long long k[2];        // rank still to find among the pairs that match the prefix
+    int same;                       // 1 while both ranks have the same prefix (one histogram serves both)
+    int pad;
+};
+
+__global__ void norms_kernel(const double* __restrict__ p, int n, int d, double* __restrict__ out) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const double* r = p + (size_t)i * d;
+    double s = 0.0;
+    for (int k = 0; k < d; ++k) s = fma(r[k], r[k], s);
+    out[i] = s;
+}
+
+__global__ void select_init_kernel(SelectState* st, unsigned* __restrict__ hist, unsigned long long N) {
+    for (int b = threadIdx.x; b < 2 * kBins; b += blockDim.x) hist[b] = 0u;
+    if (threadIdx.x == 0) {
+        st->prefix[0] = st->prefix[1] = 0ull;
+        st->k[0] = (N - 1ull) / 2ull;
+        st->k[1] = N / 2ull;
+        st->same = 1;
+    }
+}
+
+__device__ __forceinline__ unsigned long long cost_key(double c) {
+    // max(c, 0); -0.0 and +0.0 are the same cost and the same key
+    const unsigned long long b = (unsigned long long)__double_as_longlong(c > 0.0 ? c : 0.0);
+    return b & 0x7fffffffffffffffull;
+}
+
+// One digit pass over the workgroup's 256 x 256 block of pairs.
+__global__ __launch_bounds__(kRowsPerBlock) void select_pass_kernel(
+    const double* __restrict__ x, const double* __restrict__ y, const double* __restrict__ xx,
+    const double* __restrict__ yy, int n, int m, int d, const SelectState* __restrict__ st,
+    unsigned* __restrict__ hist, int shift, int width) {
+    __shared__ double ys[kColTile * 129];          // kColTile points, row stride d + 1 (d <= 128)
+    __shared__ unsigned h[2][kBins];
+    const int tid = threadIdx.x;
+    const int same = st->same;
+    const unsigned long long high = shift + width >= 64 ? 0ull : ~((1ull << (shift + width)) - 1ull);
+    const unsigned long long p0 = st->prefix[0] & high, p1 = st->prefix[1] & high;
+    const unsigned dmask = (1u << width) - 1u;
+    for (int b = tid; b < 2 * kBins; b += kRowsPerBlock) (&h[0][0])[b] = 0u;
+
+    const int i = blockIdx.x * kRowsPerBlock + tid;
+    const bool row_ok = i < n;
+    const double xi2 = row_ok ? xx[i] : 0.0;
+    const double* xr = x + (size_t)(row_ok ? i : 0) * d;
+    const int ld = d + 1;
+    const int j_begin = blockIdx.y * kColsPerBlock;
+    const int j_end = j_begin + kColsPerBlock < m ? j_begin + kColsPerBlock : m;
+
+    for (int j0 = j_begin; j0 < j_end; j0 += kColTile) {
+        const int nj = j_end - j0 < kColTile ? j_end - j0 : kColTile;
+        __syncthreads();                           // previous tile's reads (and the histogram clear) done
+        for (int e = tid; e < nj * d; e += kRowsPerBlock) {
+            const int jj = e / d, kk = e - jj * d;
+            ys[jj * ld + kk] = y[(size_t)(j0 + jj) * d + kk];
+        }
+        __syncthreads();
+        double acc[kColTile];
+#pragma unroll
+        for (int jj = 0; jj < kColTile; ++jj) acc[jj] = 0.0;
+        for (int k0 = 0; k0 < d; k0 += kChunk) {
+            const int kn = d - k0 < kChunk ? d - k0 : kChunk;
+            double xv[kChunk];
+#pragma unroll
+            for (int kk = 0; kk < kChunk; ++kk) xv[kk] = kk < kn ? xr[k0 + kk] : 0.0;
+#pragma unroll
+            for (int jj = 0; jj < kColTile; ++jj) {
+                const double* yr = ys + jj * ld + k0;
+                double a = acc[jj];
+#pragma unroll
+                for (int kk = 0; kk < kChunk; ++kk)
+                    if (kk < kn) a = fma(xv[kk], yr[kk], a);
+                acc[jj] = a;
+            }
+        }
+        if (row_ok) {
+#pragma unroll
+            for (int jj = 0; jj < kColTile; ++jj) {
+                if (jj < nj) {
+                    const double c = (xi2 + yy[j0 + jj]) - 2.0 * acc[jj];
+                    const unsigned long long key = cost_key(c);
+                    const unsigned digit = (unsigned)(key >> shift) & dmask;
+                    if ((key & high) == p0) atomicAdd(&h[0][digit], 1u);
+                    if (!same && (key & high) == p1) atomicAdd(&h[1][digit], 1u);
+                }
+            }
+        }
+    }
+    __syncthreads();
+    for (int b = tid; b < 2 * kBins; b += kRowsPerBlock) {
+        const unsigned v = (&h[0][0])[b];
+        if (v != 0u) atomicAdd(&hist[b], v);
+    }
+}
+
+// Pick, for each rank, the digit whose bin holds it; narrow the prefix and the rank; clear the histograms.
+__global__ __launch_bounds__(1024) void select_scan_kernel(SelectState* st, unsigned* __restrict__ hist, int shift,
+                                                           int width) {
+    __shared__ unsigned long long part[1024];
+    __shared__ int pick[2];
+    __shared__ unsigned long long below[2];
+    const int tid = threadIdx.x;
+    const int bins = 1 << width;
+    const int same = st->same;
+    for (int s = 0; s < 2; ++s) {
+        const unsigned* hs = hist + (same ? 0 : s) * kBins;
+        // two bins per thread, then an inclusive scan over the threads (Hillis-Steele)
+        const unsigned long long c0 = 2 * tid < bins ? hs[2 * tid] : 0ull;
+        const unsigned long long c1 = 2 * tid + 1 < bins ? hs[2 * tid + 1] : 0ull;
+        part[tid] = c0 + c1;
+        __syncthreads();
+        for (int off = 1; off < 1024; off <<= 1) {
+            const unsigned long long v = tid >= off ? part[tid - off] : 0ull;
+            __syncthreads();
+            part[tid] += v;
+            __syncthreads();
+        }
+        const unsigned long long k = st->k[s];
+        const unsigned long long before = tid > 0 ? part[tid - 1] : 0ull;
+        if (tid == 0) {
+            pick[s] = 0;
+            below[s] = 0ull;
+        }
+        __syncthreads();
+        if (k >= before && k < before + c0) {
+            pick[s] = 2 * tid;
+            below[s] = before;
+        } else if (k >= before + c0 && k < before + c0 + c1) {
+            pick[s] = 2 * tid + 1;
+            below[s] = before + c0;
+        }
+        __syncthreads();
+    }
+    if (tid == 0) {
+        for (int s = 0; s < 2; ++s) {
+            st->prefix[s] |= (unsigned long long)pick[s] << shift;
+            st->k[s] -= below[s];
+        }
+        st->same = (same && pick[0] == pick[1]) ? 1 : 0;
+    }
+    for (int b = tid; b < 2 * kBins; b += 1024) hist[b] = 0u;
+}
+
+__global__ void select_finish_kernel(const SelectState* st, double* out) {
+    if (threadIdx.x != 0) return;
+    const double a = __longlong_as_double((long long)st->prefix[0]);
+    const double b = __longlong_as_double((long long)st->prefix[1]);
+    *out = (a + b) * 0.5;
+}
+
+size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+}  // namespace
+
+extern "C" {
+
+size_t sk_cost_median_workspace_bytes(int n, int m, int d) {
+    if (n < 1 || m < 1 || d < 1 || d > SK_MEDIAN_D_MAX) return 0;
+    return align256(sizeof(SelectState)) + align256(2 * kBins * sizeof(unsigned)) + align256((size_t)n * 8) +
+           align256((size_t)m * 8);
+}
+
+int sk_cost_median_f64(const double* xc, const double* yc, int n, int m, int d, double* out, void* ws,
+                       size_t ws_bytes, void* stream) {
+    if (xc == nullptr || yc == nullptr || out == nullptr || ws == nullptr)
+        return fail(SK_E_ARG, "sk_cost_median_f64: null pointer");
+    if (n < 1 || m < 1 || d < 1 || d > SK_MEDIAN_D_MAX)
+        return fail(SK_E_SHAPE, "sk_cost_median_f64: need n, m >= 1 and 1 <= d <= SK_MEDIAN_D_MAX");
+    if ((unsigned long long)n * (unsigned long long)m > 0xffffffffull)
+        return fail(SK_E_SHAPE, "sk_cost_median_f64: n * m must be below 2^32");
+    if (ws_bytes < sk_cost_median_workspace_bytes(n, m, d))
+        return fail(SK_E_WORKSPACE, "sk_cost_median_f64: workspace too small");
+    if (((uintptr_t)ws & 255) != 0) return fail(SK_E_ARG, "sk_cost_median_f64: workspace must be 256-byte aligned");
+    char* p = (char*)ws;
+    SelectState* st = (SelectState*)p;
+    p += align256(sizeof(SelectState));
+    unsigned* hist = (unsigned*)p;
+    p += align256(2 * kBins * sizeof(unsigned));
+    double* xx = (double*)p;
+    p += align256((size_t)n * 8);
+    double* yy = (double*)p;
+    hipStream_t s = (hipStream_t)stream;
+    hipLaunchKernelGGL(norms_kernel, dim3((n + 255) / 256), dim3(256), 0, s, xc, n, d, xx);
+    hipLaunchKernelGGL(norms_kernel, dim3((m + 255) / 256), dim3(256), 0, s, yc, m, d, yy);
+    hipLaunchKernelGGL(select_init_kernel, dim3(1), dim3(1024), 0, s, st, hist,
+                       (unsigned long long)n * (unsigned long long)m);
+    const dim3 grid((n + kRowsPerBlock - 1) / kRowsPerBlock, (m + kColsPerBlock - 1) / kColsPerBlock);
+    for (int q = 0; q < kPasses; ++q) {
+        hipLaunchKernelGGL(select_pass_kernel, grid, dim3(kRowsPerBlock), 0, s, xc, yc, xx, yy, n, m, d, st, hist,
+                           kShift[q], kWidth[q]);
+        hipLaunchKernelGGL(select_scan_kernel, dim3(1), dim3(1024), 0, s, st, hist, kShift[q], kWidth[q]);
+    }
+    hipLaunchKernelGGL(select_finish_kernel, dim3(1), dim3(64), 0, s, st, out);
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? SK_OK : hip_fail(e, "sk_cost_median_f64");
+}
+
+}  // extern "C"

@@ -39,6 +39,7 @@ UNITS = [   # (source, object name, extra flags)
                                                     "-mllvm", "-amdgpu-mfma-vgpr-form"]),
     ("sk_lse_partial.hip", "sk_lse_partial_large", ["-fno-honor-nans", "-mno-amdgpu-ieee", "-DSK_PARTIAL_LARGE=1"]),
     ("sk_kernels.hip", "sk_kernels", []),
+    ("sk_median.hip", "sk_median", []),
 ]
 
 

@@ -85,6 +85,9 @@ _SIGS = {
     "sk_loop_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int, ctypes.c_int, ctypes.c_int]),
     "sk_loop_init_f32": (ctypes.c_int, [ctypes.POINTER(SkLoop), ctypes.c_void_p]),
     "sk_loop_run_f32": (ctypes.c_int, [ctypes.POINTER(SkLoop), ctypes.c_int, ctypes.c_void_p]),
+    "sk_cost_median_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int, ctypes.c_int, ctypes.c_int]),
+    "sk_cost_median_f64": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                          ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
 }
 SYMBOLS = tuple(_SIGS)
 
@@ -281,6 +284,28 @@ def half_step(side: HipCloud, other: HipCloud, other_h: torch.Tensor, sc: torch.
     return out
 
 
+MEDIAN_D_MAX = 128                        # SK_MEDIAN_D_MAX
+
+
+def cost_median(xc: np.ndarray, yc: np.ndarray, device) -> float:
+    """median over all pairs of max(|xc_i|^2 + |yc_j|^2 - 2 xc_i . yc_j, 0) in float64, np.median's definition,
+    on the GPU (sk_cost_median_f64): the exact-median branch of normalization(how="median")
+    (src/trnopt/sinkhorn.py:229-233) without the n x m matrix. xc, yc: centred float64 (n, d), (m, d)."""
+    xc = np.ascontiguousarray(xc, dtype=np.float64)
+    yc = np.ascontiguousarray(yc, dtype=np.float64)
+    if xc.ndim != 2 or yc.ndim != 2 or xc.shape[1] != yc.shape[1]:
+        raise ValueError("xc (n, d) and yc (m, d) must share d")
+    (n, d), m = xc.shape, yc.shape[0]
+    lb = lib()
+    X = torch.as_tensor(xc).to(device)
+    Y = torch.as_tensor(yc).to(device)
+    out = torch.empty(1, dtype=torch.float64, device=device)
+    ws = _workspace(lb.sk_cost_median_workspace_bytes(n, m, d), device)
+    _check(lb.sk_cost_median_f64(X.data_ptr(), Y.data_ptr(), n, m, d, out.data_ptr(), ws.data_ptr(), ws.numel(),
+                                 _stream()), "sk_cost_median_f64")
+    return float(out.item())
+
+
 # ---------------------------------------------------------------------------------------------------------
 # The on-device loop
 
@@ -288,8 +313,8 @@ class DeviceLoop:
     """The iteration loop of src/trnopt/sinkhorn.py:346-378 on the GPU.
 
     Each enqueued iteration is: f update (X rows against Y), g update (Y rows against X, which also reduces
-    the convergence measures), and a one-wave control kernel that advances it / stage / stage_it, runs the
-    reference's checks at its cadence, sets `done` and writes the next eps's scalars. Kernels enqueued after
+    the convergence measures; the last workgroup of its merge advances it / stage / stage_it, runs the
+    reference's checks at its cadence, sets `done` and writes the next eps's scalars). Kernels enqueued after
     `done` return at once, so the host enqueues batches and reads the 72-byte state once per batch, with the
     next batch already queued behind it (no per-iteration synchronisation)."""
 

@@ -25,7 +25,8 @@ from dataclasses import dataclass, replace
 
 import numpy as np
 
-from .sinkhorn import SinkhornOptions, SinkhornResult, normalization, sinkhorn, transport_plan
+from .sinkhorn import (SinkhornOptions, SinkhornResult, _gpu_device, _use_hip, normalization, sinkhorn,
+                       transport_plan)
 
 PAIR_KEYS = ("f", "g", "eps", "center", "cost_scale", "row_mass", "col_mass", "learned_growth", "cells0",
              "cells1", "x0", "x1")
@@ -66,10 +67,13 @@ def wot_transport_map(x0: np.ndarray, x1: np.ndarray, growth: np.ndarray | None 
     supplies backend, kernel, check_every and max_iters; eps, rho, normalize and the stages are set here."""
     I, J = len(x0), len(x1)
     G = np.ones(I) if growth is None else np.power(np.asarray(growth, dtype=np.float64), delta_days)
+    opts = opts or SinkhornOptions()
+    hip = _use_hip(opts, np.shape(x0)[1])
     t = time.perf_counter()
-    norm = normalization(x0, x1, how="median")
+    # once per pair (the cost does not change across growth iterations); on the GPU when the fused path runs
+    norm = normalization(x0, x1, how="median", device=_gpu_device(opts) if hip and np.shape(x0)[1] <= 128 else None)
     seconds = time.perf_counter() - t
-    base = replace(opts or SinkhornOptions(), eps=eps, rho=(lambda1, lambda2), normalize=norm,
+    base = replace(opts, eps=eps, rho=(lambda1, lambda2), normalize=norm,
                    eps_stages=wot_eps_stages(eps), stage_tol=stage_tol, tol=tol, eps_start=None, fixed_iters=False)
     a, b = np.full(I, 1.0 / I), np.full(J, 1.0 / J)
     learned, iters, res = [], 0, None

@@ -249,13 +249,22 @@ def _log_weights(w, n: int, name: str) -> np.ndarray:
 
 
 def normalization(x: np.ndarray, y: np.ndarray, samples: int = 20_000, seed: int = 0,
-                  how: str = "mean") -> tuple[np.ndarray, float]:
+                  how: str = "mean", device=None) -> tuple[np.ndarray, float]:
     """(center, cost_scale) as the reference computes them (src/trnopt/sinkhorn.py:220-238): center = mean of all
     points; cost_scale = the mean squared x-y distance over `samples` random pairs (rng seed `seed`), or with
-    how="median" the median over all pairs when n m <= 1e8 (else over the random pairs). 1 if that is 0."""
+    how="median" the median over all pairs when n m <= 1e8 (else over the random pairs). 1 if that is 0.
+
+    device: a ROCm GPU device to take the exact median there (sk_cost_median_f64: radix select over the cost
+    recomputed on the fly, no n x m array); None computes it on the host like the reference."""
+    x = np.asarray(x, dtype=np.float64)
+    y = np.asarray(y, dtype=np.float64)
     center = np.concatenate([x, y]).mean(axis=0)
     if how == "median" and len(x) * len(y) <= 100_000_000:
         xc, yc = x - center, y - center
+        if device is not None:
+            from . import hip_sinkhorn as hk
+            scale = hk.cost_median(xc, yc, device)
+            return center, (scale if scale > 0 else 1.0)
         C = ((xc * xc).sum(1)[:, None] + (yc * yc).sum(1)[None, :] - 2.0 * (xc @ yc.T)).ravel()
         scale = float(np.median(np.maximum(C, 0.0)))
     else:
@@ -266,8 +275,14 @@ def normalization(x: np.ndarray, y: np.ndarray, samples: int = 20_000, seed: int
     return center, (scale if scale > 0 else 1.0)
 
 
-def _prepare(x, y, a, b, opts: SinkhornOptions, a_target, b_target):
-    """Validation, weights, normalisation and the eps schedule (src/trnopt/sinkhorn.py:250-320, 340-344)."""
+def _gpu_device(opts: SinkhornOptions):
+    dev = torch.device(opts.backend.device)
+    return torch.device("cuda", torch.cuda.current_device()) if dev.index is None else dev
+
+
+def _prepare(x, y, a, b, opts: SinkhornOptions, a_target, b_target, hip: bool = False):
+    """Validation, weights, normalisation and the eps schedule (src/trnopt/sinkhorn.py:250-320, 340-344). With
+    the HIP path selected, an exact median normalisation runs on the GPU."""
     be = opts.backend
     x = np.asarray(x, dtype=np.float64)
     y = np.asarray(y, dtype=np.float64)
@@ -288,7 +303,9 @@ def _prepare(x, y, a, b, opts: SinkhornOptions, a_target, b_target):
     if isinstance(opts.normalize, tuple):
         center, scale = np.asarray(opts.normalize[0], dtype=np.float64), float(opts.normalize[1])
     elif opts.normalize:
-        center, scale = normalization(x, y, how=opts.normalize if isinstance(opts.normalize, str) else "mean")
+        how = opts.normalize if isinstance(opts.normalize, str) else "mean"
+        center, scale = normalization(x, y, how=how,
+                                      device=_gpu_device(opts) if hip and x.shape[1] <= 128 else None)
     else:
         center, scale = np.zeros(x.shape[1]), 1.0
     root = np.sqrt(scale)
@@ -317,8 +334,8 @@ def sinkhorn(x, y, a=None, b=None, opts: SinkhornOptions | None = None, a_target
     rho KL(P 1 | a_target) and rho KL(P^T 1 | b_target) pull the plan's sums toward a_target and b_target (default
     a and b): wot's formulation is a uniform reference, a_target = growth / I, b_target = mean growth / J."""
     opts = opts or SinkhornOptions()
-    p = _prepare(x, y, a, b, opts, a_target, b_target)
-    hip = _use_hip(opts, p.x.shape[1])
+    hip = _use_hip(opts, np.shape(x)[1])
+    p = _prepare(x, y, a, b, opts, a_target, b_target, hip)
     if max(1, int(opts.cores)) > 1:
         raise ValueError("cores > 1 split rows across NeuronCores in the reference; this build runs on one GPU")
     if hip:

@@ -2,6 +2,7 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
     python bench.py --profile [--reps R]     # for rocprofv3: R half-steps, then a 256 MiB copy
+    python bench.py --workload {single-cell, single-cell-pipeline, stress-65k} [--no-cpu]
 
 Workload: synthetic balanced 10,000 x 10,000, d = 64, fp32, x ~ N(0, 1) (seed 0), y ~ N(0, 1) + 0.5
 (seed 1), uniform weights, squared-Euclidean cost, no normalisation, eps = 0.1 (the reference's
@@ -161,6 +162,166 @@ def cpu_baseline(iters=2):
                        f"after 1 warm-up iteration; torch {torch.__version__} CPU float32")
 
 
+# ---------------------------------------------------------------------------------------------------------
+# Other workloads of the reference's benchmark set (opt-in with --workload; the headline is the default line).
+# Each prints one JSON line: GPU wall time, and beside it the CPU port on a bounded sample, extrapolated.
+
+def single_cell_inputs(n=7355, m=8962, d=30, t0=0, t1=1):
+    """Anisotropic Gaussians (per-axis std 1/sqrt(k+1), PCA-like), cloud t offset by 0.3 sigma t, and
+    lognormal(0, 0.5) source growth weights normalised to 1."""
+    import numpy as np
+    sig = 1.0 / np.sqrt(np.arange(d) + 1.0)
+    x = np.random.default_rng(t0).standard_normal((n, d)) * sig + 0.3 * sig * t0
+    y = np.random.default_rng(t1).standard_normal((m, d)) * sig + 0.3 * sig * t1
+    w = np.random.default_rng(2).lognormal(0.0, 0.5, n)
+    return x, y, w / w.sum()
+
+
+def _cpu_per_iteration(x, y, a, b, center, scale, iters=3, **kw):
+    """Seconds per iteration of the float32 CPU port (block 2048, all host cores) over `iters` fixed iterations."""
+    import torch
+    sys.path.insert(0, str(ROOT))
+    from oracle.reference import sinkhorn_ref
+    torch.set_num_threads(len(os.sched_getaffinity(0)))
+    r = sinkhorn_ref(x, y, a, b, normalize=(center, scale), max_iters=iters, fixed_iters=True, dtype=torch.float32,
+                     block=2048, **kw)
+    return r.seconds / iters
+
+
+def _host_median_seconds(x, y):
+    sys.path.insert(0, str(ROOT))
+    from oracle.reference import normalization as ref_normalization
+    t = time.perf_counter()
+    ref_normalization(x, y, how="median")
+    return time.perf_counter() - t
+
+
+def workload_single_cell(cpu):
+    """One unbalanced single-cell-shaped solve to convergence (7,355 x 8,962, d 30, eps 0.05, KL weights 1 and
+    50, median-normalised cost, wot formulation: uniform reference, growth-weighted row target), end to end."""
+    import numpy as np
+    import torch
+    from trnopt import Backend, SinkhornOptions, sinkhorn
+    from trnopt.sinkhorn import normalization
+    x, y, w = single_cell_inputs()
+    I, J = len(x), len(y)
+    a, b = np.full(I, 1.0 / I), np.full(J, 1.0 / J)
+    o = SinkhornOptions(eps=0.05, rho=(1.0, 50.0), normalize="median", tol=1e-6, max_iters=50_000,
+                        kernel="hip", backend=Backend.preset("rocm"))
+    sinkhorn(x, y, a, b, o, a_target=w, b_target=b)
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    r = sinkhorn(x, y, a, b, o, a_target=w, b_target=b)
+    e2e = time.perf_counter() - t
+    t = time.perf_counter()
+    center, scale = normalization(x, y, how="median", device="cuda")
+    med = time.perf_counter() - t
+    line = {"metric": "end-to-end seconds, single-cell-shaped unbalanced solve to tol 1e-6", "value": round(e2e, 4),
+            "unit": "s", "higher_is_better": False, "n_gpus": 1, "dtype": "f32", "data": "synthetic",
+            "iterations": r.iterations, "converged": r.converged,
+            "ms_per_iteration": round(r.seconds * 1e3 / max(r.iterations, 1), 4), "gpu_median_s": round(med, 4),
+            "config": {"workload": "unbalanced 7355 x 8962, d 30, eps 0.05, rho (1, 50), median cost, tol 1e-6"}}
+    if cpu:
+        hm = _host_median_seconds(x, y)
+        per = _cpu_per_iteration(x, y, a, b, center, scale, eps=0.05, rho=(1.0, 50.0), a_target=w, b_target=b)
+        line["cpu_baseline"] = {"value": round(hm + per * r.iterations, 2), "unit": "s",
+                                "cores": len(os.sched_getaffinity(0)), "kind": "port",
+                                "sample": f"host median {hm:.2f} s + 3 fixed float32 iterations "
+                                          f"({per * 1e3:.1f} ms each) x the GPU's {r.iterations} iterations"}
+    return line
+
+
+def pipeline_sizes(n_points=39, total=175_000):
+    import numpy as np
+    s = np.exp(np.random.default_rng(3).uniform(np.log(1500), np.log(9000), n_points))
+    return np.maximum(np.round(s * total / s.sum()).astype(int), 2)
+
+
+def workload_pipeline(cpu):
+    """38 consecutive wot transport maps (39 time points, log-uniform sizes in [1,500, 9,000] summing to
+    ~175,000, d 30), each with median normalisation, wot's eps stages and 3 growth iterations, end to end."""
+    import numpy as np
+    import torch
+    from trnopt import Backend, SinkhornOptions
+    from trnopt.singlecell import wot_transport_map
+    sizes = pipeline_sizes()
+    o = SinkhornOptions(check_every=5, max_iters=50_000, kernel="hip", backend=Backend.preset("rocm"))
+    clouds = [single_cell_inputs(n=int(sizes[t]), m=int(sizes[t + 1]), t0=t, t1=t + 1)[:2]
+              for t in range(len(sizes) - 1)]
+    wot_transport_map(*clouds[0], growth_iters=1, opts=o)          # warm-up
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    work = iters = 0
+    for k, (x0, x1) in enumerate(clouds):
+        tm = wot_transport_map(x0, x1, growth_iters=3, tol=1e-6, stage_tol=1e-6, opts=o)
+        iters += tm.iterations
+        work += tm.iterations * len(x0) * len(x1)
+        print(f"pair {k}: {len(x0)} x {len(x1)}, {tm.iterations} iterations, {tm.seconds:.3f} s", file=sys.stderr,
+              flush=True)
+    total = time.perf_counter() - t
+    line = {"metric": "total seconds, 38-pair wot pipeline (3 growth iterations each)", "value": round(total, 3),
+            "unit": "s", "higher_is_better": False, "n_gpus": 1, "dtype": "f32", "data": "synthetic",
+            "pairs": len(clouds), "iterations": iters, "points": int(sizes.sum()),
+            "config": {"workload": "39 time points, d 30, eps 0.05, rho (1, 50), wot stages, tol 1e-6, growth 3"}}
+    if cpu:
+        x0, x1 = clouds[0]
+        I, J = len(x0), len(x1)
+        sys.path.insert(0, str(ROOT))
+        from oracle.reference import normalization as ref_normalization
+        c, sc = ref_normalization(x0, x1, how="median")
+        per = _cpu_per_iteration(x0, x1, np.full(I, 1 / I), np.full(J, 1 / J), c, sc, eps=0.05, rho=(1.0, 50.0))
+        medians = sum(_host_median_seconds(a_, b_) for a_, b_ in clouds[:3]) / 3 * len(clouds)
+        est = medians + per / (I * J) * work
+        line["cpu_baseline"] = {"value": round(est, 1), "unit": "s", "cores": len(os.sched_getaffinity(0)),
+                                "kind": "port",
+                                "sample": f"3 fixed float32 iterations of the first pair ({I} x {J}) scaled by the "
+                                          f"GPU run's sum of iterations x n0 n1, plus host medians of 3 pairs "
+                                          f"scaled to {len(clouds)}"}
+    return line
+
+
+def stress_inputs(n=65_536, d=128):
+    import numpy as np
+    r = np.random.default_rng(0)
+    mu = 2.0 * r.standard_normal((8, d))
+    x = mu[r.integers(8, size=n)] + 0.5 * r.standard_normal((n, d))
+    r1 = np.random.default_rng(1)
+    y = mu[r1.integers(8, size=n)] + 0.5 * r1.standard_normal((n, d))
+    return x, y
+
+
+def workload_stress(cpu):
+    """65,536 x 65,536, d 128, 8-component Gaussian mixtures, median-normalised cost (sampled pairs), eps
+    annealed 1.0 -> 0.01 by 0.7 per stage, 20 iterations per stage, 280 iterations in all."""
+    import numpy as np
+    import torch
+    from trnopt import Backend, SinkhornOptions, sinkhorn
+    x, y = stress_inputs()
+    o = SinkhornOptions(eps=0.01, eps_stages=tuple(0.7 ** k for k in range(13)), stage_max_iters=20,
+                        check_every=20, fixed_iters=True, max_iters=280, normalize="median", kernel="hip",
+                        backend=Backend.preset("rocm"))
+    sinkhorn(x[:4096], y[:4096], opts=o)
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    r = sinkhorn(x, y, opts=o)
+    e2e = time.perf_counter() - t
+    line = {"metric": "end-to-end seconds, 65k x 65k d 128 eps-scaling stress solve (280 iterations)",
+            "value": round(e2e, 3), "unit": "s", "higher_is_better": False, "n_gpus": 1, "dtype": "f32",
+            "data": "synthetic", "iterations": r.iterations,
+            "ms_per_iteration": round(r.seconds * 1e3 / max(r.iterations, 1), 3),
+            "config": {"workload": "balanced 65536 x 65536, d 128, eps 1.0 -> 0.01 (0.7 per stage), 280 its"}}
+    if cpu:
+        per = _cpu_per_iteration(x, y, None, None, r.center, r.cost_scale, iters=2, eps=0.01)
+        line["cpu_baseline"] = {"value": round(per * 280, 1), "unit": "s", "cores": len(os.sched_getaffinity(0)),
+                                "kind": "port",
+                                "sample": f"2 fixed float32 iterations at eps 0.01 ({per:.2f} s each) x 280"}
+    return line
+
+
+WORKLOADS = {"single-cell": workload_single_cell, "single-cell-pipeline": workload_pipeline,
+             "stress-65k": workload_stress}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -170,6 +331,8 @@ def main():
     ap.add_argument("--cpu-iters", type=int, default=2)
     ap.add_argument("--profile", action="store_true", help="only the launches the rocprofv3 summaries use")
     ap.add_argument("--reps", type=int, default=20)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default=None,
+                    help="one of the other benchmark workloads instead of the headline line")
     a = ap.parse_args()
     if a.gpus != 1:
         print("bench.py measures one GPU: this build's path is single-GPU (the multi-GPU row split is a design "
@@ -177,6 +340,9 @@ def main():
         sys.exit(2)
     if a.profile:
         profile_run(a.reps)
+        return
+    if a.workload is not None:
+        print(json.dumps(WORKLOADS[a.workload](not a.no_cpu)), flush=True)
         return
     g = gpu_run(a.steps, a.warmup)
     cpu = None if a.no_cpu else cpu_baseline(a.cpu_iters)

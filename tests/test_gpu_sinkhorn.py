@@ -160,3 +160,21 @@ def test_wot_formulation_matches_wot_scaling(staged):
                            tol=1e-6, max_iters=20_000, check_every=5, eps_stages=wot_eps_stages(eps) if staged else None,
                            a_target=G / I, b_target=np.full(J, G.mean() / J), dtype=torch.float32)
     assert abs(res.iterations - r32.iterations) <= 10
+
+
+def test_single_cell_unbalanced_converges_like_the_reference_op_sequence():
+    """The single-cell-shaped unbalanced solve (7,355 x 8,962, d 30, eps 0.05, rho (1, 50), median cost, tol 1e-6,
+    floored to 5e-6 in float32) must converge as the reference's float32 op sequence does (the torch path on the
+    same GPU): a kernel whose log-sum-exp carried an iteration-dependent rounding offset stalled at 2e-5 here."""
+    x, y, w = data.single_cell_like()
+    I, J = len(x), len(y)
+    a, b = np.full(I, 1.0 / I), np.full(J, 1.0 / J)
+    o = dict(eps=0.05, rho=(1.0, 50.0), normalize="median", tol=1e-6, max_iters=5000)
+    print("single-cell hip", flush=True)
+    rh = sinkhorn(x, y, a, b, hip_opts(**o), a_target=w, b_target=b)
+    print("single-cell torch on the GPU", flush=True)
+    rt = sinkhorn(x, y, a, b, SinkhornOptions(kernel="torch", backend=ROCM, **o), a_target=w, b_target=b)
+    assert rt.converged and rh.converged, (rh.iterations, rh.error, rt.iterations, rt.error)
+    assert abs(rh.iterations - rt.iterations) <= max(30, rt.iterations // 5), (rh.iterations, rt.iterations)
+    assert inf_rel(rh.f, rt.f) < 1e-5 and inf_rel(rh.g, rt.g) < 1e-5
+    assert np.abs(rh.row_mass / rt.row_mass - 1).max() < 1e-3

@@ -60,10 +60,6 @@ namespace sk {
 namespace {
 
 __device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
-// exp2 of an exponent that is <= 0 up to the rounding of its offset, clamped to [0, 1] (the clamp bit of the
-// instruction): where a row's offset is a padding sentinel near -1e30 the rounding residual of fl(c m) is
-// itself huge, and exp2 of it must not reach infinity.
-__device__ __forceinline__ float ex2_unit(float x) { return __builtin_amdgcn_fmed3f(ex2(x), 0.0f, 1.0f); }
 
 // Hardware hands consecutive workgroup ids to the 8 XCDs in turn; renumber so that the workgroups of one
 // XCD own one contiguous range of the work.
@@ -102,18 +98,18 @@ __device__ __forceinline__ void static_for(F&& f) {
 //                  blocks; costed high so that the adds land a few MFMA slots later, past the LDS latency)
 //   j in [1, 17):  a_r = acc_r + col_r
 //   j in [17, 25): running max over a pair of scores
-//   j == 25:       cm = fl(c m)
-//   j in [26, 42): acc_r = exp2(c a_r - cm), in place
-//   j in [42, 57): the sum of the 16 exponentials as a pairwise tree (8 + 4 + 2 + 1 adds), long after the
+//   j in [25, 41): acc_r = exp2(c (a_r - m)), in place
+//   j in [41, 56): the sum of the 16 exponentials as a pairwise tree (8 + 4 + 2 + 1 adds), long after the
 //                  exponentials were issued, so no add waits on the transcendental unit
-//   j == 57:       S = S exp2(CM - cm) + sum, M = m, CM = cm
-// The row state is (M, CM = fl(c M), S) with S relative to 2^CM: subtracting the rounded offset inside the
-// fma leaves exp2(c a - fl(c m)) = 2^(c m - fl(c m)) exp2(c (a - m)), a factor common to every term of the
-// row, so the log-sum-exp CM + log2 S is exact up to the rounding of c M itself (2^-24 relative, as if the
-// result were rounded to fp32 once).
+//   j == 56:       S = S exp2(c (M - m)) + sum, M = m
+// The max is subtracted before the scaling: a - m is exact for the scores near the maximum, so the dominant
+// term is exactly 1 and S is relative to 2^(c M) exactly, which is what the merge of the slots assumes.
+// (Folding the offset into one fma, exp2(c a - fl(c m)), would leave S relative to the rounded fl(c M): an
+// error of up to half an ulp of c M in the log-sum-exp, which moves with M from one iteration to the next
+// and holds float32 Sinkhorn several ulps away from its fixed point.)
 // Steps are spread over the MFMA slots of the next tile in proportion to their cost.
-constexpr int kOps = 58;
-constexpr int op_cost(int j) { return j == 0 ? 8 : (j >= 26 && j < 42) ? 3 : j == 57 ? 4 : 1; }
+constexpr int kOps = 57;
+constexpr int op_cost(int j) { return j == 0 ? 8 : (j >= 25 && j < 41) ? 4 : j == 56 ? 4 : 1; }
 constexpr int block_cost() {
     int s = 0;
     for (int j = 0; j < kOps; ++j) s += op_cost(j);
@@ -134,11 +130,10 @@ constexpr int op_begin(int i, int NS) {
 // col4(q) returns the column terms of accumulators 4q .. 4q + 3 of the tile being updated.
 template <int RB>
 struct Online {
-    float m[RB], cm[RB];
+    float m[RB];
     f32x4 cv[4];
     template <int k, class ColFn>
-    __device__ __forceinline__ void step(f32x16 (&acc)[RB], ColFn&& col4, float (&M)[RB], float (&CM)[RB],
-                                         float (&S)[RB], float c) {
+    __device__ __forceinline__ void step(f32x16 (&acc)[RB], ColFn&& col4, float (&M)[RB], float (&S)[RB], float c) {
         constexpr int j = k / RB, b = k % RB;
         if constexpr (j == 0) {
             if constexpr (b == 0)
@@ -151,22 +146,19 @@ struct Online {
         } else if constexpr (j < 25) {
             constexpr int p = j - 17;
             m[b] = max3(m[b], acc[b][2 * p], acc[b][2 * p + 1]);
-        } else if constexpr (j == 25) {
-            cm[b] = c * m[b];
-        } else if constexpr (j < 42) {
-            constexpr int r = j - 26;
-            acc[b][r] = ex2_unit(fmaf(c, acc[b][r], -cm[b]));
-        } else if constexpr (j < 57) {
+        } else if constexpr (j < 41) {
+            constexpr int r = j - 25;
+            acc[b][r] = ex2(c * (acc[b][r] - m[b]));
+        } else if constexpr (j < 56) {
             // tree level l (stride 2^l) pairs acc[2^(l+1) q] += acc[2^(l+1) q + 2^l]
-            constexpr int t = j - 42;
+            constexpr int t = j - 41;
             constexpr int l = t < 8 ? 0 : t < 12 ? 1 : t < 14 ? 2 : 3;
             constexpr int q = t - (l == 0 ? 0 : l == 1 ? 8 : l == 2 ? 12 : 14);
             constexpr int lo = q << (l + 1), hi = lo + (1 << l);
             acc[b][lo] = acc[b][lo] + acc[b][hi];
         } else {
-            S[b] = fmaf(S[b], ex2(CM[b] - cm[b]), acc[b][0]);
+            S[b] = fmaf(S[b], ex2(c * (M[b] - m[b])), acc[b][0]);
             M[b] = m[b];
-            CM[b] = cm[b];
         }
     }
 };
@@ -199,20 +191,18 @@ struct Contract<kBF16x3> {
 };
 
 // End of a work segment: lanes l and l + 32 hold the same row over different columns; merge them and store
-// (M / sigma, S) of each row. fl(c M) is monotone in M, so the larger CM belongs to the larger M.
+// (M / sigma, S) of each row.
 template <int RB>
-__device__ __forceinline__ void store_rows(const PartialArgs& a, const float (&M)[RB], const float (&CM)[RB],
-                                           const float (&S)[RB], int rb0, int slot, float inv_sigma, int lane) {
+__device__ __forceinline__ void store_rows(const PartialArgs& a, const float (&M)[RB], const float (&S)[RB], int rb0,
+                                           int slot, float c, float inv_sigma, int lane) {
 #pragma unroll
     for (int b = 0; b < RB; ++b) {
         const float Mo = __shfl_xor(M[b], 32);
-        const float CMo = __shfl_xor(CM[b], 32);
         const float So = __shfl_xor(S[b], 32);
-        const float CMn = fmaxf(CM[b], CMo);
-        const float Sn = S[b] * ex2(CM[b] - CMn) + So * ex2(CMo - CMn);
+        const float Mn = fmaxf(M[b], Mo);
+        const float Sn = S[b] * ex2(c * (M[b] - Mn)) + So * ex2(c * (Mo - Mn));
         if (lane < 32 && rb0 + b < a.nrb)
-            a.part[(size_t)slot * a.rows_pad + (size_t)(rb0 + b) * 32 + lane] =
-                make_float2(fmaxf(M[b], Mo) * inv_sigma, Sn);
+            a.part[(size_t)slot * a.rows_pad + (size_t)(rb0 + b) * 32 + lane] = make_float2(Mn * inv_sigma, Sn);
     }
 }
 
@@ -246,11 +236,10 @@ struct Staged {
                 for (int p = 0; p < kPieces; ++p)
                     xv[b][cc][p] = xt[(size_t)blk * TILE16 + (cc * kPieces + p) * 64 + lane];
         }
-        float M[RB], CM[RB], S[RB];
+        float M[RB], S[RB];
 #pragma unroll
         for (int b = 0; b < RB; ++b) {
             M[b] = kEmpty;
-            CM[b] = c * kEmpty;
             S[b] = 0.0f;
         }
 
@@ -302,14 +291,14 @@ struct Staged {
                 accN[b] = C::mfma(yv[cc][cp], xv[b][cc][rp], accN[b]);
                 if (epi) {
                     constexpr int k0 = op_begin<RB>(i, NS), k1 = op_begin<RB>(i + 1, NS);
-                    static_for<k0, k1>([&](auto K) { on.template step<decltype(K)::value>(accP, col4, M, CM, S, c); });
+                    static_for<k0, k1>([&](auto K) { on.template step<decltype(K)::value>(accP, col4, M, S, c); });
                 }
                 __builtin_amdgcn_sched_barrier(0);
             });
         };
         auto update = [&](f32x16 (&accP)[RB], const float* colp) {
             auto col4 = [&](int q) { return *reinterpret_cast<const f32x4*>(colp + 8 * q); };
-            static_for<0, RB * kOps>([&](auto K) { on.template step<decltype(K)::value>(accP, col4, M, CM, S, c); });
+            static_for<0, RB * kOps>([&](auto K) { on.template step<decltype(K)::value>(accP, col4, M, S, c); });
         };
         auto colp_of = [&](int cbuf) { return lds_col + cbuf * 32 + 4 * h; };
 
@@ -354,7 +343,7 @@ struct Staged {
         }
         update(accA, colp_of(cb));
     done:
-        store_rows(a, M, CM, S, rb0, slot, inv_sigma, lane);
+        store_rows(a, M, S, rb0, slot, c, inv_sigma, lane);
     }
 };
 
@@ -391,11 +380,10 @@ struct Streamed {
                 for (int p = 0; p < kPieces; ++p)
                     xv[b][cc][p] = xt[(size_t)blk * TILE16 + (cc * kPieces + p) * 64 + lane];
         }
-        float M[RB], CM[RB], S[RB];
+        float M[RB], S[RB];
 #pragma unroll
         for (int b = 0; b < RB; ++b) {
             M[b] = kEmpty;
-            CM[b] = c * kEmpty;
             S[b] = 0.0f;
         }
 
@@ -449,14 +437,14 @@ struct Streamed {
                 accN[b] = C::mfma(yv[cc][cp], xv[b][cc][rp], accN[b]);
                 if (epi) {
                     constexpr int k0 = op_begin<RB>(i, NS), k1 = op_begin<RB>(i + 1, NS);
-                    static_for<k0, k1>([&](auto K) { on.template step<decltype(K)::value>(accP, col4, M, CM, S, c); });
+                    static_for<k0, k1>([&](auto K) { on.template step<decltype(K)::value>(accP, col4, M, S, c); });
                 }
                 __builtin_amdgcn_sched_barrier(0);
             });
         };
         auto update = [&](f32x16 (&accP)[RB], const float* colp) {
             auto col4 = [&](int q) { return *reinterpret_cast<const f32x4*>(colp + 8 * q); };
-            static_for<0, RB * kOps>([&](auto K) { on.template step<decltype(K)::value>(accP, col4, M, CM, S, c); });
+            static_for<0, RB * kOps>([&](auto K) { on.template step<decltype(K)::value>(accP, col4, M, S, c); });
         };
 
         // Tiles in pairs so the accumulator and operand buffers alternate without copies; the operand load of
@@ -493,7 +481,7 @@ struct Streamed {
         }
         update(accA, colp_of(t - 1));
     done:
-        store_rows(a, M, CM, S, rb0, slot, inv_sigma, lane);
+        store_rows(a, M, S, rb0, slot, c, inv_sigma, lane);
     }
 };
 

@@ -178,3 +178,41 @@ def test_single_cell_unbalanced_converges_like_the_reference_op_sequence():
     assert abs(rh.iterations - rt.iterations) <= max(30, rt.iterations // 5), (rh.iterations, rt.iterations)
     assert inf_rel(rh.f, rt.f) < 1e-5 and inf_rel(rh.g, rt.g) < 1e-5
     assert np.abs(rh.row_mass / rt.row_mass - 1).max() < 1e-3
+
+
+def test_stress_shaped_eps_stages_match_reference():
+    """The 65k stress workload's schedule at 2,048 x 2,048 (d 128, 8-component mixtures, median cost, eps
+    annealed 1.0 -> 0.01 by 0.7, 20 iterations per stage, 280 in all; the staged d 128 kernel): the fused path
+    is at least as close to the float64 reference as the reference's own float32 run."""
+    x, y = data.gaussian_mixture_8(n=2048, m=2048, d=128)
+    o = dict(eps=0.01, eps_stages=tuple(0.7 ** k for k in range(13)), stage_max_iters=20, check_every=20,
+             fixed_iters=True, max_iters=280, normalize="median")
+    print("stress-shaped hip", flush=True)
+    res = sinkhorn(x, y, opts=hip_opts(**o))
+    print("stress-shaped oracle float64 / float32", flush=True)
+    r64 = ref.sinkhorn_ref(x, y, dtype=torch.float64, block=1024, **o)
+    r32 = ref.sinkhorn_ref(x, y, dtype=torch.float32, block=1024, **o)
+    assert res.iterations == r64.iterations == 280
+    base_f, base_g = inf_rel(r32.f, r64.f), inf_rel(r32.g, r64.g)
+    print("hip vs f64", inf_rel(res.f, r64.f), inf_rel(res.g, r64.g), "torch f32 vs f64", base_f, base_g)
+    assert inf_rel(res.f, r64.f) <= 2 * base_f + 1e-6 and inf_rel(res.g, r64.g) <= 2 * base_g + 1e-6
+
+
+def test_wot_pipeline_three_pairs_matches_torch_path():
+    """The pipeline workload in miniature: three consecutive wot maps (growth re-estimated 3 times each) on the
+    fused path against the reference's float32 op sequence on the CPU."""
+    from trnopt.singlecell import wot_transport_map
+    sizes = [420, 530, 380, 610]
+    sig = 1.0 / np.sqrt(np.arange(30) + 1.0)
+    pts = [np.random.default_rng(t).standard_normal((s, 30)) * sig + 0.3 * sig * t for t, s in enumerate(sizes)]
+    cpu = SinkhornOptions(kernel="torch", backend=Backend.preset("cpu-float32"), check_every=5, max_iters=20_000)
+    gpu = SinkhornOptions(kernel="hip", backend=ROCM, check_every=5, max_iters=20_000)
+    for t in range(3):
+        print("pair", t, flush=True)
+        a = wot_transport_map(pts[t], pts[t + 1], growth_iters=3, opts=gpu)
+        b = wot_transport_map(pts[t], pts[t + 1], growth_iters=3, opts=cpu)
+        assert a.result.converged and b.result.converged
+        assert abs(a.iterations - b.iterations) <= max(20, b.iterations // 10), (a.iterations, b.iterations)
+        for Ga, Gb in zip(a.learned_growth, b.learned_growth):
+            assert np.abs(Ga / Gb - 1).max() < 1e-3
+        assert np.abs(a.result.row_mass / b.result.row_mass - 1).max() < 1e-3

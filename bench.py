@@ -78,6 +78,7 @@ def gpu_run(steps, warmup, kernel_reps=50):
                          max_iters=warmup + steps + 1, check_every=10, stage_max_iters=1000, fixed_iters=True,
                          balanced=True)
     loop.init()
+    loop.capture()                       # with TRNOPT_HIP_GRAPH=1: the graph of a batch, before any timing
     loop.enqueue(warmup)
     torch.cuda.synchronize()
     t0 = time.perf_counter()

@@ -6,6 +6,7 @@ import pytest
 import torch
 
 from oracle import brute
+from oracle import data
 from oracle import reference as ref
 from conftest import inf_rel
 
@@ -177,3 +178,34 @@ def test_out_of_range_coordinates_are_rejected(hip):
         hip.row_lse(torch.full((4, 3), 1e15, device=DEV), torch.ones(5, 3, device=DEV))
     with pytest.raises(ValueError, match="coordinates"):
         hip.HipCloud(np.full((4, 3), np.inf), np.zeros(4), DEV)
+
+
+def test_graph_replays_match_eager_launches(hip, monkeypatch):
+    """The device loop replays captured 10-iteration HIP graphs; several replays, with the program's own eager
+    work and synchronisations between them, give the eager launches' potentials and state bit for bit."""
+    import torch
+    x, y = data.clouds(n=1000, m=777, d=24, seed=9)
+    dev = torch.device("cuda", 0)
+    la, lb = np.full(len(x), -np.log(len(x))), np.full(len(y), -np.log(len(y)))
+    X = hip.HipCloud(x, la, dev, role=0)
+    Y = hip.HipCloud(y, lb, dev, role=1)
+    kw = dict(eps=0.05, rho_x=None, rho_y=None, sched=[0.5, 0.3, 0.2], stages=[], tol=1e-9, stage_tol=1e-5,
+              max_iters=10_000, check_every=10, stage_max_iters=1000, fixed_iters=False, balanced=True)
+    monkeypatch.setenv("TRNOPT_HIP_GRAPH", "1")
+    g = hip.DeviceLoop(X, Y, **kw)
+    g.init()
+    for _ in range(6):
+        g.enqueue(10)
+        torch.cuda.synchronize()
+        assert float((torch.arange(5, device=dev) * 2.0).sum()) == 20.0      # eager work between replays
+    assert g._graph is not None
+    monkeypatch.setenv("TRNOPT_HIP_GRAPH", "0")
+    e = hip.DeviceLoop(X, Y, **kw)
+    e.init()
+    e.enqueue(60)
+    sg, se = g.read_state(), e.read_state()
+    assert e._graph is None
+    assert (sg.it, sg.stage, sg.checks, sg.done) == (se.it, se.stage, se.checks, se.done)
+    assert sg.it == 60 and sg.checks == 6
+    assert sg.err == se.err
+    assert torch.equal(g.fh, e.fh) and torch.equal(g.gh, e.gh)

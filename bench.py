@@ -8,7 +8,8 @@ Workload: synthetic balanced 10,000 x 10,000, d = 64, fp32, x ~ N(0, 1) (seed 0)
 (seed 1), uniform weights, squared-Euclidean cost, no normalisation, eps = 0.1 (the reference's
 examples/sinkhorn_benchmark.py --flashsinkhorn setup). A "step" is one iteration of the on-device loop
 (f half-step, g half-step, loop control: four kernel launches), inputs resident in HBM. W untimed iterations, then
-exactly K timed iterations between two device synchronisations.
+exactly K timed iterations between two device synchronisations (defaults 100 and 200: the first ~100 iterations
+of a process run ~8 % slower while the GPU's clocks settle).
 
 Also reported on the same JSON line:
 * roofline -- the dominant kernel pair, sk_half_step_f32 (lse_partial_kernel, then merge_kernel), timed with
@@ -326,8 +327,8 @@ WORKLOADS = {"single-cell": workload_single_cell, "single-cell-pipeline": worklo
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-iters", type=int, default=2)
     ap.add_argument("--profile", action="store_true", help="only the launches the rocprofv3 summaries use")

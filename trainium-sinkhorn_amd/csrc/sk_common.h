@@ -37,6 +37,10 @@ constexpr float kPadScore = -1.0e30f;  // floor of a (scaled) column term: paddi
 
 enum Mode { kHalfStep = 0, kPlainLse = 1 };
 
+// What a kernel reads for its done flag when the call has none: an unconditional load, so that the flag is
+// requested together with the launch's other scalars.
+__device__ const int kNoSkip = 0;
+
 // Work split shared by the partial and the finalisation kernels: the (row group, column tile) units are
 // cut into P equal contiguous ranges, one per workgroup.
 struct Split {

@@ -39,9 +39,21 @@ __device__ inline void set_scalars(sk_state* st, double e, double rho_x, double 
 //     fh  = kappa ((|x|^2 + eps off) - eps lse) - |x|^2
 // With meas, also the group's convergence partials {max_{i<n_real} |new - old|, sum_i |w (exp(min((old -
 // new) / eps, 50)) - 1)|} (sinkhorn.py:360, 368-373), reduced in a fixed order into meas[g].
-__device__ inline void merge_group(const PartialArgs& a, int g) {
+// Returns false, storing nothing, when the loop is done (*skip != 0): the flag is loaded with the launch's other
+// scalars and the row's first slots, and tested once they have arrived.
+__device__ inline bool merge_group(const PartialArgs& a, int g) {
     const int i = g * kRowsPerGroup + (int)threadIdx.x;
-    const float c = a.mode == kHalfStep ? a.sc[0] * kLog2e : kLog2e;
+    const int* skip_p = a.skip != nullptr ? a.skip : &kNoSkip;
+    const float sc0 = a.sc[0], sc1 = a.sc[1], sc2 = a.sc[2], sc3 = a.sc[3];   // valid in both modes
+    const int ic = i < a.rows_pad ? i : a.rows_pad - 1;
+    const float x2 = a.mode == kHalfStep ? a.xsq[ic] : 0.0f;
+    const float o = a.off != nullptr ? a.off[ic] : 0.0f;
+    const float old = a.meas != nullptr ? a.out[ic] : 0.0f;
+    const float wi = a.meas != nullptr ? a.w[ic] : 0.0f;
+    const int skip = *skip_p;
+    asm volatile("" ::"s"(sc0), "s"(sc1), "s"(sc2), "s"(sc3), "v"(x2), "v"(o), "v"(old), "v"(wi), "v"(skip));
+    if (skip != 0) return false;
+    const float c = a.mode == kHalfStep ? sc0 * kLog2e : kLog2e;
     float dmax = 0.0f;
     double derr = 0.0;
     if (i < a.rows_pad) {
@@ -66,16 +78,13 @@ __device__ inline void merge_group(const PartialArgs& a, int g) {
         // the max enters exactly, in accumulator units
         const float l2s = ep_lg2(S);
         if (a.mode == kHalfStep) {
-            const float eps = a.sc[2], kappa = a.sc[3];
-            const float x2 = a.xsq[i];
-            const float o = a.off != nullptr ? a.off[i] : 0.0f;
+            const float eps = sc2, kappa = sc3;
             const float eps_lse = 2.0f * M + (eps * kLn2) * l2s;
             const float val = kappa * ((x2 + eps * o) - eps_lse) - x2;
             if (a.meas != nullptr) {
-                const float old = a.out[i];
                 if (i < a.n_real) dmax = fabsf(val - old);
-                const float delta = fminf((old - val) * a.sc[1], kDeltaCap);
-                derr = (double)fabsf(a.w[i] * (expf(delta) - 1.0f));
+                const float delta = fminf((old - val) * sc1, kDeltaCap);
+                derr = (double)fabsf(wi * (expf(delta) - 1.0f));
             }
             if (i < a.n_store) a.out[i] = val;
         } else if (i < a.n_store) {
@@ -106,6 +115,7 @@ __device__ inline void merge_group(const PartialArgs& a, int g) {
             a.meas[g] = make_float2(mx, (float)sm);
         }
     }
+    return true;
 }
 
 // After the g update of one iteration, by one wave: the body of sinkhorn.py:356-378. Advances (it, stage,
@@ -161,8 +171,7 @@ __device__ inline void control_step(sk_state* st, const float2* meas, int nmeas,
 // The merge pass: one workgroup per row group. With a loop state (the g update of the on-device loop), the
 // last workgroup to finish runs the loop control; the counter is zero on entry and reset by that workgroup.
 __global__ __launch_bounds__(kRowsPerGroup) void merge_kernel(PartialArgs a) {
-    if (a.skip != nullptr && *a.skip != 0) return;
-    merge_group(a, (int)blockIdx.x);
+    if (!merge_group(a, (int)blockIdx.x)) return;
     if (a.state == nullptr) return;
     __shared__ int s_last;
     __threadfence();                       // release: this group's outputs and meas[g]

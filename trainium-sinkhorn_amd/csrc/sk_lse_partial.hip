@@ -488,7 +488,14 @@ struct Streamed {
 template <int NC, int ROLE, int CT>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void lse_partial_kernel(PartialArgs a) {
-    if (a.skip != nullptr && *a.skip != 0) return;
+    // Every scalar this launch needs (the loop's done flag, the eps scalars, both clouds' scales) is requested
+    // at once, and the done flag tested after: one memory round trip before the work starts, not four.
+    const int* skip_p = a.skip != nullptr ? a.skip : &kNoSkip;
+    const float sc0 = a.sc[0], sc2 = a.sc[2];                         // a.sc is valid in both modes
+    const float sx = packed_scale(a.xr), sy = packed_scale(a.yc);   // 1 for kBF16x3
+    const int skip = *skip_p;
+    asm volatile("" ::"s"(sc0), "s"(sc2), "s"(sx), "s"(sy), "v"(skip));   // all four loaded before the test
+    if (skip != 0) return;
     constexpr bool kStream = NC <= kStreamMaxChunks;
     constexpr int kLdsY = kStream ? 1 : 2 * NC * Contract<CT>::pieces * 64;
     constexpr int kLdsCol = kStream ? (kColTiles + 1) * 32 : 3 * 32;
@@ -505,14 +512,13 @@ void lse_partial_kernel(PartialArgs a) {
     float alpha, beta, c;
     if (a.mode == kHalfStep) {
         alpha = 0.5f;
-        beta = 0.5f * a.sc[2];
-        c = a.sc[0] * kLog2e;
+        beta = 0.5f * sc2;
+        c = sc0 * kLog2e;
     } else {
         alpha = 1.0f;
         beta = 0.0f;
         c = kLog2e;
     }
-    const float sx = packed_scale(a.xr), sy = packed_scale(a.yc);   // 1 for kBF16x3
     const float sigma = sx * sy, inv_sigma = (1.0f / sx) * (1.0f / sy);
     alpha *= sigma;
     beta *= sigma;

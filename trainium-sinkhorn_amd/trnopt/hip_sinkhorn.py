@@ -97,19 +97,22 @@ _load_error: str | None = None
 
 
 def _load():
+    """The library at LIB_PATH, or the build named by TRNOPT_HIP_LIBRARY (another build of the same sources,
+    e.g. to compare two versions)."""
     global _lib, _load_error
     if _lib is not None or _load_error is not None:
         return _lib
-    if not LIB_PATH.exists():
-        _load_error = f"{LIB_PATH} is not built (run trnopt._build.build() or __graft_entry__.build())"
+    path = Path(os.environ.get("TRNOPT_HIP_LIBRARY", str(LIB_PATH)))
+    if not path.exists():
+        _load_error = f"{path} is not built (run trnopt._build.build() or __graft_entry__.build())"
         return None
     try:
-        lib = ctypes.CDLL(str(LIB_PATH))
+        lib = ctypes.CDLL(str(path))
         for name, (res, args) in _SIGS.items():
             fn = getattr(lib, name)
             fn.restype, fn.argtypes = res, args
     except OSError as e:                 # pragma: no cover - depends on the machine
-        _load_error = f"cannot load {LIB_PATH}: {e}"
+        _load_error = f"cannot load {path}: {e}"
         return None
     _lib = lib
     return lib

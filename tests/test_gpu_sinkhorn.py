@@ -51,6 +51,62 @@ def test_fixed_iterations_2048_d64_matches_reference():
     print("hip vs f64", inf_rel(res.f, r64.f), "torch f32 vs f64", inf_rel(r32.f, r64.f))
 
 
+def test_fixed_iterations_10k_d64_matches_reference():
+    """The ms/iteration workload at its full size (10,000 x 10,000, d 64, x ~ N(0, 1), y ~ N(0, 1) + 0.5, eps
+    0.1, 10 fixed iterations from g0 = |y|^2): potentials within 1e-5 (inf-norm relative) of the oracle's
+    float64 and float32 runs of the reference's plain-PyTorch path, and the plan marginals from the two sides'
+    potentials (one float64 host routine, examples/sinkhorn_libs_compare.py:43-56) within 1e-6 entrywise."""
+    x, y = data.synthetic_10k()
+    o = dict(eps=0.1, normalize=False, max_iters=10, fixed_iters=True)
+    print("hip 10k x 10k d64 10 its", flush=True)
+    res = sinkhorn(x, y, opts=hip_opts(**o))
+    assert res.iterations == 10 and not res.converged
+    print("oracle float64", flush=True)
+    r64 = ref.sinkhorn_ref(x, y, dtype=torch.float64, block=2048, **o)
+    assert inf_rel(res.f, r64.f) < 1e-5 and inf_rel(res.g, r64.g) < 1e-5, (inf_rel(res.f, r64.f), inf_rel(res.g, r64.g))
+    print("oracle float32", flush=True)
+    r32 = ref.sinkhorn_ref(x, y, dtype=torch.float32, block=2048, **o)
+    assert inf_rel(res.f, r32.f) < 1e-5 and inf_rel(res.g, r32.g) < 1e-5, (inf_rel(res.f, r32.f), inf_rel(res.g, r32.g))
+    print("hip vs f64", inf_rel(res.f, r64.f), inf_rel(res.g, r64.g), "torch f32 vs f64", inf_rel(r32.f, r64.f),
+          inf_rel(r32.g, r64.g), flush=True)
+    a, b = np.full(len(x), 1.0 / len(x)), np.full(len(y), 1.0 / len(y))
+    rows, cols = brute.plan_marginals(x, y, a, b, res.f, res.g, 0.1, chunk=1024)
+    print("marginals of the oracle's potentials", flush=True)
+    rows_ref, cols_ref = brute.plan_marginals(x, y, a, b, r64.f, r64.g, 0.1, chunk=1024)
+    print("marginal differences", np.abs(rows - rows_ref).max(), np.abs(cols - cols_ref).max(), flush=True)
+    assert np.abs(rows - rows_ref).max() <= 1e-6 and np.abs(cols - cols_ref).max() <= 1e-6
+
+
+def _sampled_last_update_error(x, y, res, j):
+    """The last update of a balanced fixed-iteration solve is g_k = T(f_k): recompute g_k at columns j in float64
+    from the returned f (g_j = -eps log sum_i a_i exp((f_i - C_ij) / eps), uniform a) and return the largest
+    difference relative to ||g||_inf."""
+    from scipy.special import logsumexp
+    s = np.sqrt(res.cost_scale)
+    xs, ys = (x - res.center) / s, (y[j] - res.center) / s
+    C = (xs * xs).sum(1)[:, None] + (ys * ys).sum(1)[None, :] - 2.0 * xs @ ys.T
+    g = -res.eps * logsumexp((res.f[:, None] - C) / res.eps - np.log(len(x)), axis=0)
+    return float(np.abs(g - res.g[j]).max() / np.abs(res.g).max())
+
+
+def test_stress_65k_last_update_matches_float64_on_sampled_columns():
+    """The 65k stress workload at its full size (65,536 x 65,536, d 128, 8-component mixtures, median cost from
+    sampled pairs, eps 1.0 -> 0.01 by 0.7, 20 iterations per stage, 280 in all): too large for the oracle's
+    dense iterates, so pinned by a size-independent property instead -- the returned g is the g update of the
+    returned f, recomputed in float64 at 512 sampled columns."""
+    x, y = data.gaussian_mixture_8()
+    o = dict(eps=0.01, eps_stages=tuple(0.7 ** k for k in range(13)), stage_max_iters=20, check_every=20,
+             fixed_iters=True, max_iters=280, normalize="median")
+    print("hip 65k x 65k d128 280 its", flush=True)
+    res = sinkhorn(x, y, opts=hip_opts(**o))
+    assert res.iterations == 280 and res.eps == 0.01
+    assert np.isfinite(res.f).all() and np.isfinite(res.g).all()
+    j = np.random.default_rng(5).choice(len(y), 512, replace=False)
+    err = _sampled_last_update_error(x, y, res, j)
+    print("sampled g update vs float64", err, flush=True)
+    assert err < 1e-5
+
+
 @pytest.mark.parametrize("iters", [1, 2, 7])
 def test_first_iterations_match_dense_float64(iters):
     """Iterate-by-iterate: the reference's init (g0 = |y|^2) and update order against the dense brute force."""

@@ -14,6 +14,7 @@ from scipy.special import logsumexp
 
 TILE, WAVES, XCDS, RB, BLOCK = 32, 4, 8, 2, 256
 STREAM_MAX_CHUNKS, COL_TILES = 4, 256        # streamed variant: nc <= 4; column terms staged per 256 tiles
+SEG_COST_STREAMED, SEG_COST_STAGED = 4, 2    # cost of a row-group boundary in tiles (sk_kernels.hip make_plan)
 ROWS_PER_GROUP = TILE * RB * WAVES
 EMPTY = -1.0e30
 FIRST = [0, 0, 1]              # fp16x2 (half-steps): (first-cloud piece, second-cloud piece) of the products
@@ -101,11 +102,28 @@ def pack(src, n, d, contraction="f16x2"):
 
 
 class Split:
-    def __init__(self, work, nt, P):
-        self.work, self.nt, self.P = work, nt, P
+    """sk_common.h's Split: units on a cost line where every row-group boundary costs alpha positions."""
+
+    def __init__(self, nt, ngroups, P, alpha):
+        self.nt, self.ngroups, self.P, self.alpha = nt, ngroups, P, alpha
+        self.work = nt * ngroups
+        self.ftot = self.work + alpha * (ngroups - 1)
+        self.q, self.r = divmod(self.ftot, P)
+
+    def cost_start(self, p):
+        return p * self.q + (p * self.r) // self.P
+
+    def unit_at(self, c):
+        span = self.nt + self.alpha
+        g, rem = divmod(c, span)
+        return g * self.nt + min(rem, self.nt)
+
+    def start(self, p):
+        return self.unit_at(self.cost_start(p))
 
     def owner(self, x):
-        return min((((x + 1) * self.P) - 1) // self.work, self.P - 1)
+        fx = x + self.alpha * (x // self.nt)
+        return min(((fx + 1) * self.P - 1) // self.ftot, self.P - 1)
 
     def first(self, g):
         return self.owner(g * self.nt)
@@ -114,12 +132,14 @@ class Split:
         return self.owner((g + 1) * self.nt - 1)
 
 
-def plan(rows_pad, m_pad, ncu=256, per_cu=1):
+def plan(rows_pad, m_pad, ncu=256, per_cu=1, nc=4, alpha=None):
     nrb, nt = rows_pad // TILE, m_pad // TILE
     ngroups = -(-rows_pad // ROWS_PER_GROUP)
     work = ngroups * nt
-    P = max(1, min(ncu * per_cu, work))
-    s = Split(work, nt, P)
+    P = max(1, min(ncu * per_cu, 1024, work))
+    if alpha is None:
+        alpha = SEG_COST_STREAMED if nc <= STREAM_MAX_CHUNKS else SEG_COST_STAGED
+    s = Split(nt, ngroups, P, alpha)
     slots = max(s.last(g) - s.first(g) + 1 for g in range(ngroups))
     return nrb, nt, ngroups, s, slots
 
@@ -160,7 +180,7 @@ def emulate_lse(xa, ya, role=0, ncu=256, per_cu=1, c=np.log2(np.e), contraction=
     u_raw = np.where(np.arange(mp) < m, 0.0, -1.0e30).astype(np.float32)
     with np.errstate(over="ignore"):
         u = np.maximum((u_raw * sigma).astype(np.float32), PAD_SCORE)     # scaled column term, floored
-    nrb, nt, ngroups, s, slots = plan(rp, mp, ncu, per_cu)
+    nrb, nt, ngroups, s, slots = plan(rp, mp, ncu, per_cu, nc=nc)
     part = np.full((slots, rp, 2), np.nan)
     lane = np.arange(64)
     h = lane >> 5
@@ -171,8 +191,8 @@ def emulate_lse(xa, ya, role=0, ncu=256, per_cu=1, c=np.log2(np.e), contraction=
     ra, ca = (FIRST_, SECOND_) if role == 0 else (SECOND_, FIRST_)
     for b in range(s.P):
         p = xcd_contiguous(b, s.P)
-        u1 = (p + 1) * s.work // s.P
-        uu = p * s.work // s.P
+        u1 = s.start(p + 1)
+        uu = s.start(p)
         while uu < u1:
             g = uu // nt
             tb = uu - g * nt
@@ -280,23 +300,55 @@ def test_emulated_partial_and_finalize_match_logsumexp(rows, m, K, ncu, role, ct
                                  (100_000, 32), (2048, 2048), (1, 5)])
 @pytest.mark.parametrize("ncu,per_cu", [(256, 1), (304, 1), (80, 1), (256, 2)])
 def test_split_covers_work_and_slot_bounds(n, m, ncu, per_cu):
-    """The stream-K split at full sizes: units covered once, slot indexes below the planned slot count,
-    workgroup renumbering a bijection."""
+    """The stream-K split at full sizes: units covered once and each owned by the workgroup whose range holds
+    it, every slot a merge reads written by a workgroup with units in that row group, slot indexes below the
+    planned slot count, workgroup renumbering a bijection; all in 32-bit range."""
     rp, mp = pad_points(n), pad_points(m)
-    nrb, nt, ngroups, s, slots = plan(rp, mp, ncu, per_cu)
-    P = s.P
-    ids = sorted(xcd_contiguous(b, P) for b in range(P))
-    assert ids == list(range(P))
-    starts = [p * s.work // P for p in range(P + 1)]
-    assert starts[0] == 0 and starts[-1] == s.work
-    for g in range(ngroups):
-        p0, p1 = s.first(g), s.last(g)
-        assert starts[p0] <= g * nt < starts[p0 + 1] or starts[p0] == starts[p0 + 1] == g * nt
-        assert p1 - p0 + 1 <= slots
-        lo, hi = g * nt, (g + 1) * nt
-        owners = [p for p in range(P) if starts[p] < hi and starts[p + 1] > lo]
-        assert owners[0] >= p0 and owners[-1] <= p1
-    assert slots * rp * 8 < 2 ** 31 * 8
+    for nc in (4, 8):
+        nrb, nt, ngroups, s, slots = plan(rp, mp, ncu, per_cu, nc=nc)
+        P = s.P
+        assert s.ftot < 2 ** 31 and P <= 1024
+        ids = sorted(xcd_contiguous(b, P) for b in range(P))
+        assert ids == list(range(P))
+        starts = np.array([s.start(p) for p in range(P + 1)])
+        assert starts[0] == 0 and starts[-1] == s.work and (np.diff(starts) >= 0).all()
+        x = np.arange(s.work)
+        fx = x + s.alpha * (x // nt)
+        owner = np.minimum(((fx + 1) * P - 1) // s.ftot, P - 1)
+        assert (owner == np.searchsorted(starts, x, side="right") - 1).all()
+        for g in range(ngroups):
+            p0, p1 = s.first(g), s.last(g)
+            assert p1 - p0 + 1 <= slots
+            lo, hi = g * nt, (g + 1) * nt
+            for p in range(p0, p1 + 1):
+                assert starts[p] < hi and starts[p + 1] > lo and starts[p + 1] > starts[p], (g, p)
+        assert slots * rp * 8 < 2 ** 31 * 8
+
+
+def _costs(s, starts):
+    """Per workgroup: tiles + alpha * (row-group boundaries its range crosses)."""
+    out = []
+    for p in range(s.P):
+        a, b = starts[p], starts[p + 1]
+        segs = 0 if b == a else (b - 1) // s.nt - a // s.nt + 1
+        out.append(b - a + s.alpha * max(segs - 1, 0))
+    return np.array(out)
+
+
+def test_split_balances_segment_costs():
+    """Workgroups whose range crosses a row-group boundary get about alpha fewer tiles: every workgroup's cost
+    is within one tile plus alpha of ftot / P, and at 10k x 10k the largest cost is below the equal-tiles
+    split's."""
+    for n, m in [(10_000, 10_000), (7355, 8962), (65_536, 65_536), (2048, 2048), (300, 100_000)]:
+        rp, mp = pad_points(n), pad_points(m)
+        nrb, nt, ngroups, s, slots = plan(rp, mp, 256, 1, nc=4)
+        starts = [s.start(p) for p in range(s.P + 1)]
+        cost = _costs(s, starts)
+        assert cost.max() <= s.q + 1 + s.alpha, (n, m, cost.max(), s.q)
+        u = Split(nt, ngroups, s.P, 0)
+        uniform = _costs(Split(nt, ngroups, s.P, s.alpha), [p * u.work // s.P for p in range(s.P + 1)])
+        if (n, m) == (10_000, 10_000):
+            assert cost.max() < uniform.max(), (cost.max(), uniform.max())
 
 
 def test_scale_and_split2_error_bound():

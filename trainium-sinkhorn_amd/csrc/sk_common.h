@@ -41,24 +41,43 @@ enum Mode { kHalfStep = 0, kPlainLse = 1 };
 // requested together with the launch's other scalars.
 __device__ const int kNoSkip = 0;
 
-// Work split shared by the partial and the finalisation kernels: the (row group, column tile) units are
-// cut into P equal contiguous ranges, one per workgroup.
+// Work split shared by the partial and the merge kernels. The (row group, column tile) units are laid out on a
+// cost line: unit x of row group g = x / nt sits at position F(x) = x + alpha g, i.e. every row-group boundary
+// costs alpha positions, because a workgroup whose range crosses one starts a second segment (its row
+// operands, column terms and stores again: about alpha tiles of time). The line [0, ftot), ftot = work +
+// alpha (ngroups - 1), is cut into P equal pieces: workgroup p owns the units whose positions lie in
+// [C_p, C_(p+1)), C_p = floor(p ftot / P) = p q + floor(p r / P) with (q, r) = divmod(ftot, P). Everything is
+// 32-bit (ftot < 2^31 and P <= 1024, checked by the planner), so a kernel's prologue needs no 64-bit division.
 struct Split {
-    long long work;  // row groups * column tiles
-    int nt;          // column tiles
+    int nt;          // column tiles per row group
+    int ngroups;     // row groups
     int P;           // workgroups
+    int alpha;       // cost of a row-group boundary, in tiles
+    int ftot;        // ngroups * nt + alpha * (ngroups - 1)
+    int q, r;        // ftot = q P + r
 };
 
-// Workgroup p owns units [p * work / P, (p + 1) * work / P). The owner of unit x is the largest p with
-// floor(p * work / P) <= x, i.e. ((x + 1) * P - 1) / work.
-__host__ __device__ inline int owner_of(long long x, const Split& s) {
-    const long long p = ((x + 1) * (long long)s.P - 1) / s.work;
-    return (int)(p < s.P - 1 ? p : s.P - 1);
+// C_p, the first cost position of workgroup p (C_P = ftot).
+__host__ __device__ inline int cost_start(int p, const Split& s) { return p * s.q + (p * s.r) / s.P; }
+
+// The first unit at or after cost position c: inside a row group's span the unit at c, inside the boundary
+// gap after group g the first unit of group g + 1.
+__host__ __device__ inline int unit_at(int c, const Split& s) {
+    const int span = s.nt + s.alpha;
+    const int g = c / span, rem = c - g * span;
+    return g * s.nt + (rem < s.nt ? rem : s.nt);
 }
-__host__ __device__ inline int first_wg(int g, const Split& s) { return owner_of((long long)g * s.nt, s); }
-__host__ __device__ inline int last_wg(int g, const Split& s) {
-    return owner_of((long long)(g + 1) * s.nt - 1, s);
+
+// Workgroup p owns units [unit_at(C_p), unit_at(C_(p+1))). The owner of unit x is the largest p with
+// C_p <= F(x) (unit_at(C) <= x exactly when C <= F(x)), i.e. ((F(x) + 1) P - 1) / ftot.
+__host__ __device__ inline int owner_of(int x, const Split& s) {
+    const int fx = x + s.alpha * (x / s.nt);
+    const int p = fx < 0x7fffffff / s.P ? ((fx + 1) * s.P - 1) / s.ftot
+                                        : (int)((((long long)fx + 1) * s.P - 1) / s.ftot);
+    return p < s.P - 1 ? p : s.P - 1;
 }
+__host__ __device__ inline int first_wg(int g, const Split& s) { return owner_of(g * s.nt, s); }
+__host__ __device__ inline int last_wg(int g, const Split& s) { return owner_of((g + 1) * s.nt - 1, s); }
 
 // Tiles of a packed cloud (after its header) and its scale (1 for kBF16x3).
 template <class T>

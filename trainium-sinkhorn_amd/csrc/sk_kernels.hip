@@ -231,7 +231,14 @@ struct Plan {
     int nrb, nt, ngroups;
     Split s;
     int slots;       // partial slots per row
+    bool ok;         // the split fits 32-bit arithmetic (at most 2^31 - 1 cost positions)
 };
+
+// The cost of a row-group boundary in tiles (Split::alpha): what a second segment adds to a workgroup, its
+// row operands, column-term staging and stores, measured at about 3 us against 0.84 us per 32-column tile
+// (kp 64, 10k x 10k). TRNOPT_HIP_SEG_COST overrides it.
+constexpr int kSegCostStreamed = 4;
+constexpr int kSegCostStaged = 2;
 
 Plan make_plan(int rows_pad, int m_pad, int kp) {
     Plan pl;
@@ -239,16 +246,27 @@ Plan make_plan(int rows_pad, int m_pad, int kp) {
     pl.nrb = rows_pad / SK_TILE;
     pl.nt = m_pad / SK_TILE;
     pl.ngroups = (rows_pad + kRowsPerGroup - 1) / kRowsPerGroup;
-    pl.s.nt = pl.nt;
-    pl.s.work = (long long)pl.ngroups * pl.nt;
+    const long long work = (long long)pl.ngroups * pl.nt;
     int per_cu = env_int("TRNOPT_HIP_WG_PER_CU", 1);
     if (per_cu < 1 || per_cu > 4) per_cu = 1;
     long long P = (long long)cu_count() * per_cu;
-    if (P > pl.s.work) P = pl.s.work;
+    if (P > 1024) P = 1024;
+    if (P > work) P = work;
     if (P < 1) P = 1;
+    int alpha = env_int("TRNOPT_HIP_SEG_COST", pl.nc <= 4 ? kSegCostStreamed : kSegCostStaged);
+    if (alpha < 0 || alpha > 64) alpha = 0;
+    const long long ftot = work + (long long)alpha * (pl.ngroups - 1);
+    pl.s.nt = pl.nt;
+    pl.s.ngroups = pl.ngroups;
     pl.s.P = (int)P;
+    pl.s.alpha = alpha;
+    pl.s.ftot = (int)ftot;
+    pl.s.q = (int)(ftot / P);
+    pl.s.r = (int)(ftot % P);
+    pl.ok = ftot < 0x7fffffffLL;
     int slots = 1;
-    for (int g = 0; g < pl.ngroups; ++g) slots = std::max(slots, last_wg(g, pl.s) - first_wg(g, pl.s) + 1);
+    if (pl.ok)
+        for (int g = 0; g < pl.ngroups; ++g) slots = std::max(slots, last_wg(g, pl.s) - first_wg(g, pl.s) + 1);
     pl.slots = slots;
     return pl;
 }
@@ -400,6 +418,7 @@ size_t sk_row_lse_workspace_bytes(int rows, int m, int K) {
     if (rows < 1 || m < 1 || K < 1 || sk_pad_dim(K) > SK_KP_MAX) return 0;
     const int rp = sk_pad_points(rows), mp = sk_pad_points(m), kp = sk_pad_dim(K);
     const Plan pl = make_plan(rp, mp, kp);
+    if (!pl.ok) return 0;
     return align_up(packed_bf3_bytes(rows, K)) + align_up(packed_bf3_bytes(m, K)) + align_up((size_t)mp * 4) +
            partial_bytes(pl, rp);
 }
@@ -411,6 +430,7 @@ int sk_row_lse_f32(const float* xa, const float* ya, float* lse, int rows, int m
     if (rows < 1 || m < 1) return fail(SK_E_SHAPE, "sk_row_lse_f32: rows %d, m %d", rows, m);
     if (int r = check_kp(K)) return r;
     const size_t need = sk_row_lse_workspace_bytes(rows, m, K);
+    if (need == 0) return fail(SK_E_SHAPE, "sk_row_lse_f32: %d x %d is too large for one launch", rows, m);
     if (ws_bytes < need) return fail(SK_E_WORKSPACE, "sk_row_lse_f32: workspace %zu < %zu bytes", ws_bytes, need);
     if (((uintptr_t)ws & 255) != 0) return fail(SK_E_ARG, "sk_row_lse_f32: workspace must be 256-byte aligned");
     const int rp = sk_pad_points(rows), mp = sk_pad_points(m), kp = sk_pad_dim(K);
@@ -457,6 +477,7 @@ int sk_row_lse_f32(const float* xa, const float* ya, float* lse, int rows, int m
 size_t sk_half_step_workspace_bytes(int rows_pad, int m_pad, int d) {
     if (rows_pad < SK_TILE || m_pad < SK_TILE || d < 1 || sk_pad_dim(d) > SK_KP_MAX) return 0;
     const Plan pl = make_plan(rows_pad, m_pad, sk_pad_dim(d));
+    if (!pl.ok) return 0;
     return partial_bytes(pl, rows_pad);
 }
 
@@ -479,6 +500,7 @@ int sk_half_step_f32(const void* x_pk, const float* xsq, const float* off, int r
     if (!aligned16(x_pk) || !aligned16(y_pk) || !aligned16(gh) || !aligned16(log_b))
         return fail(SK_E_ARG, "sk_half_step_f32: packed clouds, gh and log_b must be 16-byte aligned");
     const size_t need = sk_half_step_workspace_bytes(rows_pad, m_pad, d);
+    if (need == 0) return fail(SK_E_SHAPE, "sk_half_step_f32: %d x %d is too large for one launch", rows_pad, m_pad);
     if (ws_bytes < need) return fail(SK_E_WORKSPACE, "sk_half_step_f32: workspace %zu < %zu bytes", ws_bytes, need);
     if (((uintptr_t)ws & 255) != 0) return fail(SK_E_ARG, "sk_half_step_f32: workspace must be 256-byte aligned");
     const Plan pl = make_plan(rows_pad, m_pad, sk_pad_dim(d));
@@ -511,6 +533,7 @@ size_t sk_loop_workspace_bytes(int nx_pad, int ny_pad, int d) {
     if (nx_pad < SK_TILE || ny_pad < SK_TILE || d < 1 || sk_pad_dim(d) > SK_KP_MAX) return 0;
     const int kp = sk_pad_dim(d);
     const Plan pf = make_plan(nx_pad, ny_pad, kp), pg = make_plan(ny_pad, nx_pad, kp);
+    if (!pf.ok || !pg.ok) return 0;
     return std::max(partial_bytes(pf, nx_pad), partial_bytes(pg, ny_pad)) +
            align_up((size_t)meas_count(ny_pad) * sizeof(float2)) + align_up(sizeof(int));
 }
@@ -549,6 +572,7 @@ int sk_loop_init_f32(const sk_loop_f32* L, void* stream) {
     if (int r = check_cloud(L->y, "y")) return r;
     if (int r = check_kp(L->d)) return r;
     const size_t need = sk_loop_workspace_bytes(L->x.npad, L->y.npad, L->d);
+    if (need == 0) return fail(SK_E_SHAPE, "sk_loop: %d x %d is too large for one launch", L->x.npad, L->y.npad);
     if (L->ws_bytes < need) return fail(SK_E_WORKSPACE, "sk_loop_init_f32: workspace %zu < %zu bytes", L->ws_bytes, need);
     if (((uintptr_t)L->ws & 255) != 0) return fail(SK_E_ARG, "sk_loop_init_f32: workspace must be 256-byte aligned");
     const LoopLayout lo = loop_layout(L);
@@ -566,6 +590,7 @@ int sk_loop_run_f32(const sk_loop_f32* L, int iters, void* stream) {
     if (int r = check_kp(L->d)) return r;
     if (iters < 0) return fail(SK_E_ARG, "sk_loop_run_f32: iters %d < 0", iters);
     const size_t need = sk_loop_workspace_bytes(L->x.npad, L->y.npad, L->d);
+    if (need == 0) return fail(SK_E_SHAPE, "sk_loop: %d x %d is too large for one launch", L->x.npad, L->y.npad);
     if (L->ws_bytes < need) return fail(SK_E_WORKSPACE, "sk_loop_run_f32: workspace %zu < %zu bytes", L->ws_bytes, need);
     if (((uintptr_t)L->ws & 255) != 0) return fail(SK_E_ARG, "sk_loop_run_f32: workspace must be 256-byte aligned");
     const int kp = sk_pad_dim(L->d);

@@ -77,13 +77,6 @@ __device__ __forceinline__ float max3(float a, float b, float c) {
     return r;
 }
 
-// A wave-uniform 64-bit value moved to scalar registers.
-__device__ __forceinline__ long long uniform64(long long v) {
-    const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)v);
-    const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)((unsigned long long)v >> 32));
-    return (long long)(((unsigned long long)hi << 32) | lo);
-}
-
 // Compile-time loop: f(integral_constant<int, i>) for i in [B, E).
 template <int B, int E, class F>
 __device__ __forceinline__ void static_for(F&& f) {
@@ -524,15 +517,14 @@ void lse_partial_kernel(PartialArgs a) {
     beta *= sigma;
     c *= inv_sigma;
 
-    // The 64-bit divisions below expand to vector code; their results are the same in every lane, and
-    // readfirstlane hands them to the scalar unit, so the tile loop's counters and operand addresses stay in
-    // scalar registers.
-    const long long u1 = uniform64((long long)(p + 1) * a.s.work / P);
-    for (long long u = uniform64((long long)p * a.s.work / P); u < u1;) {
-        const int g = __builtin_amdgcn_readfirstlane((int)(u / a.s.nt));
-        const int tb = (int)(u - (long long)g * a.s.nt);
-        const long long left = u1 - u;
-        const int te = left < (long long)(a.s.nt - tb) ? tb + (int)left : a.s.nt;
+    // The segment bounds are 32-bit integer arithmetic (the divisions expand to vector code); their results are
+    // the same in every lane, and readfirstlane hands them to the scalar unit, so the tile loop's counters and
+    // operand addresses stay in scalar registers.
+    const int u1 = __builtin_amdgcn_readfirstlane(unit_at(cost_start(p + 1, a.s), a.s));
+    for (int u = __builtin_amdgcn_readfirstlane(unit_at(cost_start(p, a.s), a.s)); u < u1;) {
+        const int g = __builtin_amdgcn_readfirstlane(u / a.s.nt);
+        const int tb = u - g * a.s.nt;
+        const int te = u1 - u < a.s.nt - tb ? tb + (u1 - u) : a.s.nt;
         const int slot = __builtin_amdgcn_readfirstlane(p - first_wg(g, a.s));
         // Waves past the last row block recompute it (their rows are not stored) so that every wave takes part
         // in the workgroup's barriers.

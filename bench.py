@@ -136,6 +136,7 @@ def profile_run(reps):
     Y = hk.HipCloud(y, np.full(M, -np.log(M)), dev, role=1)
     gh = torch.zeros(Y.npad, dtype=torch.float32, device=dev)
     sc = hk.scalars(EPS, 1.0, dev)
+    hk.bake_log2(X, Y, sc)               # as the loop does: scores in log2 units from the matrix cores
     out = torch.empty(X.npad, dtype=torch.float32, device=dev)
     for _ in range(reps):
         hk.half_step(X, Y, gh, sc, out=out)

@@ -16,7 +16,7 @@
  *     positive hipError_t for a runtime failure. sk_last_error() describes the last failure on the
  *     calling thread. Nothing aborts the process.
  *   - Point clouds are "packed": a header holding the cloud's power-of-two scale s (max |coordinate| * s
- *     in [2^13, 2^14)), then the points padded to a multiple of SK_TILE and the coordinates to
+ *     in [2^4, 2^5)), then the points padded to a multiple of SK_TILE and the coordinates to
  *     SK_KP_ALIGN, every scaled coordinate s x split into two fp16 pieces (within 2^-23 of s x), in the
  *     tile-interleaved order that the fp16 MFMA kernels read with one coalesced 16-byte load per lane
  *     (sk_pack_cloud_f32 builds it from a row-major (n, d) fp32 array; sk_packed_bytes gives its size).
@@ -37,8 +37,8 @@ extern "C" {
 
 #define SK_TILE 32            /* points per packed tile (one 32x32 MFMA output block) */
 #define SK_KP_ALIGN 16        /* coordinates are padded to a multiple of this (one fp16 MFMA K chunk) */
-#define SK_PACKED_BYTES_PER_COORD 4   /* two fp16 pieces per padded coordinate */
-#define SK_PACKED_HEADER_BYTES 256    /* before the tiles: max |coordinate| and the scale */
+#define SK_PACKED_BYTES_PER_COORD 8   /* two fp16 pieces per padded coordinate, twice: own scale, log2 copy */
+#define SK_PACKED_HEADER_BYTES 256    /* before the tiles: max |coordinate|, the scale, the log2 copy's tag */
 #define SK_KP_MAX 128         /* largest padded dimension the kernels are built for */
 #define SK_PAD_LOG_WEIGHT (-1e9)  /* log weight of a padding point (src/trnopt/sinkhorn.py:59) */
 
@@ -68,6 +68,20 @@ int sk_pad_dim(int d);         /* d rounded up to a multiple of SK_KP_ALIGN */
  */
 size_t sk_packed_bytes(int n, int d);
 int sk_pack_cloud_f32(const float* pts, int n, int d, int ld, void* out, void* stream);
+
+/*
+ * The log2-unit copy of the first cloud of a pair (the x of a solve, rows_role 0), stored in the second
+ * half of its packed buffer: every coordinate x as two fp16 pieces of fl(c x) / s2, c = sc[0] log2(e) =
+ * (2 / eps) log2(e) for sc = {2/eps, ...} on the device, s2 the second cloud's scale. Half-steps over this
+ * pair with the same sc[0] then read the scores in log2 units straight from the matrix cores (one VALU
+ * multiply less per score, same accuracy, the two directions still bit-identical); with any other sc[0],
+ * or a copy made against another second cloud, they scale on the VALU as before. The copy is not made
+ * (and the pair keeps scaling on the VALU) when max |fl(c x)| / s2 falls outside [2^-1, 2^15). One launch.
+ * sk_loop_init_f32 makes it for the loop's first eps and the loop remakes it when eps changes; a caller of
+ * sk_half_step_f32 may make it once per eps. No counterpart in the reference (an fp32-MFMA-free way to
+ * apply its 1/eps scaling, src/trnopt/nki_sinkhorn.py:197-210).
+ */
+int sk_bake_log2_f32(void* first_pk, const void* second_pk, int n_first, int d, const float* sc, void* stream);
 
 /*
  * Row-wise log-sum-exp of a matrix product (the core of the fused kernel):
@@ -118,7 +132,7 @@ int sk_half_step_f32(const void* x_pk, const float* xsq, const float* off, int r
  * g update, stage advance, balanced / unbalanced checks every check_every iterations, fp32 floors).
  */
 typedef struct sk_cloud_f32 {
-    const void* pk;       /* packed points (sk_pack_cloud_f32 layout) */
+    const void* pk;       /* packed points (sk_pack_cloud_f32 layout); the loop rewrites x's log2-unit copy */
     const float* sq;      /* |p|^2 (npad), float64 sums cast to fp32 (src/trnopt/sinkhorn.py:149) */
     const float* log_w;   /* log weights (npad), padding SK_PAD_LOG_WEIGHT */
     const float* w;       /* exp(log_w) (npad), padding 0 */
@@ -163,7 +177,8 @@ typedef struct sk_loop_f32 {
 } sk_loop_f32;
 
 size_t sk_loop_workspace_bytes(int nx_pad, int ny_pad, int d);
-/* Write the initial state (it = 0, first eps and its scalars). */
+/* Write the initial state (it = 0, first eps and its scalars); make x's log2-unit copy for that eps
+ * (sk_bake_log2_f32) and the loop's log2-unit potentials (c / 2) fh, (c / 2) gh in ws from fh and gh. */
 int sk_loop_init_f32(const sk_loop_f32* L, void* stream);
 /* Enqueue `iters` iterations (f update, g update with the loop control in its merge: four launches each);
  * iterations after `done` do nothing. ws (sk_loop_workspace_bytes) must be 256-byte aligned. */

@@ -132,32 +132,111 @@ def test_errors_are_reported_not_fatal(hip):
         hip.row_lse(torch.zeros(3, 200, device=DEV), torch.zeros(4, 200, device=DEV))
 
 
-def _dots_by_half_step(hip, rows_pts, rows_role, col_pt):
-    """x_i . y for every row i and one column point y, read exactly off a half-step: one real column (log b = 0,
-    gh = 0, the padding columns weigh exactly 0), |x|^2 = 0, eps = 1, kappa = 1 gives fh_i = -2 x_i . y."""
-    n, d = rows_pts.shape
-    R = hip.HipCloud(rows_pts, np.zeros(n), DEV, role=rows_role)
-    C = hip.HipCloud(col_pt[None, :], np.zeros(1), DEV, role=1 - rows_role)
+def _masked_dots(hip, X, Y, rows_role, k, sc, bake=True):
+    """x_i . y_k (rows_role 0) or y_j . x_k (rows_role 1) for all rows, read off a half-step of the pair whose
+    column cloud weighs exactly 0 except at column k (log weight 0), with gh = 0 and |rows|^2 = 0: fh = -2 dot.
+    With bake, the first cloud's log2-unit copy is made first. Returns the dots and the first cloud's tag."""
+    R, C = (X, Y) if rows_role == 0 else (Y, X)
+    lw = np.full(C.n, -1e9)
+    lw[k] = 0.0
+    Ck = hip.HipCloud(C._pts, lw, DEV, role=C.role)
+    first, second = (R, Ck) if rows_role == 0 else (Ck, R)
+    if bake:
+        hip.bake_log2(first, second, sc)
+    sq = R.sq.clone()
     R.sq.zero_()
-    gh = torch.zeros(C.npad, dtype=torch.float32, device=DEV)
-    out = hip.half_step(R, C, gh, hip.scalars(1.0, 1.0, DEV)).cpu().numpy()[:n]
-    return -0.5 * out
+    out = hip.half_step(R, Ck, torch.zeros(Ck.npad, dtype=torch.float32, device=DEV), sc)
+    R.sq.copy_(sq)
+    return -0.5 * out.cpu().numpy()[:R.n], _log2_tag(first)
 
 
 @pytest.mark.parametrize("d", [3, 16, 64, 100, 128])
 def test_f_and_g_updates_form_bit_identical_dots(hip, d):
-    """The f update (rows x, role 0) and the g update (rows y, role 1) issue the piece products in the same
-    order: x_i . y_j agrees bit for bit in both directions, and is fp32-accurate."""
+    """The f update (rows x, role 0) and the g update (rows y, role 1) of one pair of clouds issue the piece
+    products in the same order: x_i . y_j agrees bit for bit in both directions, and is fp32-accurate."""
     rng = np.random.default_rng(d)
-    x = rng.normal(size=(70, d)).astype(np.float32)
-    y = (rng.normal(size=(40, d)) * 1.7 + 0.3).astype(np.float32)
+    x = rng.normal(size=(70, d))
+    y = rng.normal(size=(40, d)) * 1.7 + 0.3
+    X = hip.HipCloud(x, np.zeros(70), DEV, role=0)
+    Y = hip.HipCloud(y, np.zeros(40), DEV, role=1)
+    X._pts, Y._pts = x, y
+    sc = hip.scalars(1.0, 1.0, DEV)
     for j in (0, 7, 39):
-        f_side = _dots_by_half_step(hip, x, 0, y[j])                     # x_i . y_j, i = 0..69
+        f_side, tag = _masked_dots(hip, X, Y, 0, j, sc, bake=False)
+        assert tag == 0.0
         for i in (0, 33, 69):
-            g_side = _dots_by_half_step(hip, y, 1, x[i])                 # y_j' . x_i, j' = 0..39
-            assert f_side[i].tobytes() == np.float32(g_side[j]).tobytes(), (i, j, f_side[i], g_side[j])
-        exact = x.astype(np.float64) @ y[j].astype(np.float64)
-        bound = np.abs(x.astype(np.float64)) @ np.abs(y[j].astype(np.float64))
+            g_side, _ = _masked_dots(hip, X, Y, 1, i, sc, bake=False)
+            assert np.float32(f_side[i]).tobytes() == np.float32(g_side[j]).tobytes(), (i, j, f_side[i], g_side[j])
+        exact = x.astype(np.float32).astype(np.float64) @ y[j].astype(np.float32).astype(np.float64)
+        bound = np.abs(x) @ np.abs(y[j])
+        assert np.all(np.abs(f_side - exact) <= 4e-7 * bound + 1e-30)
+
+
+def _log2_tag(cloud):
+    """The packed header's log2-copy tag: the score scale the copy was made for (0: none)."""
+    return float(cloud.pk[8:12].cpu().numpy().view(np.float32)[0])
+
+
+@pytest.mark.parametrize("rows,m,d,eps,kappa,mag", [(137, 91, 5, 0.1, 1.0, 1.0), (1300, 1700, 50, 0.05, 0.9, 1.0),
+                                                    (2048, 2048, 64, 0.1, 1.0, 1.0), (333, 4000, 30, 0.01, 1.0, 0.3),
+                                                    (64, 64, 128, 0.5, 0.7, 1.0), (500, 600, 16, 0.1, 1.0, 1e3)])
+def test_half_step_with_log2_copy_matches_float64(hip, rows, m, d, eps, kappa, mag):
+    """With the first cloud's log2-unit copy the half-step (both directions) meets the same float64 known answer
+    as without it and agrees with the VALU-scaled result to rounding; where the copy cannot fit fp16 (mag 1e3 at
+    eps 0.1) it is not made and the half-step scales on the VALU."""
+    x, y, gh, log_b, off = _half_inputs(rows, m, d, eps, seed=rows + 7 * m + d)
+    x, y, gh = x * mag, y * mag, gh * mag * mag
+    la = np.log(np.full(rows, 1.0 / rows))
+    X = hip.HipCloud(x, la, DEV, off=off, role=0)
+    Y = hip.HipCloud(y, log_b, DEV, role=1)
+    sc = hip.scalars(eps, kappa, DEV)
+    ghp = torch.zeros(Y.npad, dtype=torch.float32, device=DEV)
+    ghp[:m] = torch.as_tensor(gh, dtype=torch.float32)
+    fhp = torch.zeros(X.npad, dtype=torch.float32, device=DEV)
+    fhp[:rows] = torch.as_tensor(np.random.default_rng(rows).normal(scale=2.0, size=rows) * mag * mag - 0.5 * (x * x).sum(1),
+                                 dtype=torch.float32)
+    print(f"log2 copy rows={rows} m={m} d={d} eps={eps} mag={mag}", flush=True)
+    f_vpu = hip.half_step(X, Y, ghp, sc).cpu().numpy()[:rows].astype(np.float64)
+    g_vpu = hip.half_step(Y, X, fhp, sc).cpu().numpy()[:m].astype(np.float64)
+    hip.bake_log2(X, Y, sc)
+    torch.cuda.synchronize()
+    made = _log2_tag(X) != 0.0
+    assert made == (mag == 1.0 or mag == 0.3), _log2_tag(X)
+    f_l2 = hip.half_step(X, Y, ghp, sc).cpu().numpy()[:rows].astype(np.float64)
+    g_l2 = hip.half_step(Y, X, fhp, sc).cpu().numpy()[:m].astype(np.float64)
+    x32, y32 = x.astype(np.float32), y.astype(np.float32)
+    k32 = float(np.float32(kappa))
+    f_want = brute.half_step_f64(x32, (x * x).sum(1).astype(np.float32), off.astype(np.float32), y32,
+                                 gh.astype(np.float32), log_b.astype(np.float32), eps, k32)
+    g_want = brute.half_step_f64(y32, (y * y).sum(1).astype(np.float32), np.zeros(m), x32,
+                                 fhp.cpu().numpy()[:rows], la.astype(np.float32), eps, k32)
+    for got, vpu, want in ((f_l2, f_vpu, f_want), (g_l2, g_vpu, g_want)):
+        assert inf_rel(got, want) < 2e-6, (inf_rel(got, want), inf_rel(vpu, want))
+        assert inf_rel(got, vpu) < 2e-6
+        if not made:
+            assert np.array_equal(got, vpu)
+
+
+@pytest.mark.parametrize("d", [3, 16, 64, 128])
+def test_log2_copy_keeps_f_and_g_dots_bit_identical(hip, d):
+    """On the log2-unit copy the f update (rows x) and the g update (rows y) of one pair of clouds still form
+    every x_i . y_j bit for bit alike (read back through the merge's division by c), fp32-accurate."""
+    rng = np.random.default_rng(100 + d)
+    x = rng.normal(size=(70, d))
+    y = rng.normal(size=(40, d)) * 1.7 + 0.3
+    X = hip.HipCloud(x, np.zeros(70), DEV, role=0)
+    Y = hip.HipCloud(y, np.zeros(40), DEV, role=1)
+    X._pts, Y._pts = x, y
+    sc = hip.scalars(0.5, 1.0, DEV)
+    for j in (0, 7, 39):
+        f_side, tag = _masked_dots(hip, X, Y, 0, j, sc)
+        assert tag != 0.0
+        for i in (0, 33, 69):
+            g_side, tag = _masked_dots(hip, X, Y, 1, i, sc)
+            assert tag != 0.0
+            assert np.float32(f_side[i]).tobytes() == np.float32(g_side[j]).tobytes(), (i, j, f_side[i], g_side[j])
+        exact = x.astype(np.float32).astype(np.float64) @ y[j].astype(np.float32).astype(np.float64)
+        bound = np.abs(x) @ np.abs(y[j])
         assert np.all(np.abs(f_side - exact) <= 4e-7 * bound + 1e-30)
 
 

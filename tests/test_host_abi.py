@@ -68,7 +68,7 @@ def test_constants_match_the_header(hk):
         assert lb.sk_pad_points(n) == hk.pad_points(n)
     for d in (1, 7, 8, 30, 64, 65, 128):
         assert lb.sk_pad_dim(d) == hk.pad_dim(d)
-        assert lb.sk_packed_bytes(1000, d) == hk.packed_bytes(1000, d) == 256 + 1024 * hk.pad_dim(d) * 4
+        assert lb.sk_packed_bytes(1000, d) == hk.packed_bytes(1000, d) == 256 + 1024 * hk.pad_dim(d) * 8
     assert lb.sk_packed_bytes(10, 129) == 0 and lb.sk_packed_bytes(0, 8) == 0
 
 

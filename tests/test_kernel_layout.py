@@ -34,11 +34,11 @@ def pad_dim(d):
 
 
 def pack_scale(m):
-    """The power-of-two scale of a cloud with max |coordinate| m: m * s in [2^13, 2^14), clamped."""
+    """The power-of-two scale of a cloud with max |coordinate| m: m * s in [2^4, 2^5), clamped."""
     if not m > 0:
         return np.float32(1.0)
     e = np.frexp(np.float32(m))[1]                      # m in [2^(e-1), 2^e)
-    k = -32 if e > 46 else (40 if e < -26 else 14 - e)
+    k = -32 if e > 37 else (40 if e < -35 else 5 - e)
     return np.float32(np.ldexp(1.0, k))
 
 
@@ -353,11 +353,12 @@ def test_split_balances_segment_costs():
 
 def test_scale_and_split2_error_bound():
     rng = np.random.default_rng(1)
-    for mag in (1.0, 1e-3, 7.3e4, 1e-7, 3e12):        # the full-precision range: max |x| in [2^-26, 7e13]
+    for mag in (1.0, 1e-3, 7.3e4, 1e-7, 3e12, 1e-10):  # the full-precision range: max |x| in [2^-35, 7e13]
         x = (rng.normal(size=100_000) * mag).astype(np.float32)
         s = pack_scale(np.abs(x).max())
         scaled_max = np.abs(x).max() * s
-        assert (2.0 ** 13 <= scaled_max < 2.0 ** 14) or (s == 2.0 ** 40 and scaled_max < 2.0 ** 13)
+        assert ((2.0 ** 4 <= scaled_max < 2.0 ** 5) or (s == 2.0 ** 40 and scaled_max < 2.0 ** 4)
+                or (s == 2.0 ** -32 and 2.0 ** 5 <= scaled_max < 2.0 ** 14))
         v = (x * s).astype(np.float32)
         np.testing.assert_array_equal(v.astype(np.float64), x.astype(np.float64) * float(s))   # exact scaling
         a0, a1 = split2(v)
@@ -404,6 +405,63 @@ def test_three_products_are_fp32_accurate_and_symmetric():
     # a rule that does not transpose the piece order for role 1 adds the cross terms in another order
     g_wrong = accumulate(1, ys, xs, swap_rule=False)
     assert np.abs(f - g_wrong.T).max() > 0
+
+
+def bake_log2(xs, sx, sy, mx, c):
+    """sk_epilogue.h bake_params / bake_unit: the first cloud's log2-unit copy, pieces of fl(c x) / s_y where
+    x = (x0 + x1) / s_x; None where the copy would leave fp16's full-precision range."""
+    c = np.float32(c)
+    wmax = np.float32(np.float32(c * np.float32(mx)) * np.float32(1.0 / sy))
+    if not (c > 0 and 0.5 <= wmax < 32768.0):
+        return None
+    x = ((xs[0] + xs[1]).astype(np.float32) * np.float32(1.0 / sx)).astype(np.float32)
+    w = ((c * x).astype(np.float32) * np.float32(1.0 / sy)).astype(np.float32)
+    return split2(w)
+
+
+@pytest.mark.parametrize("eps,shift", [(0.1, 0.5), (0.01, 0.0), (1.0, 0.0), (0.05, 3.0)])
+def test_log2_copy_gives_c_x_dot_y_to_fp32_accuracy(eps, shift):
+    """With the first cloud's log2-unit copy, the three piece products against the second cloud's own pieces
+    sum to c x.y (c = fp32(2/eps) log2 e, the kernels' score scale) with no scaling left: as accurate as the
+    own-scale contraction times c, the transposed product order still adds the same terms in the same order,
+    and the per-score VALU form exp2(a - m) equals exp2(c (a_acc - m_acc)) to rounding."""
+    rng = np.random.default_rng(3)
+    x = rng.normal(size=(60, 64)).astype(np.float32)
+    y = (rng.normal(size=(50, 64)) + shift).astype(np.float32)
+    sx, sy = pack_scale(np.abs(x).max()), pack_scale(np.abs(y).max())
+    xs, ys = split2(x * sx), split2(y * sy)
+    c = np.float32(np.float32(2.0 / eps) * np.float32(np.log2(np.e)))
+    ws = bake_log2(xs, sx, sy, np.abs(x).max(), c)
+    assert ws is not None
+    for p in range(2):
+        np.testing.assert_array_equal(ws[p], ws[p].astype(np.float16).astype(np.float32))
+    exact = float(c) * (x.astype(np.float64) @ y.astype(np.float64).T)
+    bound = float(c) * (np.abs(x.astype(np.float64)) @ np.abs(y.astype(np.float64)).T)
+    approx = sum(ws[FIRST[p]].astype(np.float64) @ ys[SECOND[p]].astype(np.float64).T for p in range(3))
+    err = np.max(np.abs(approx - exact) / bound)
+    assert err < 2.0 ** -21, err
+    assert err < np.max(np.abs(float(c) * (x @ y.T).astype(np.float64) - exact) / bound)    # c times an fp32 dot
+
+    def accumulate(rows, cols, ra, ca):
+        acc = np.zeros((rows[0].shape[0], cols[0].shape[0]), dtype=np.float32)
+        for p in range(3):
+            acc = (acc + (rows[ra[p]].astype(np.float64) @ cols[ca[p]].astype(np.float64).T).astype(np.float32))
+        return acc
+
+    np.testing.assert_array_equal(accumulate(ws, ys, FIRST, SECOND), accumulate(ys, ws, SECOND, FIRST).T)
+
+
+def test_log2_copy_validity_window():
+    """The copy is made only while max |fl(c x)| / s_y stays in [2^-1, 2^15); outside it the pair scales on
+    the VALU (header tag 0)."""
+    rng = np.random.default_rng(4)
+    y = rng.normal(size=(20, 8)).astype(np.float32)
+    sy = pack_scale(np.abs(y).max())
+    for mag, c, ok in [(1.0, 28.85, True), (1e-6, 28.85, False), (1e6, 288.5, False), (30.0, 2.885, True),
+                       (1.0, 0.0, False)]:
+        x = (rng.normal(size=(20, 8)) * mag).astype(np.float32)
+        sx = pack_scale(np.abs(x).max())
+        assert (bake_log2(split2(x * sx), sx, sy, np.abs(x).max(), c) is not None) == ok, (mag, c)
 
 
 @pytest.mark.parametrize("ct", ["f16x2", "bf16x3"])

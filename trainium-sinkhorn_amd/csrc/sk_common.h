@@ -30,8 +30,7 @@ constexpr int kMaxChunks = 8;          // K chunks of 16 coordinates: kp = 16 * 
 //              (exact over the whole fp32 range), six products (6 bytes per coordinate).
 enum Contraction { kF16x2 = 0, kBF16x3 = 1 };
 constexpr int pieces_of(int ct) { return ct == kF16x2 ? 2 : 3; }
-constexpr int kHeaderBytes = 256;      // packed cloud header: [0] max |coordinate| (as uint), [1] scale (float)
-constexpr float kScaleTarget = 16384.0f;   // the scale puts max |coordinate| in [2^13, 2^14)
+constexpr int kHeaderBytes = 256;      // packed cloud header (layout below, packed_tiles)
 constexpr float kMaxAbsCoordinate = 7.0e13f; // above this the scaled coordinates would not fit fp16
 constexpr float kPadScore = -1.0e30f;  // floor of a (scaled) column term: padding, never -inf
 
@@ -79,12 +78,30 @@ __host__ __device__ inline int owner_of(int x, const Split& s) {
 __host__ __device__ inline int first_wg(int g, const Split& s) { return owner_of(g * s.nt, s); }
 __host__ __device__ inline int last_wg(int g, const Split& s) { return owner_of((g + 1) * s.nt - 1, s); }
 
-// Tiles of a packed cloud (after its header) and its scale (1 for kBF16x3).
+// A packed cloud: a 256-byte header of 32-bit words
+//     [0] max |coordinate| (float bits), [1] s, the power-of-two scale of the cloud's own pieces (1 for kBF16x3),
+//     [2] c_b, the score scale its log2-unit copy was made for (0: no valid copy),
+//     [3] the scale of the second cloud that copy was made against,
+// then the tiles of the cloud's own pieces (s x), then (kF16x2 only) the tiles of its log2-unit copy: two fp16
+// pieces of fl(c_b x) / s_2 per coordinate, which the first cloud of a pair carries so that its piece products
+// with the second cloud's own pieces sum to c_b x.y, the half-step's score in log2 units (see bake_log2).
 template <class T>
 __host__ __device__ inline const T* packed_tiles(const void* pk) {
     return reinterpret_cast<const T*>(reinterpret_cast<const char*>(pk) + kHeaderBytes);
 }
+// The log2-unit copy of a kF16x2 cloud of npad points and nc K chunks.
+template <class T>
+__host__ __device__ inline const T* packed_log2_tiles(const void* pk, int npad, int nc) {
+    return packed_tiles<T>(pk) + (size_t)(npad / 32) * nc * 2 * 64;
+}
 __device__ inline float packed_scale(const void* pk) { return reinterpret_cast<const float*>(pk)[1]; }
+
+// The half-step may take its scores in log2 units from the matrix cores when the first cloud's log2-unit copy
+// was made for this score scale c = (2 / eps) log2(e) and against this second cloud (its scale).
+__device__ inline bool log2_ready(const void* first, const void* second, float c) {
+    const float* h = reinterpret_cast<const float*>(first);
+    return h[2] != 0.0f && h[2] == c && h[3] == packed_scale(second);
+}
 
 // The on-device loop's configuration (src/trnopt/sinkhorn.py:313-320, 340-344).
 struct LoopCfg {
@@ -100,6 +117,7 @@ struct PartialArgs {
     const void* yc;     // packed columns
     const float* u;     // column term = alpha * u + beta * v  (m_pad each)
     const float* v;
+    float* u2;          // or null: the column cloud's potential in log2 units, (c / 2) u (on-device loop)
     const float* sc;    // {2/eps, 1/eps, eps, kappa} (half-step mode)
     const int* skip;
     float2* part;       // [slot][rows_pad] partial (M, S): M = max_j a_ij, S = sum_j exp2(c (a_ij - M))
@@ -108,20 +126,24 @@ struct PartialArgs {
     int mode;
     int rows_role;      // 0: the rows are the first cloud of the pair, 1: the second (piece order)
     int contraction;    // kF16x2 or kBF16x3 (the packing of both clouds)
+    int nc;             // K chunks of 16 coordinates
     Split s;
     // The merge pass (one workgroup per row group):
     const float* xsq;   // |x|^2 (half-step epilogue)
     const float* off;   // log(target / weight) or null
     float* out;         // merged result (fh, or the plain row-LSE)
+    float* out2;        // or null: with log2-unit scores, also the result in log2 units, (c / 2) fh
     int n_store;        // rows of out written
     float2* meas;       // per-group convergence partials (g update of the loop), or null
     const float* w;     // row weights, with meas
     int n_real;         // real rows, with meas
     int* counters;      // with state: one arrival counter, zero on entry and left zero
     int ngroups;
-    // ... and, in the last merge workgroup of a g update, the loop control (null: none).
+    // ... and, in the last merge workgroup of a g update, the loop control (null: none), which also remakes the
+    // log2-unit copy of the first cloud (rebake, the packed first cloud; null: never) when eps changes.
     sk_state* state;
     LoopCfg cfg;
+    char* rebake;
 };
 
 // Launch the partial kernel for kp = 16 * nc on P workgroups (nc <= 4: launch_partial_small, else

@@ -13,6 +13,56 @@ constexpr float kDeltaCap = 50.0f;     // cap of (g_old - g_new) / eps in the ba
 __device__ __forceinline__ float ep_ex2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float ep_lg2(float x) { return __builtin_amdgcn_logf(x); }
 
+// The first cloud's log2-unit copy for score scale c = (2 / eps) log2(e) = sc[0] log2(e), against the second
+// cloud's scale s2: every coordinate x, as the cloud's own pieces hold it (x = (v0 + v1) / s1, exact), becomes
+// w = fl(c x) / s2 in two fp16 pieces (w0 = fp16(w), w1 = fp16(w - w0)). Products with the second cloud's own
+// pieces (s2 y) then sum to c x.y in fp32, the score in log2 units, so the exponentials need no scaling; the
+// f and g updates both use this copy, in the same product order, and stay bit-identical. The copy is valid
+// (header c_b = c, [3] = s2) when max |w| = fl(c max |x|) / s2 lies in [2^-1, 2^15): within fp16's range
+// and with w1 normal for the largest coordinates; otherwise c_b = 0 and the half-steps scale on the VALU.
+struct BakeParams {
+    float c, inv_s1, inv_s2;
+    bool valid;
+};
+
+__device__ inline BakeParams bake_params(const void* first, const void* second, const float* sc) {
+    const float* h1 = reinterpret_cast<const float*>(first);
+    BakeParams b;
+    b.c = sc[0] * kLog2e;                                   // as the half-step kernels form it
+    const float s1 = h1[1], s2 = packed_scale(second);
+    b.inv_s1 = 1.0f / s1;                                   // powers of two: exact
+    b.inv_s2 = 1.0f / s2;
+    const float wmax = (b.c * __uint_as_float(reinterpret_cast<const unsigned*>(first)[0])) * b.inv_s2;
+    b.valid = b.c > 0.0f && wmax >= 0.5f && wmax < 32768.0f;
+    return b;
+}
+
+// One 16-byte unit (8 coordinates of one tile row half, one K chunk) of the copy.
+__device__ inline void bake_unit(char* first, long long idx, int npad, int nc, const BakeParams& b) {
+    const f16x8* own = reinterpret_cast<const f16x8*>(first + kHeaderBytes);
+    f16x8* cp = reinterpret_cast<f16x8*>(first + kHeaderBytes) + (size_t)(npad / SK_TILE) * nc * 2 * 64;
+    const int lane = (int)(idx % 64);
+    const long long tc = idx / 64;                          // tile * nc + chunk
+    const f16x8 p0 = own[tc * 128 + lane], p1 = own[tc * 128 + 64 + lane];
+    f16x8 q0, q1;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float x = ((float)p0[e] + (float)p1[e]) * b.inv_s1;
+        const float w = (b.c * x) * b.inv_s2;
+        const _Float16 a0 = (_Float16)w;
+        q0[e] = a0;
+        q1[e] = (_Float16)(w - (float)a0);
+    }
+    cp[tc * 128 + lane] = q0;
+    cp[tc * 128 + 64 + lane] = q1;
+}
+
+__device__ inline void bake_header(char* first, const void* second, const BakeParams& b) {
+    float* h = reinterpret_cast<float*>(first);
+    h[2] = b.valid ? b.c : 0.0f;
+    h[3] = packed_scale(second);
+}
+
 // eps of the iteration that starts with `it` iterations done (sinkhorn.py:347-350).
 __device__ inline double eps_for(const LoopCfg& c, int it, int stage) {
     if (c.n_stages > 0) return stage < c.n_stages ? c.stages[stage] : c.eps;
@@ -36,6 +86,9 @@ __device__ inline void set_scalars(sk_state* st, double e, double rho_x, double 
 
 // Merge the slots of row i = 256 g + threadIdx.x (one row per thread of the workgroup) and apply the epilogue:
 //     lse = (2 / eps) M + ln S  (half-step, accumulator units) or M + ln S  (plain row-LSE)
+// When the partial kernel took its scores in log2 units (log2_ready: the same test on the same headers), the
+// slots hold M in log2 units: they merge without c, and M / c (correctly rounded, so that no constant factor
+// enters the potentials) gives the accumulator units.
 //     fh  = kappa ((|x|^2 + eps off) - eps lse) - |x|^2
 // With meas, also the group's convergence partials {max_{i<n_real} |new - old|, sum_i |w (exp(min((old -
 // new) / eps, 50)) - 1)|} (sinkhorn.py:360, 368-373), reduced in a fixed order into meas[g].
@@ -45,6 +98,10 @@ __device__ inline bool merge_group(const PartialArgs& a, int g) {
     const int i = g * kRowsPerGroup + (int)threadIdx.x;
     const int* skip_p = a.skip != nullptr ? a.skip : &kNoSkip;
     const float sc0 = a.sc[0], sc1 = a.sc[1], sc2 = a.sc[2], sc3 = a.sc[3];   // valid in both modes
+    const void* first = a.rows_role == 0 ? a.xr : a.yc;
+    const void* second = a.rows_role == 0 ? a.yc : a.xr;
+    const float c_hs = sc0 * kLog2e;
+    const bool l2 = a.mode == kHalfStep && a.contraction == kF16x2 && log2_ready(first, second, c_hs);
     const int ic = i < a.rows_pad ? i : a.rows_pad - 1;
     const float x2 = a.mode == kHalfStep ? a.xsq[ic] : 0.0f;
     const float o = a.off != nullptr ? a.off[ic] : 0.0f;
@@ -53,7 +110,7 @@ __device__ inline bool merge_group(const PartialArgs& a, int g) {
     const int skip = *skip_p;
     asm volatile("" ::"s"(sc0), "s"(sc1), "s"(sc2), "s"(sc3), "v"(x2), "v"(o), "v"(old), "v"(wi), "v"(skip));
     if (skip != 0) return false;
-    const float c = a.mode == kHalfStep ? sc0 * kLog2e : kLog2e;
+    const float c = l2 ? 1.0f : a.mode == kHalfStep ? c_hs : kLog2e;
     float dmax = 0.0f;
     double derr = 0.0;
     if (i < a.rows_pad) {
@@ -75,12 +132,25 @@ __device__ inline bool merge_group(const PartialArgs& a, int g) {
             M = Mn;
             S = Sn;
         }
-        // the max enters exactly, in accumulator units
         const float l2s = ep_lg2(S);
         if (a.mode == kHalfStep) {
             const float eps = sc2, kappa = sc3;
-            const float eps_lse = 2.0f * M + (eps * kLn2) * l2s;
-            const float val = kappa * ((x2 + eps * o) - eps_lse) - x2;
+            float val;
+            if (l2 && a.out2 != nullptr) {
+                // In log2 units, R = (c / 2) fh (the loop's state): (c / 2) eps lse = M + log2 S exactly in the
+                // mathematics, so R = kappa ((X2 + O) - (M + log2 S)) - X2 with X2 = (c / 2) |x|^2 and
+                // O = log2(e) off: sums only, as the accumulator-unit form below, and fh = R / (c / 2).
+                const float k2 = 0.5f * c_hs;
+                const float X2 = x2 * k2;
+                const float val2 = kappa * ((X2 + o * kLog2e) - (M + l2s)) - X2;
+                val = __fdiv_rn(val2, k2);
+                if (i < a.n_store) a.out2[i] = val2;
+            } else {
+                // the max enters exactly, in accumulator units (log2-unit slots: M / c, correctly rounded)
+                const float Ma = l2 ? __fdiv_rn(M, c_hs) : M;
+                const float eps_lse = 2.0f * Ma + (eps * kLn2) * l2s;
+                val = kappa * ((x2 + eps * o) - eps_lse) - x2;
+            }
             if (a.meas != nullptr) {
                 if (i < a.n_real) dmax = fabsf(val - old);
                 const float delta = fminf((old - val) * sc1, kDeltaCap);
@@ -180,8 +250,48 @@ __global__ __launch_bounds__(kRowsPerGroup) void merge_kernel(PartialArgs a) {
     __syncthreads();
     if (s_last == 0) return;
     __threadfence();                       // acquire: every group's meas
+    // The loop control, by the first wave; thread 0 keeps the scalars of the iteration that ran and hands the next
+    // iteration's over through LDS.
+    __shared__ float s_sc[4];
+    __shared__ float s_sc0_ran;
+    __shared__ int s_done;
+    if (threadIdx.x == 0) s_sc0_ran = a.state->sc_x[0];
     if (threadIdx.x < 64) control_step(a.state, a.meas, a.ngroups, a.cfg);
-    if (threadIdx.x == 0) a.counters[0] = 0;
+    if (threadIdx.x == 0) {
+        a.counters[0] = 0;
+        s_done = a.state->done;
+        for (int k = 0; k < 4; ++k) s_sc[k] = a.state->sc_x[k];
+    }
+    if (a.rebake == nullptr) return;
+    __syncthreads();
+    if (s_done != 0 || s_sc[0] == s_sc0_ran) return;     // same eps next: the copy and the log2 states stand
+    // A new eps (a schedule or a stage): the log2-unit potentials R = (c / 2) fh of both clouds again from the
+    // accumulator-unit ones, and the first cloud's log2-unit copy for the new score scale, so that the next f
+    // update already finds them. (This is the g update: rows y, columns x.)
+    const float k2 = 0.5f * (s_sc[0] * kLog2e);
+    const int nx = a.s.nt * SK_TILE;
+    for (int i = (int)threadIdx.x; i < a.rows_pad; i += (int)blockDim.x) a.out2[i] = a.out[i] * k2;
+    for (int i = (int)threadIdx.x; i < nx; i += (int)blockDim.x) a.u2[i] = a.u[i] * k2;
+    const void* second = a.xr;
+    const BakeParams b = bake_params(a.rebake, second, s_sc);
+    const float* h = reinterpret_cast<const float*>(a.rebake);
+    if (b.valid ? h[2] == b.c && h[3] == packed_scale(second) : h[2] == 0.0f) return;
+    if (b.valid) {
+        const long long total = (long long)(nx / SK_TILE) * a.nc * 64;
+        for (long long idx = threadIdx.x; idx < total; idx += blockDim.x) bake_unit(a.rebake, idx, nx, a.nc, b);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) bake_header(a.rebake, second, b);
+}
+
+// The on-device loop's log2-unit potentials from the accumulator-unit ones, R = (c / 2) fh, c = sc[0] log2(e).
+__global__ __launch_bounds__(256) void derive_log2_kernel(const float* __restrict__ fh, float* __restrict__ rf, int nx,
+                                                          const float* __restrict__ gh, float* __restrict__ rg, int ny,
+                                                          const float* __restrict__ sc) {
+    const float k2 = 0.5f * (sc[0] * kLog2e);
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < nx) rf[i] = fh[i] * k2;
+    if (i < ny) rg[i] = gh[i] * k2;
 }
 
 }  // namespace sk

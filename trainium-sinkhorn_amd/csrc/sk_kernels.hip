@@ -92,6 +92,8 @@ __global__ void pack_header_kernel(unsigned* __restrict__ header) {
     if (threadIdx.x == 0) {
         header[0] = 0u;
         header[1] = __float_as_uint(1.0f);
+        header[2] = 0u;                     // no log2-unit copy yet
+        header[3] = 0u;
     }
 }
 
@@ -112,13 +114,16 @@ __global__ __launch_bounds__(256) void absmax_kernel(const float* __restrict__ s
     }
 }
 
-// The power-of-two scale for a max |coordinate| m: m * s in [2^13, 2^14), clamped to [2^-32, 2^40] so that
-// s_x s_y and the scaled column terms stay well inside the fp32 range (m <= 7e13 < 2^46 keeps m s <= 2^14).
+// The power-of-two scale for a max |coordinate| m: m * s in [2^4, 2^5), clamped to [2^-32, 2^40] so that
+// s_x s_y and the scaled column terms stay well inside the fp32 range (m <= 7e13 < 2^46 keeps m s < 2^14).
+// The pieces then hold every coordinate within max(2^-23 |v|, 2^-25) of v = s x: relative to the largest,
+// 2^-23 at worst. The target sits low in the fp16 range so that the first cloud's log2-unit copy against
+// this scale, fl(c x) / s, lands in fp16's full-precision range for the usual score scales (bake_log2).
 __device__ __forceinline__ float pack_scale(float m) {
     if (!(m > 0.0f)) return 1.0f;
     int e;
     frexpf(m, &e);                          // m in [2^(e-1), 2^e)
-    const int k = e > 46 ? -32 : (e < -26 ? 40 : 14 - e);
+    const int k = e > 37 ? -32 : (e < -35 ? 40 : 5 - e);
     return ldexpf(1.0f, k);
 }
 
@@ -147,6 +152,16 @@ __global__ void pack_cloud_kernel(const float* __restrict__ src, int n, int d, i
     f16x8* o = reinterpret_cast<f16x8*>(dst + kHeaderBytes) + (T * nc + cc) * (2 * 64) + lane;
     o[0] = p0;
     o[64] = p1;
+}
+
+// The first cloud's log2-unit copy (bake_params / bake_unit / bake_header, sk_epilogue.h), one unit per thread.
+__global__ __launch_bounds__(256) void bake_log2_kernel(char* __restrict__ first, const void* __restrict__ second,
+                                                        int npad, int nc, const float* __restrict__ sc) {
+    const BakeParams b = bake_params(first, second, sc);
+    const long long total = (long long)(npad / SK_TILE) * nc * 64;
+    const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b.valid && idx < total) bake_unit(first, idx, npad, nc, b);
+    if (idx == 0) bake_header(first, second, b);
 }
 
 // The general row log-sum-exp's packing: three bf16 pieces per coordinate (exact), no scale (the header
@@ -287,6 +302,7 @@ struct Pass {
     int kp;
     const float* u;
     const float* v;
+    float* u2;      // the column cloud's log2-unit potential (on-device loop), or null
     const float* sc;
     const int* skip;
     int mode;
@@ -295,6 +311,7 @@ struct Pass {
     const float* xsq;
     const float* off;
     float* out;
+    float* out2;    // the rows' log2-unit potential (on-device loop), or null
     int n_store;
     float2* meas;
     const float* w;
@@ -303,6 +320,7 @@ struct Pass {
     int* counters;  // with state: one arrival counter, zero on entry and left zero
     sk_state* state;  // loop control after the merge (g update of the loop), or null
     LoopCfg cfg;
+    char* rebake;   // with state: the packed first cloud, whose log2-unit copy the control remakes on a new eps
 };
 
 hipError_t run_pass(const Pass& ps, const Plan& pl, hipStream_t st) {
@@ -311,6 +329,7 @@ hipError_t run_pass(const Pass& ps, const Plan& pl, hipStream_t st) {
     a.yc = ps.yc;
     a.u = ps.u;
     a.v = ps.v;
+    a.u2 = ps.u2;
     a.sc = ps.sc;
     a.skip = ps.skip;
     a.part = ps.part;
@@ -319,10 +338,12 @@ hipError_t run_pass(const Pass& ps, const Plan& pl, hipStream_t st) {
     a.mode = ps.mode;
     a.rows_role = ps.rows_role;
     a.contraction = ps.contraction;
+    a.nc = pl.nc;
     a.s = pl.s;
     a.xsq = ps.xsq;
     a.off = ps.off;
     a.out = ps.out;
+    a.out2 = ps.out2;
     a.n_store = ps.n_store;
     a.meas = ps.meas;
     a.w = ps.w;
@@ -331,6 +352,7 @@ hipError_t run_pass(const Pass& ps, const Plan& pl, hipStream_t st) {
     a.ngroups = pl.ngroups;
     a.state = ps.state;
     a.cfg = ps.cfg;
+    a.rebake = ps.rebake;
     hipError_t e = launch_partial(a, pl.nc, st);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(merge_kernel, dim3(pl.ngroups), dim3(kRowsPerGroup), 0, st, a);
@@ -374,6 +396,16 @@ int check_cloud(const sk_cloud_f32& c, const char* name) {
     return SK_OK;
 }
 
+// TRNOPT_HIP_LOG2=0 turns the log2-unit copies off (every half-step then scales on the VALU), to compare the paths.
+bool log2_enabled() { return env_int("TRNOPT_HIP_LOG2", 1) != 0; }
+
+void launch_bake(void* first, const void* second, int npad, int nc, const float* sc, hipStream_t st) {
+    if (!log2_enabled()) return;
+    const long long total = (long long)(npad / SK_TILE) * nc * 64;
+    hipLaunchKernelGGL(bake_log2_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, (char*)first, second,
+                       npad, nc, sc);
+}
+
 }  // namespace
 
 // ===================================================================================================
@@ -392,6 +424,18 @@ int sk_pad_dim(int d) { return d <= 0 ? 0 : (d + SK_KP_ALIGN - 1) / SK_KP_ALIGN 
 size_t sk_packed_bytes(int n, int d) {
     if (n < 1 || d < 1 || sk_pad_dim(d) > SK_KP_MAX) return 0;
     return SK_PACKED_HEADER_BYTES + (size_t)sk_pad_points(n) * sk_pad_dim(d) * SK_PACKED_BYTES_PER_COORD;
+}
+
+int sk_bake_log2_f32(void* first_pk, const void* second_pk, int n_first, int d, const float* sc, void* stream) {
+    if (first_pk == nullptr || second_pk == nullptr || sc == nullptr)
+        return fail(SK_E_ARG, "sk_bake_log2_f32: null pointer");
+    if (n_first < 1) return fail(SK_E_SHAPE, "sk_bake_log2_f32: n_first %d", n_first);
+    if (int r = check_kp(d)) return r;
+    if (!aligned16(first_pk) || !aligned16(second_pk))
+        return fail(SK_E_ARG, "sk_bake_log2_f32: packed clouds must be 16-byte aligned");
+    launch_bake(first_pk, second_pk, sk_pad_points(n_first), sk_pad_dim(d) / 16, sc, (hipStream_t)stream);
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? SK_OK : hip_fail(e, "sk_bake_log2_f32");
 }
 
 int sk_pack_cloud_f32(const float* pts, int n, int d, int ld, void* out, void* stream) {
@@ -535,18 +579,22 @@ size_t sk_loop_workspace_bytes(int nx_pad, int ny_pad, int d) {
     const Plan pf = make_plan(nx_pad, ny_pad, kp), pg = make_plan(ny_pad, nx_pad, kp);
     if (!pf.ok || !pg.ok) return 0;
     return std::max(partial_bytes(pf, nx_pad), partial_bytes(pg, ny_pad)) +
-           align_up((size_t)meas_count(ny_pad) * sizeof(float2)) + align_up(sizeof(int));
+           align_up((size_t)meas_count(ny_pad) * sizeof(float2)) + align_up(sizeof(int)) +
+           align_up((size_t)nx_pad * sizeof(float)) + align_up((size_t)ny_pad * sizeof(float));
 }
 
 namespace {
 // The loop's workspace: partial slots (shared by the f and g updates), the g update's per-group convergence
-// partials, the arrival counter of the g update's merge (zeroed at init; every merge leaves it zero).
+// partials, the arrival counter of the g update's merge (zeroed at init; every merge leaves it zero), and the
+// two potentials in log2 units, R = (c / 2) fh, that the iteration carries when the scores come in log2 units.
 struct LoopLayout {
     Plan pf, pg;
     float2* part;
     float2* meas;
     int* counters;
     int ncounters;
+    float* rf;
+    float* rg;
 };
 
 LoopLayout loop_layout(const sk_loop_f32* L) {
@@ -559,12 +607,15 @@ LoopLayout loop_layout(const sk_loop_f32* L) {
     o.meas = (float2*)((char*)L->ws + part_sz);
     o.counters = (int*)((char*)o.meas + align_up((size_t)meas_count(L->y.npad) * sizeof(float2)));
     o.ncounters = 1;
+    o.rf = (float*)((char*)o.counters + align_up(sizeof(int)));
+    o.rg = (float*)((char*)o.rf + align_up((size_t)L->x.npad * sizeof(float)));
     return o;
 }
 }  // namespace
 
 int sk_loop_init_f32(const sk_loop_f32* L, void* stream) {
-    if (L == nullptr || L->state == nullptr || L->ws == nullptr) return fail(SK_E_ARG, "sk_loop_init_f32: null pointer");
+    if (L == nullptr || L->state == nullptr || L->fh == nullptr || L->gh == nullptr || L->ws == nullptr)
+        return fail(SK_E_ARG, "sk_loop_init_f32: null pointer");
     if (L->n_sched > 0 && L->sched == nullptr) return fail(SK_E_ARG, "sk_loop_init_f32: n_sched without sched");
     if (L->n_stages > 0 && L->stages == nullptr) return fail(SK_E_ARG, "sk_loop_init_f32: n_stages without stages");
     if (!(L->eps > 0.0)) return fail(SK_E_ARG, "sk_loop_init_f32: eps must be > 0");
@@ -578,6 +629,13 @@ int sk_loop_init_f32(const sk_loop_f32* L, void* stream) {
     const LoopLayout lo = loop_layout(L);
     hipLaunchKernelGGL(loop_init_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, L->state, loop_cfg(L),
                        lo.counters, lo.ncounters);
+    // x's log2-unit copy for the first iteration's eps and both log2-unit potentials (from fh and the caller's
+    // gh); the loop control remakes them when eps changes
+    launch_bake(const_cast<void*>(L->x.pk), L->y.pk, L->x.npad, sk_pad_dim(L->d) / 16, L->state->sc_x,
+                (hipStream_t)stream);
+    const int nmax = std::max(L->x.npad, L->y.npad);
+    hipLaunchKernelGGL(derive_log2_kernel, dim3((nmax + 255) / 256), dim3(256), 0, (hipStream_t)stream, L->fh, lo.rf,
+                       L->x.npad, L->gh, lo.rg, L->y.npad, L->state->sc_x);
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? SK_OK : hip_fail(e, "sk_loop_init_f32");
 }
@@ -612,6 +670,7 @@ int sk_loop_run_f32(const sk_loop_f32* L, int iters, void* stream) {
     f.kp = kp;
     f.u = L->gh;
     f.v = L->y.log_w;
+    f.u2 = lo.rg;
     f.sc = st->sc_x;
     f.skip = skip;
     f.mode = kHalfStep;
@@ -620,6 +679,7 @@ int sk_loop_run_f32(const sk_loop_f32* L, int iters, void* stream) {
     f.xsq = L->x.sq;
     f.off = L->x.off;
     f.out = L->fh;
+    f.out2 = lo.rf;
     f.n_store = L->x.npad;
     f.part = part;
 
@@ -631,6 +691,7 @@ int sk_loop_run_f32(const sk_loop_f32* L, int iters, void* stream) {
     g.kp = kp;
     g.u = L->fh;
     g.v = L->x.log_w;
+    g.u2 = lo.rf;
     g.sc = st->sc_y;
     g.skip = skip;
     g.mode = kHalfStep;
@@ -639,6 +700,7 @@ int sk_loop_run_f32(const sk_loop_f32* L, int iters, void* stream) {
     g.xsq = L->y.sq;
     g.off = L->y.off;
     g.out = L->gh;
+    g.out2 = lo.rg;
     g.n_store = L->y.npad;
     g.meas = meas;
     g.w = L->y.w;
@@ -647,6 +709,7 @@ int sk_loop_run_f32(const sk_loop_f32* L, int iters, void* stream) {
     g.counters = lo.counters;
     g.state = st;
     g.cfg = cfg;
+    g.rebake = log2_enabled() ? (char*)const_cast<void*>(L->x.pk) : nullptr;
 
     for (int k = 0; k < iters; ++k) {
         hipError_t e = run_pass(f, pf, hs);

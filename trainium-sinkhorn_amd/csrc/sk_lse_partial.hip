@@ -120,8 +120,9 @@ constexpr int op_begin(int i, int NS) {
     return k;
 }
 
-// col4(q) returns the column terms of accumulators 4q .. 4q + 3 of the tile being updated.
-template <int RB>
+// col4(q) returns the column terms of accumulators 4q .. 4q + 3 of the tile being updated. With L2 the scores
+// are already in log2 units (the first cloud's log2-unit copy) and c is not applied.
+template <int RB, bool L2>
 struct Online {
     float m[RB];
     f32x4 cv[4];
@@ -141,7 +142,7 @@ struct Online {
             m[b] = max3(m[b], acc[b][2 * p], acc[b][2 * p + 1]);
         } else if constexpr (j < 41) {
             constexpr int r = j - 25;
-            acc[b][r] = ex2(c * (acc[b][r] - m[b]));
+            acc[b][r] = L2 ? ex2(acc[b][r] - m[b]) : ex2(c * (acc[b][r] - m[b]));
         } else if constexpr (j < 56) {
             // tree level l (stride 2^l) pairs acc[2^(l+1) q] += acc[2^(l+1) q + 2^l]
             constexpr int t = j - 41;
@@ -150,7 +151,7 @@ struct Online {
             constexpr int lo = q << (l + 1), hi = lo + (1 << l);
             acc[b][lo] = acc[b][lo] + acc[b][hi];
         } else {
-            S[b] = fmaf(S[b], ex2(c * (M[b] - m[b])), acc[b][0]);
+            S[b] = fmaf(S[b], ex2(L2 ? M[b] - m[b] : c * (M[b] - m[b])), acc[b][0]);
             M[b] = m[b];
         }
     }
@@ -184,8 +185,8 @@ struct Contract<kBF16x3> {
 };
 
 // End of a work segment: lanes l and l + 32 hold the same row over different columns; merge them and store
-// (M / sigma, S) of each row.
-template <int RB>
+// (M / sigma, S) of each row, or with L2 (M, S) in log2 units.
+template <int RB, bool L2>
 __device__ __forceinline__ void store_rows(const PartialArgs& a, const float (&M)[RB], const float (&S)[RB], int rb0,
                                            int slot, float c, float inv_sigma, int lane) {
 #pragma unroll
@@ -193,13 +194,14 @@ __device__ __forceinline__ void store_rows(const PartialArgs& a, const float (&M
         const float Mo = __shfl_xor(M[b], 32);
         const float So = __shfl_xor(S[b], 32);
         const float Mn = fmaxf(M[b], Mo);
-        const float Sn = S[b] * ex2(c * (M[b] - Mn)) + So * ex2(c * (Mo - Mn));
+        const float Sn = L2 ? S[b] * ex2(M[b] - Mn) + So * ex2(Mo - Mn)
+                            : S[b] * ex2(c * (M[b] - Mn)) + So * ex2(c * (Mo - Mn));
         if (lane < 32 && rb0 + b < a.nrb)
-            a.part[(size_t)slot * a.rows_pad + (size_t)(rb0 + b) * 32 + lane] = make_float2(Mn * inv_sigma, Sn);
+            a.part[(size_t)slot * a.rows_pad + (size_t)(rb0 + b) * 32 + lane] = make_float2(L2 ? Mn : Mn * inv_sigma, Sn);
     }
 }
 
-template <int NC, int ROLE, int CT>
+template <int NC, int ROLE, int CT, bool L2>
 struct Staged {
     using C = Contract<CT>;
     using T = typename C::T;
@@ -211,13 +213,16 @@ struct Staged {
     static constexpr int NS = kProducts * NC * RB;     // MFMA slots per tile
 
     // Rows rb0 .. rb0 + RB - 1 against column tiles [tb, te); writes one (M, S) per row into `slot`.
-    __device__ __forceinline__ static void run(const PartialArgs& a, int rb0, int tb, int te, int slot, float alpha,
-                                               float beta, float c, float inv_sigma, T* lds_y, float* lds_col) {
+    __device__ __forceinline__ static void run(const PartialArgs& a, int rb0, int tb, int te, int slot, const float* cu,
+                                               float alpha, float beta, float cs, float c, float inv_sigma,
+                                               T* lds_y, float* lds_col) {
         const int tid = threadIdx.x;
         const int lane = tid & 63;
         const int h = lane >> 5;
-        const T* xt = packed_tiles<T>(a.xr);
-        const T* yt = packed_tiles<T>(a.yc);
+        // With L2 the first cloud of the pair (the rows for ROLE 0, the columns for ROLE 1) is read from its
+        // log2-unit copy.
+        const T* xt = L2 && ROLE == 0 ? packed_log2_tiles<T>(a.xr, a.nrb * 32, NC) : packed_tiles<T>(a.xr);
+        const T* yt = L2 && ROLE == 1 ? packed_log2_tiles<T>(a.yc, a.s.nt * 32, NC) : packed_tiles<T>(a.yc);
 
         T xv[RB][NC][kPieces];
 #pragma unroll
@@ -250,7 +255,7 @@ struct Staged {
                 const int idx = tid + k * kBlock < TILE16 ? tid + k * kBlock : TILE16 - 1;
                 pf[k] = yt[(size_t)t * TILE16 + idx];
             }
-            pc = fmaxf(fmaf(beta, a.v[t * 32 + cj], alpha * a.u[t * 32 + cj]), kPadScore);
+            pc = fmaxf(cs * fmaf(beta, a.v[t * 32 + cj], alpha * cu[t * 32 + cj]), kPadScore);
         };
         auto stage = [&](int buf, int cbuf) {
 #pragma unroll
@@ -269,7 +274,7 @@ struct Staged {
         };
 
         f32x16 accA[RB], accB[RB];
-        Online<RB> on;
+        Online<RB, L2> on;
         // One tile: MFMAs into accN from zero; with `epi`, the update of the previous tile (accP, its column
         // terms at colp) is spread between them, one slot per MFMA, fenced so the compiler keeps the interleave.
         auto tile = [&](f32x16 (&accN)[RB], f32x16 (&accP)[RB], const float* colp, bool epi) {
@@ -336,7 +341,7 @@ struct Staged {
         }
         update(accA, colp_of(cb));
     done:
-        store_rows(a, M, S, rb0, slot, c, inv_sigma, lane);
+        store_rows<RB, L2>(a, M, S, rb0, slot, c, inv_sigma, lane);
     }
 };
 
@@ -345,7 +350,7 @@ constexpr int kColTiles = 256;
 constexpr int kColBatch = 8;
 constexpr int kStreamMaxChunks = 4;
 
-template <int NC, int ROLE, int CT>
+template <int NC, int ROLE, int CT, bool L2>
 struct Streamed {
     using C = Contract<CT>;
     using T = typename C::T;
@@ -355,13 +360,16 @@ struct Streamed {
     static constexpr int TILE16 = NC * kPieces * 64;
     static constexpr int NS = kProducts * NC * RB;
 
-    __device__ __forceinline__ static void run(const PartialArgs& a, int rb0, int tb, int te, int slot, float alpha,
-                                               float beta, float c, float inv_sigma, float* lds_col) {
+    __device__ __forceinline__ static void run(const PartialArgs& a, int rb0, int tb, int te, int slot, const float* cu,
+                                               float alpha, float beta, float cs, float c, float inv_sigma,
+                                               float* lds_col) {
         const int tid = threadIdx.x;
         const int lane = tid & 63;
         const int h = lane >> 5;
-        const T* xt = packed_tiles<T>(a.xr);
-        const T* yt = packed_tiles<T>(a.yc);
+        // With L2 the first cloud of the pair (the rows for ROLE 0, the columns for ROLE 1) is read from its
+        // log2-unit copy.
+        const T* xt = L2 && ROLE == 0 ? packed_log2_tiles<T>(a.xr, a.nrb * 32, NC) : packed_tiles<T>(a.xr);
+        const T* yt = L2 && ROLE == 1 ? packed_log2_tiles<T>(a.yc, a.s.nt * 32, NC) : packed_tiles<T>(a.yc);
 
         T xv[RB][NC][kPieces];
 #pragma unroll
@@ -394,13 +402,13 @@ struct Streamed {
                 for (int q = 0; q < kColBatch; ++q) {
                     const int k = k0 + q * kBlock + tid, j = base + k;
                     const int jc = (k < n && j >= 0) ? j : 0;     // clamped in bounds; not stored
-                    uu[q] = a.u[jc];
+                    uu[q] = cu[jc];
                     vv[q] = a.v[jc];
                 }
 #pragma unroll
                 for (int q = 0; q < kColBatch; ++q) {
                     const int k = k0 + q * kBlock + tid, j = base + k;
-                    if (k < n && j >= 0) lds_col[k] = fmaxf(fmaf(beta, vv[q], alpha * uu[q]), kPadScore);
+                    if (k < n && j >= 0) lds_col[k] = fmaxf(cs * fmaf(beta, vv[q], alpha * uu[q]), kPadScore);
                 }
             }
             __syncthreads();
@@ -416,7 +424,7 @@ struct Streamed {
         auto colp_of = [&](int t) { return lds_col + (t - cbase) * 32 + 4 * h; };
 
         f32x16 accA[RB], accB[RB];
-        Online<RB> on;
+        Online<RB, L2> on;
         auto tile = [&](f32x16 (&accN)[RB], f32x16 (&accP)[RB], const float* colp, const T (&yv)[NC][kPieces],
                         bool epi) {
             auto col4 = [&](int q) { return *reinterpret_cast<const f32x4*>(colp + 8 * q); };
@@ -474,49 +482,16 @@ struct Streamed {
         }
         update(accA, colp_of(t - 1));
     done:
-        store_rows(a, M, S, rb0, slot, c, inv_sigma, lane);
+        store_rows<RB, L2>(a, M, S, rb0, slot, c, inv_sigma, lane);
     }
 };
 
-template <int NC, int ROLE, int CT>
-__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(1, 1)))
-void lse_partial_kernel(PartialArgs a) {
-    // Every scalar this launch needs (the loop's done flag, the eps scalars, both clouds' scales) is requested
-    // at once, and the done flag tested after: one memory round trip before the work starts, not four.
-    const int* skip_p = a.skip != nullptr ? a.skip : &kNoSkip;
-    const float sc0 = a.sc[0], sc2 = a.sc[2];                         // a.sc is valid in both modes
-    const float sx = packed_scale(a.xr), sy = packed_scale(a.yc);   // 1 for kBF16x3
-    const int skip = *skip_p;
-    asm volatile("" ::"s"(sc0), "s"(sc2), "s"(sx), "s"(sy), "v"(skip));   // all four loaded before the test
-    if (skip != 0) return;
-    constexpr bool kStream = NC <= kStreamMaxChunks;
-    constexpr int kLdsY = kStream ? 1 : 2 * NC * Contract<CT>::pieces * 64;
-    constexpr int kLdsCol = kStream ? (kColTiles + 1) * 32 : 3 * 32;
-    __shared__ typename Contract<CT>::T lds_y[kLdsY];
-    __shared__ __attribute__((aligned(16))) float lds_col[kLdsCol];
-    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // one value per wave
-    const int P = a.s.P;
-    const int p = xcd_contiguous(blockIdx.x, P);
-
-    // a_ij = x_i . y_j + alpha u_j + beta v_j in accumulator units, scores exp2(c (a - M)):
-    // half-step: a = x . y + (gh + eps log b) / 2, c = (2 / eps) log2(e); plain row-LSE: a = xa . ya + mask,
-    // c = log2(e). The kernel works in units scaled by sigma = s_rows s_cols (a power of two): alpha, beta
-    // times sigma, c divided by it.
-    float alpha, beta, c;
-    if (a.mode == kHalfStep) {
-        alpha = 0.5f;
-        beta = 0.5f * sc2;
-        c = sc0 * kLog2e;
-    } else {
-        alpha = 1.0f;
-        beta = 0.0f;
-        c = kLog2e;
-    }
-    const float sigma = sx * sy, inv_sigma = (1.0f / sx) * (1.0f / sy);
-    alpha *= sigma;
-    beta *= sigma;
-    c *= inv_sigma;
-
+// The work segments of workgroup p: a_ij = x_i . y_j + cs (alpha cu_j + beta v_j) in the kernel's units, scores
+// exp2(c (a - M)) (with L2: exp2(a - M), a already in log2 units).
+template <int NC, int ROLE, int CT, bool L2>
+__device__ __forceinline__ void segments(const PartialArgs& a, int p, int wv, const float* cu, float alpha, float beta,
+                                         float cs, float c, float inv_sigma, typename Contract<CT>::T* lds_y,
+                                         float* lds_col) {
     // The segment bounds are 32-bit integer arithmetic (the divisions expand to vector code); their results are
     // the same in every lane, and readfirstlane hands them to the scalar unit, so the tile loop's counters and
     // operand addresses stay in scalar registers.
@@ -529,12 +504,65 @@ void lse_partial_kernel(PartialArgs a) {
         // Waves past the last row block recompute it (their rows are not stored) so that every wave takes part
         // in the workgroup's barriers.
         const int rb0 = (g * kWaves + wv) * kRowBlocks;
-        if constexpr (kStream)
-            Streamed<NC, ROLE, CT>::run(a, rb0, tb, te, slot, alpha, beta, c, inv_sigma, lds_col);
+        if constexpr (NC <= kStreamMaxChunks)
+            Streamed<NC, ROLE, CT, L2>::run(a, rb0, tb, te, slot, cu, alpha, beta, cs, c, inv_sigma, lds_col);
         else
-            Staged<NC, ROLE, CT>::run(a, rb0, tb, te, slot, alpha, beta, c, inv_sigma, lds_y, lds_col);
+            Staged<NC, ROLE, CT, L2>::run(a, rb0, tb, te, slot, cu, alpha, beta, cs, c, inv_sigma, lds_y, lds_col);
         u += te - tb;
     }
+}
+
+template <int NC, int ROLE, int CT>
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void lse_partial_kernel(PartialArgs a) {
+    // Every scalar this launch needs (the loop's done flag, the eps scalars, both clouds' scales, the first
+    // cloud's log2-copy tag) is requested at once, and the done flag tested after: one memory round trip before
+    // the work starts.
+    const int* skip_p = a.skip != nullptr ? a.skip : &kNoSkip;
+    const float* h1 = reinterpret_cast<const float*>(ROLE == 0 ? a.xr : a.yc);   // the first cloud's header
+    const float sc0 = a.sc[0], sc2 = a.sc[2];                         // a.sc is valid in both modes
+    const float sx = packed_scale(a.xr), sy = packed_scale(a.yc);   // 1 for kBF16x3
+    const float cb = h1[2], cb_s2 = h1[3];
+    const int skip = *skip_p;
+    asm volatile("" ::"s"(sc0), "s"(sc2), "s"(sx), "s"(sy), "s"(cb), "s"(cb_s2), "v"(skip));
+    if (skip != 0) return;
+    constexpr bool kStream = NC <= kStreamMaxChunks;
+    constexpr int kLdsY = kStream ? 1 : 2 * NC * Contract<CT>::pieces * 64;
+    constexpr int kLdsCol = kStream ? (kColTiles + 1) * 32 : 3 * 32;
+    __shared__ typename Contract<CT>::T lds_y[kLdsY];
+    __shared__ __attribute__((aligned(16))) float lds_col[kLdsCol];
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // one value per wave
+    const int p = xcd_contiguous(blockIdx.x, a.s.P);
+
+    // a_ij = x_i . y_j + alpha u_j + beta v_j in accumulator units, scores exp2(c (a - M)):
+    // half-step: a = x . y + (gh + eps log b) / 2, c = (2 / eps) log2(e); plain row-LSE: a = xa . ya + mask,
+    // c = log2(e).
+    float alpha, beta, c;
+    if (a.mode == kHalfStep) {
+        alpha = 0.5f;
+        beta = 0.5f * sc2;
+        c = sc0 * kLog2e;
+    } else {
+        alpha = 1.0f;
+        beta = 0.0f;
+        c = kLog2e;
+    }
+    // With a valid log2-unit copy of the first cloud for this c (log2_ready), the matrix cores produce c x.y and
+    // the exponentials take the scores as they are. The column term c (gh / 2 + eps log b / 2) then comes from
+    // the column cloud's potential in log2 units R = (c / 2) gh when the caller keeps one (u2, the on-device
+    // loop: R + log2(e) log b, one rounding), else from gh, scaled by c. Otherwise the kernel works in units
+    // scaled by sigma = s_rows s_cols (a power of two): column terms times sigma, c divided by it.
+    if constexpr (CT == kF16x2) {
+        if (a.mode == kHalfStep && cb != 0.0f && cb == c && cb_s2 == (ROLE == 0 ? sy : sx)) {
+            if (a.u2 != nullptr)
+                segments<NC, ROLE, CT, true>(a, p, wv, a.u2, 1.0f, kLog2e, 1.0f, 1.0f, 1.0f, lds_y, lds_col);
+            else
+                segments<NC, ROLE, CT, true>(a, p, wv, a.u, alpha, beta, c, 1.0f, 1.0f, lds_y, lds_col);
+            return;
+        }
+    }
+    const float sigma = sx * sy, inv_sigma = (1.0f / sx) * (1.0f / sy);
+    segments<NC, ROLE, CT, false>(a, p, wv, a.u, alpha, beta, sigma, c * inv_sigma, inv_sigma, lds_y, lds_col);
 }
 
 template <int NC>

@@ -33,7 +33,7 @@ PAD_LOG_WEIGHT = -1e9                    # src/trnopt/sinkhorn.py:59
 TILE = 32                                 # SK_TILE
 KP_ALIGN = 16                             # SK_KP_ALIGN
 KP_MAX = 128                              # SK_KP_MAX
-PACKED_BYTES_PER_COORD = 4                # SK_PACKED_BYTES_PER_COORD: two fp16 pieces
+PACKED_BYTES_PER_COORD = 8                # SK_PACKED_BYTES_PER_COORD: two fp16 pieces, own scale and log2 copy
 PACKED_HEADER_BYTES = 256                 # SK_PACKED_HEADER_BYTES
 MAX_ABS_COORDINATE = 7.0e13               # larger coordinates do not fit the kernels' scaled fp16 pieces
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libtrnopt_hip.so"
@@ -74,6 +74,8 @@ _SIGS = {
     "sk_packed_bytes": (ctypes.c_size_t, [ctypes.c_int, ctypes.c_int]),
     "sk_pack_cloud_f32": (ctypes.c_int, [_c_float_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
                                          ctypes.c_void_p]),
+    "sk_bake_log2_f32": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, _c_float_p,
+                                        ctypes.c_void_p]),
     "sk_row_lse_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int, ctypes.c_int, ctypes.c_int]),
     "sk_row_lse_f32": (ctypes.c_int, [_c_float_p, _c_float_p, _c_float_p, ctypes.c_int, ctypes.c_int,
                                       ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
@@ -262,6 +264,17 @@ class HipCloud:
     def c_struct(self) -> SkCloud:
         return SkCloud(self.pk.data_ptr(), self.sq.data_ptr(), self.log_w.data_ptr(), self.w.data_ptr(),
                        _ptr(self.off), self.n, self.npad)
+
+
+def bake_log2(first: HipCloud, second: HipCloud, sc: torch.Tensor) -> None:
+    """Make the first cloud's log2-unit copy for sc[0] = 2/eps against `second` (sk_bake_log2_f32): half-steps
+    of this pair at that eps then take their scores in log2 units from the matrix cores. Any other eps, or a
+    copy that does not fit fp16's range, falls back to scaling on the VALU; the results agree to rounding."""
+    _require_device_f32("sc", sc, 4)
+    if first.role != 0 or second.role != 1 or first.d != second.d:
+        raise ValueError("bake_log2 pairs a first cloud (role 0) with a second (role 1) of the same dimension")
+    _check(lib().sk_bake_log2_f32(first.pk.data_ptr(), second.pk.data_ptr(), first.n, first.d, sc.data_ptr(),
+                                  _stream()), "sk_bake_log2_f32")
 
 
 def half_step(side: HipCloud, other: HipCloud, other_h: torch.Tensor, sc: torch.Tensor, use_off: bool = True,

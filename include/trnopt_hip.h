@@ -22,8 +22,10 @@
  *     (sk_pack_cloud_f32 builds it from a row-major (n, d) fp32 array; sk_packed_bytes gives its size).
  *     The kernels form x.y from three products of the pieces (x0 y0, x0 y1, x1 y0), accumulated in
  *     fp32: at least as accurate as an fp32 dot product, and bit-identical in the two directions of a pair of half-steps (rows_role 0
- *     and 1) over the same two clouds. Coordinates must satisfy max |x| <= 7e13; the precision is that of
- *     fp32 for max |x| >= 2^-26 (1.5e-8) and degrades gracefully below.
+ *     and 1) over the same two clouds. Coordinates must satisfy max |x| <= 7e13; every coordinate is held
+ *     within 2^-23 of the cloud's largest for max |x| >= 2^-36, and the precision degrades gracefully below.
+ *     The first cloud of a pair may also carry a log2-unit copy of its pieces (sk_bake_log2_f32), with
+ *     which the scores come out of the matrix cores already scaled by (2 / eps) log2(e).
  *   - Shifted potentials follow the reference (src/trnopt/sinkhorn.py:28-33): fh = f - |x|^2.
  */
 #ifndef TRNOPT_HIP_H

@@ -96,12 +96,10 @@ __host__ __device__ inline const T* packed_log2_tiles(const void* pk, int npad, 
 }
 __device__ inline float packed_scale(const void* pk) { return reinterpret_cast<const float*>(pk)[1]; }
 
-// The half-step may take its scores in log2 units from the matrix cores when the first cloud's log2-unit copy
-// was made for this score scale c = (2 / eps) log2(e) and against this second cloud (its scale).
-__device__ inline bool log2_ready(const void* first, const void* second, float c) {
-    const float* h = reinterpret_cast<const float*>(first);
-    return h[2] != 0.0f && h[2] == c && h[3] == packed_scale(second);
-}
+// A half-step takes its scores in log2 units from the matrix cores ("log2_ready") when the first cloud's
+// log2-unit copy was made for its score scale c = (2 / eps) log2(e) and against its second cloud: header word
+// [2] of the first cloud equals c (and is not 0) and word [3] equals the second cloud's scale, word [1]. The
+// partial and the merge kernels test this on the same header words.
 
 // The on-device loop's configuration (src/trnopt/sinkhorn.py:313-320, 340-344).
 struct LoopCfg {
@@ -140,7 +138,9 @@ struct PartialArgs {
     int* counters;      // with state: one arrival counter, zero on entry and left zero
     int ngroups;
     // ... and, in the last merge workgroup of a g update, the loop control (null: none), which also remakes the
-    // log2-unit copy of the first cloud (rebake, the packed first cloud; null: never) when eps changes.
+    // log2-unit copy of the first cloud (rebake, the packed first cloud; null: never) when eps changes; the f
+    // update's merge advances the state's iteration counters (tick; null: none).
+    sk_state* tick;
     sk_state* state;
     LoopCfg cfg;
     char* rebake;

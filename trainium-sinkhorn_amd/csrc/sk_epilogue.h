@@ -86,7 +86,7 @@ __device__ inline void set_scalars(sk_state* st, double e, double rho_x, double 
 
 // Merge the slots of row i = 256 g + threadIdx.x (one row per thread of the workgroup) and apply the epilogue:
 //     lse = (2 / eps) M + ln S  (half-step, accumulator units) or M + ln S  (plain row-LSE)
-// When the partial kernel took its scores in log2 units (log2_ready: the same test on the same headers), the
+// When the partial kernel took its scores in log2 units (log2_ready, tested on the same header words), the
 // slots hold M in log2 units: they merge without c, and M / c (correctly rounded, so that no constant factor
 // enters the potentials) gives the accumulator units.
 //     fh  = kappa ((|x|^2 + eps off) - eps lse) - |x|^2
@@ -98,31 +98,39 @@ __device__ inline bool merge_group(const PartialArgs& a, int g) {
     const int i = g * kRowsPerGroup + (int)threadIdx.x;
     const int* skip_p = a.skip != nullptr ? a.skip : &kNoSkip;
     const float sc0 = a.sc[0], sc1 = a.sc[1], sc2 = a.sc[2], sc3 = a.sc[3];   // valid in both modes
-    const void* first = a.rows_role == 0 ? a.xr : a.yc;
-    const void* second = a.rows_role == 0 ? a.yc : a.xr;
-    const float c_hs = sc0 * kLog2e;
-    const bool l2 = a.mode == kHalfStep && a.contraction == kF16x2 && log2_ready(first, second, c_hs);
+    const float* h1 = reinterpret_cast<const float*>(a.rows_role == 0 ? a.xr : a.yc);   // the first cloud
+    const float* h2 = reinterpret_cast<const float*>(a.rows_role == 0 ? a.yc : a.xr);
+    const float cb = h1[2], cb_s2 = h1[3], s2 = h2[1];
     const int ic = i < a.rows_pad ? i : a.rows_pad - 1;
     const float x2 = a.mode == kHalfStep ? a.xsq[ic] : 0.0f;
     const float o = a.off != nullptr ? a.off[ic] : 0.0f;
     const float old = a.meas != nullptr ? a.out[ic] : 0.0f;
     const float wi = a.meas != nullptr ? a.w[ic] : 0.0f;
+    // The first eight slots of the row (all there are up to 8 workgroups per row group) come with the scalars.
+    const int p0 = first_wg(g, a.s), p1 = last_wg(g, a.s);
+    const float2* pp = a.part + ic;
+    float2 v0[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v0[k] = p0 + k <= p1 ? pp[(size_t)k * a.rows_pad] : make_float2(kEmpty, 0.0f);
     const int skip = *skip_p;
-    asm volatile("" ::"s"(sc0), "s"(sc1), "s"(sc2), "s"(sc3), "v"(x2), "v"(o), "v"(old), "v"(wi), "v"(skip));
+    asm volatile("" ::"s"(sc0), "s"(sc1), "s"(sc2), "s"(sc3), "s"(cb), "s"(cb_s2), "s"(s2), "v"(x2), "v"(o),
+                 "v"(old), "v"(wi), "v"(skip));
     if (skip != 0) return false;
+    const float c_hs = sc0 * kLog2e;
+    // log2_ready, on the header words loaded above
+    const bool l2 = a.mode == kHalfStep && a.contraction == kF16x2 && cb != 0.0f && cb == c_hs && cb_s2 == s2;
     const float c = l2 ? 1.0f : a.mode == kHalfStep ? c_hs : kLog2e;
     float dmax = 0.0f;
     double derr = 0.0;
     if (i < a.rows_pad) {
-        const int p0 = first_wg(g, a.s), p1 = last_wg(g, a.s);
-        const float2* pp = a.part + i;
         // One pass, online: (M, S) <- (max(M, m_k), S 2^(c (M - M')) + s_k 2^(c (m_k - M'))), slots loaded eight
         // at a time so that their latencies overlap.
         float M = kEmpty, S = 0.0f;
         for (int q = p0; q <= p1; q += 8) {
             float2 v[8];
 #pragma unroll
-            for (int k = 0; k < 8; ++k) v[k] = q + k <= p1 ? pp[(size_t)(q + k - p0) * a.rows_pad] : make_float2(kEmpty, 0.0f);
+            for (int k = 0; k < 8; ++k)
+                v[k] = q == p0 ? v0[k] : q + k <= p1 ? pp[(size_t)(q + k - p0) * a.rows_pad] : make_float2(kEmpty, 0.0f);
             float Mn = M;
 #pragma unroll
             for (int k = 0; k < 8; ++k) Mn = fmaxf(Mn, v[k].x);
@@ -188,9 +196,22 @@ __device__ inline bool merge_group(const PartialArgs& a, int g) {
     return true;
 }
 
-// After the g update of one iteration, by one wave: the body of sinkhorn.py:356-378. Advances (it, stage,
-// stage_it), runs the balanced / unbalanced check at the reference's cadence, sets `done`, and writes the
-// next iteration's eps and {2/eps, 1/eps, eps, kappa}.
+// Whether the g update of an iteration must run the loop control, given (it, stage, stage_it) as the f update's
+// merge left them (already counting this iteration): a check at the reference's cadence, the last iteration,
+// or an eps-schedule step. Otherwise the control would only write the state it finds (sinkhorn.py:347-378).
+__device__ inline bool needs_control(int it, int stage, int stage_it, const LoopCfg& c) {
+    if (it >= c.max_iters) return true;
+    if (c.n_stages > 0) {
+        if (stage < c.n_stages) return stage_it % c.check_every == 0;
+        return c.fixed_iters == 0 && stage_it % c.check_every == 0;
+    }
+    if (it <= c.n_sched) return true;                 // the next iteration's eps comes from the schedule
+    return c.fixed_iters == 0 && stage_it % c.check_every == 0;
+}
+
+// After the g update of one iteration, by one wave: the body of sinkhorn.py:356-378. With (it, stage_it)
+// already advanced by the f update's merge, runs the balanced / unbalanced check at the reference's cadence,
+// advances the stage, sets `done`, and writes the next iteration's eps and {2/eps, 1/eps, eps, kappa}.
 __device__ inline void control_step(sk_state* st, const float2* meas, int nmeas, const LoopCfg& c) {
     float mx = 0.0f;
     double sm = 0.0;
@@ -206,9 +227,9 @@ __device__ inline void control_step(sk_state* st, const float2* meas, int nmeas,
     }
     if (threadIdx.x != 0) return;
     const float inv_eps = st->sc_x[1];          // 1/eps of the iteration that just ran
-    const int it = st->it + 1;
+    const int it = st->it;
     int stage = st->stage;
-    int stage_it = st->stage_it + 1;
+    int stage_it = st->stage_it;
     int conv = 0;
     if (c.n_stages > 0 && stage < c.n_stages) {
         // An intermediate stage: advance once the potentials settle or after stage_max_iters.
@@ -230,7 +251,6 @@ __device__ inline void control_step(sk_state* st, const float2* meas, int nmeas,
         }
     }
     const int done = (conv != 0 || it >= c.max_iters) ? 1 : 0;
-    st->it = it;
     st->stage = stage;
     st->stage_it = stage_it;
     st->converged = conv;
@@ -241,8 +261,22 @@ __device__ inline void control_step(sk_state* st, const float2* meas, int nmeas,
 // The merge pass: one workgroup per row group. With a loop state (the g update of the on-device loop), the
 // last workgroup to finish runs the loop control; the counter is zero on entry and reset by that workgroup.
 __global__ __launch_bounds__(kRowsPerGroup) void merge_kernel(PartialArgs a) {
+    // The g update's view of the loop counters, read before any workgroup can reach the control.
+    int it = 0, stage = 0, stage_it = 0;
+    if (a.state != nullptr) {
+        it = a.state->it;
+        stage = a.state->stage;
+        stage_it = a.state->stage_it;
+    }
     if (!merge_group(a, (int)blockIdx.x)) return;
-    if (a.state == nullptr) return;
+    if (a.tick != nullptr) {                   // the f update: count the iteration (nobody reads these meanwhile)
+        if (blockIdx.x == 0 && threadIdx.x == 0) {
+            a.tick->it += 1;
+            a.tick->stage_it += 1;
+        }
+        return;
+    }
+    if (a.state == nullptr || !needs_control(it, stage, stage_it, a.cfg)) return;
     __shared__ int s_last;
     __threadfence();                       // release: this group's outputs and meas[g]
     __syncthreads();

@@ -318,6 +318,7 @@ struct Pass {
     int n_real;
     float2* part;   // workspace: partial slots
     int* counters;  // with state: one arrival counter, zero on entry and left zero
+    sk_state* tick;   // the loop's state whose iteration counters the merge advances (f update), or null
     sk_state* state;  // loop control after the merge (g update of the loop), or null
     LoopCfg cfg;
     char* rebake;   // with state: the packed first cloud, whose log2-unit copy the control remakes on a new eps
@@ -350,6 +351,7 @@ hipError_t run_pass(const Pass& ps, const Plan& pl, hipStream_t st) {
     a.n_real = ps.n_real;
     a.counters = ps.counters;
     a.ngroups = pl.ngroups;
+    a.tick = ps.tick;
     a.state = ps.state;
     a.cfg = ps.cfg;
     a.rebake = ps.rebake;
@@ -681,6 +683,7 @@ int sk_loop_run_f32(const sk_loop_f32* L, int iters, void* stream) {
     f.out = L->fh;
     f.out2 = lo.rf;
     f.n_store = L->x.npad;
+    f.tick = st;
     f.part = part;
 
     Pass g = {};

@@ -238,27 +238,27 @@ class HipCloud:
         n, d = pts.shape
         if pad_dim(d) > KP_MAX:
             raise ValueError(f"d = {d} is above the HIP kernels' limit (d <= {KP_MAX})")
-        npad = pad_points(n)
-        P = np.zeros((npad, d))
-        P[:n] = pts
-        L = np.full(npad, PAD_LOG_WEIGHT)
-        L[:n] = log_w
-        f32 = dict(dtype=torch.float32, device=device)
         if role not in (0, 1):
             raise ValueError("role must be 0 (first cloud) or 1 (second cloud)")
+        pts = np.asarray(pts, dtype=np.float64)
         _check_range("points", float(np.abs(pts).max()) if pts.size else 0.0)
+        npad = pad_points(n)
         self.n, self.npad, self.d, self.device, self.role = n, npad, d, device, role
-        self.sq = torch.as_tensor((P * P).sum(axis=1), dtype=torch.float32).to(device)
-        self.log_w = torch.as_tensor(L, dtype=torch.float32).to(device)
-        self.w = torch.as_tensor(np.exp(L), dtype=torch.float32).to(device)
+        # |p|^2 (float64 sums), log w, w and the offset in one host array and one copy to the device; padding
+        # points have |p|^2 = 0, log weight PAD_LOG_WEIGHT (weight exactly 0) and no offset
+        vec = np.zeros((3 if off is None else 4, npad), dtype=np.float32)
+        vec[0, :n] = (pts * pts).sum(axis=1)           # as the reference sums them (float64), then cast
+        L = np.full(npad, PAD_LOG_WEIGHT)
+        L[:n] = log_w
+        vec[1] = L
+        vec[2] = np.exp(L)
         if off is not None:
-            O = np.zeros(npad)
-            O[:n] = off
-            self.off = torch.as_tensor(O, dtype=torch.float32).to(device)
-        else:
-            self.off = None
-        self.zero_off = torch.zeros(npad, **f32)
-        pts32 = torch.as_tensor(P, dtype=torch.float32).to(device)
+            vec[3, :n] = off
+        dv = torch.from_numpy(vec).to(device)
+        self.sq, self.log_w, self.w = dv[0], dv[1], dv[2]
+        self.off = dv[3] if off is not None else None
+        # the points unpadded: the packing pads them to npad x kp with zeros
+        pts32 = torch.from_numpy(np.ascontiguousarray(pts, dtype=np.float32)).to(device)
         self.pk = pack_cloud(pts32)
 
     def c_struct(self) -> SkCloud:

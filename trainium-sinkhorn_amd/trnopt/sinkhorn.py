@@ -309,7 +309,10 @@ def _prepare(x, y, a, b, opts: SinkhornOptions, a_target, b_target, hip: bool = 
     else:
         center, scale = np.zeros(x.shape[1]), 1.0
     root = np.sqrt(scale)
-    xs, ys = (x - center) / root, (y - center) / root
+    if np.any(center != 0.0) or root != 1.0:
+        xs, ys = (x - center) / root, (y - center) / root
+    else:                                   # (x - 0) / 1 is x exactly: no copies
+        xs, ys = x, y
     stages = [e for e in (opts.eps_stages or ()) if e > opts.eps]
     sched = []
     if not stages and opts.eps_start is not None and opts.eps_start > opts.eps:

@@ -107,6 +107,26 @@ def test_stress_65k_last_update_matches_float64_on_sampled_columns():
     assert err < 1e-5
 
 
+@pytest.mark.parametrize("log2", ["0", "1"])
+def test_both_score_paths_match_reference(monkeypatch, log2):
+    """The loop with x's log2-unit copy (scores in log2 units, the default) and without it (TRNOPT_HIP_LOG2=0:
+    scores scaled on the VALU): the 2048 x 2048 d 64 workload, 100 fixed iterations, and an eps-scaling solve
+    (a copy remade at every eps of the schedule), both within 1e-5 of the oracle's float64 run."""
+    monkeypatch.setenv("TRNOPT_HIP_LOG2", log2)
+    x, y = data.balanced_gaussian()
+    o = dict(eps=0.1, normalize=False, max_iters=100, fixed_iters=True)
+    print("hip 2048 d64, log2 copy", log2, flush=True)
+    res = sinkhorn(x, y, opts=hip_opts(**o))
+    r64 = ref.sinkhorn_ref(x, y, dtype=torch.float64, **o)
+    assert inf_rel(res.f, r64.f) < 1e-5 and inf_rel(res.g, r64.g) < 1e-5, (inf_rel(res.f, r64.f), inf_rel(res.g, r64.g))
+    x, y = data.clouds(n=600, m=500, d=16, seed=4)
+    o = dict(eps=0.05, eps_start=1.0, eps_decay=0.8, tol=1e-6, max_iters=3000)
+    res = sinkhorn(x, y, opts=hip_opts(**o))
+    r64 = ref.sinkhorn_ref(x, y, dtype=torch.float64, **o)
+    assert res.converged and abs(res.iterations - r64.iterations) <= 10, (res.iterations, r64.iterations)
+    assert inf_rel(res.f, r64.f) < 1e-5 and inf_rel(res.g, r64.g) < 1e-5, (inf_rel(res.f, r64.f), inf_rel(res.g, r64.g))
+
+
 @pytest.mark.parametrize("iters", [1, 2, 7])
 def test_first_iterations_match_dense_float64(iters):
     """Iterate-by-iterate: the reference's init (g0 = |y|^2) and update order against the dense brute force."""

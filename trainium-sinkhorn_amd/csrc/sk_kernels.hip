@@ -13,31 +13,36 @@
 // the power-of-two scaled fp32 coordinates (sk_lse_partial.hip), bit-identical in the f and g updates; the
 // column term is added on the VALU. The running (max, sum) of a row is kept as
 //
-//     eps * lse_i = 2 M_i + eps ln(2) log2 S_i,   S_i = sum_j exp2(c (a_ij - M_i)),  M_i = max_j a_ij.
+//     eps * lse_i = 2 M_i + eps ln(2) log2 S_i,   S_i = sum_j exp2(c (a_ij - M_i)),  M_i = max_j a_ij,
+//
+// or, when x carries its log2-unit copy (bake_log2_kernel), with M_i in log2 units (c a) and the loop's
+// potentials in log2 units too (sk_epilogue.h).
 //
 // Packed cloud layout. A 256-byte header ([0] max |coordinate| as float bits, [1] the scale s, a power of
-// two with max |coordinate| * s in [2^13, 2^14)), then the tiles: points padded to a multiple of 32,
+// two with max |coordinate| * s in [2^4, 2^5), [2], [3] the log2-unit copy's tag), then the tiles: points
+// padded to a multiple of 32,
 // coordinates to kp = 16 * nc, every scaled coordinate v = s x stored as two fp16 pieces (v0 = fp16(v),
 // v1 = fp16(v - v0)). Within tile T, the 16-byte unit ((T * nc + c) * 2 + p) * 64 + 32 h + r holds piece p
 // of coordinates [16 c + 8 h, 16 c + 8 h + 8) of point 32 T + r: lane l = 32 h + r reads its
 // v_mfma_f32_32x32x16_f16 operand for K chunk c with one coalesced 16-byte load (a wave reads 1 KB
 // contiguous). The same layout serves a cloud as rows (one half-step) and as columns (the other).
-// 4 kp bytes per point.
+// 4 kp bytes per point, and as many again for the log2-unit copy that follows.
 //
 // Work decomposition ("stream-K" over row groups x column tiles). A workgroup is 4 waves, one per SIMD;
-// wave w owns 2 row blocks of 32 rows of a row group (256 rows) and all 4 waves walk the same column tiles,
-// which the workgroup stages in LDS once. The (row group, column tile) units are split into equal contiguous
-// ranges, one per workgroup (one workgroup per CU), so every workgroup does the same amount of MFMA work
-// whatever n and m are. A range may end inside a row group; each (workgroup, row group) segment writes a
-// partial (M, S) per row into its own slot, and a finalisation pass merges the slots of every row and
-// applies the kappa / offset epilogue.
+// wave w owns 2 row blocks of 32 rows of a row group (256 rows) and all 4 waves walk the same column tiles.
+// The (row group, column tile) units are split into contiguous ranges of equal cost, one per workgroup (one
+// workgroup per CU; a row-group boundary inside a range costs as much as a few tiles, Split), so every
+// workgroup does about the same work whatever n and m are. A range may end inside a row group; each
+// (workgroup, row group) segment writes a partial (M, S) per row into its own slot, and the merge pass merges
+// the slots of every row and applies the kappa / offset epilogue.
 //
 // A half-step is two launches: the partial kernel, then the merge kernel (sk_epilogue.h), one workgroup per
 // row group, which merges the group's slots and applies the epilogue. The on-device loop
-// (src/trnopt/sinkhorn.py:346-378) is four launches per iteration: in the g update the merge also produces
-// per-group convergence partials, and the last merge workgroup to finish advances (it, stage, stage_it), runs
-// the balanced / unbalanced checks at the reference's cadence, sets `done`, and writes the next iteration's
-// eps and {2/eps, 1/eps, eps, kappa} into the device state. Every loop kernel returns immediately once `done`
+// (src/trnopt/sinkhorn.py:346-378) is four launches per iteration: the f update's merge counts the iteration;
+// in the g update the merge also produces per-group convergence partials, and at a check, a schedule step or
+// the last iteration its last workgroup to finish runs the balanced / unbalanced checks at the reference's
+// cadence, advances the stage, sets `done`, and writes the next iteration's eps and {2/eps, 1/eps, eps,
+// kappa} into the device state (remaking x's log2-unit copy when eps changes). Every loop kernel returns immediately once `done`
 // is set, so the host may enqueue whole batches of iterations.
 
 #include <hip/hip_runtime.h>

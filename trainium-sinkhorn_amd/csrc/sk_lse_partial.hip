@@ -4,7 +4,7 @@
 // IEEE mode would first be canonicalised one by one. No value here is NaN or infinite: padding and empty
 // rows use large finite sentinels.
 //
-// Contraction. Every packed cloud carries a power-of-two scale s (max |coordinate| * s in [2^13, 2^14)),
+// Contraction. Every packed cloud carries a power-of-two scale s (max |coordinate| * s in [2^4, 2^5)),
 // and every scaled coordinate v = s x is stored as two fp16 pieces v = v0 + v1 (22 significand bits: within
 // 2^-23 of v, about one fp32 ulp; sk_kernels.hip packs them). The dot product of two scaled points is
 // accumulated in fp32 by v_mfma_f32_32x32x16_f16 from the three products
@@ -15,6 +15,9 @@
 // an fp32 dot product (error ~1e-7 of sum |x_k y_k| on N(0, 1) data; a float32 dot product gives ~2.3e-7,
 // the fp32 MFMA chain 3.2e-7). With sigma = s_x s_y, the kernel works in scaled accumulator units
 // sigma a = D + sigma (column term) and c / sigma, all exact power-of-two rescalings, and stores M / sigma.
+// When the first cloud carries its log2-unit copy (pieces of fl(c x) / s_y) for this launch's c, the same
+// three products of the copy and the second cloud's own pieces give c x.y: the scores are in log2 units and
+// the exponentials take them without a multiply (L2 below); M is stored in log2 units.
 // On gfx950 the fp16 matrix pipe runs at ~15x the fp32 MFMA rate and, unlike the fp32 MFMA, issues alongside
 // VALU work of the same SIMD, so the exp / max / sum epilogue of one tile hides under the MFMAs of the next.
 // The general row log-sum-exp of arbitrary fp32 matrices (whose columns may mix magnitudes 1e9 apart, as the

@@ -217,6 +217,41 @@ def test_half_step_with_log2_copy_matches_float64(hip, rows, m, d, eps, kappa, m
             assert np.array_equal(got, vpu)
 
 
+@pytest.mark.parametrize("eps,gscale,bake", [(0.1, 1e-3, False), (0.1, 1e-3, True), (0.1, 3e2, True),
+                                             (0.01, 3e4, True), (1.0, 1e6, False), (1.0, 1e6, True)])
+def test_half_step_column_terms_across_magnitudes(hip, eps, gscale, bake):
+    """The matrix pipe adds each column term (gh_j + eps log b_j) / 2, in the kernel's units, as three fp16
+    pieces: column terms from 1e-3 to 1e6 times the dot products, and a fifth of the columns masked by
+    log b = -1e9 (weight exactly 0), meet the float64 known answer, with and without the log2-unit copy."""
+    rows, m, d = 300, 2000, 16
+    rng = np.random.default_rng(int(gscale) + int(100 * eps) + bake)
+    x = rng.normal(size=(rows, d))
+    y = rng.normal(size=(m, d)) * 0.8 + 0.3
+    gh = rng.normal(size=m) * gscale * np.exp(rng.uniform(-3, 0, m))    # magnitudes over three decades
+    log_b = np.log(rng.uniform(0.5, 1.5, m) / m)
+    log_b[rng.random(m) < 0.2] = -1e9
+    X = hip.HipCloud(x, np.zeros(rows), DEV, role=0)
+    Y = hip.HipCloud(y, log_b, DEV, role=1)
+    ghp = torch.zeros(Y.npad, dtype=torch.float32, device=DEV)
+    ghp[:m] = torch.as_tensor(gh, dtype=torch.float32)
+    sc = hip.scalars(eps, 1.0, DEV)
+    if bake:
+        hip.bake_log2(X, Y, sc)
+        torch.cuda.synchronize()
+        assert _log2_tag(X) != 0.0
+    print(f"column terms eps={eps} gscale={gscale} bake={bake}", flush=True)
+    out = hip.half_step(X, Y, ghp, sc).cpu().numpy()[:rows].astype(np.float64)
+    x32, y32 = x.astype(np.float32), y.astype(np.float32)
+    xsq32 = (x * x).sum(1).astype(np.float32)
+    keep = log_b > -1e8
+    want = brute.half_step_f64(x32, xsq32, np.zeros(rows), y32, gh.astype(np.float32),
+                               log_b.astype(np.float32), eps, 1.0)
+    want_kept = brute.half_step_f64(x32, xsq32, np.zeros(rows), y32[keep], gh.astype(np.float32)[keep],
+                                    log_b.astype(np.float32)[keep], eps, 1.0)
+    np.testing.assert_allclose(want, want_kept, rtol=1e-13, atol=0)
+    assert inf_rel(out, want) < 2e-6, inf_rel(out, want)
+
+
 @pytest.mark.parametrize("d", [3, 16, 64, 128])
 def test_log2_copy_keeps_f_and_g_dots_bit_identical(hip, d):
     """On the log2-unit copy the f update (rows x) and the g update (rows y) of one pair of clouds still form

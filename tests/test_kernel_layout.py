@@ -14,6 +14,9 @@ from scipy.special import logsumexp
 
 TILE, WAVES, XCDS, RB, BLOCK = 32, 4, 8, 2, 256
 STREAM_MAX_CHUNKS, COL_TILES = 4, 256        # streamed variant: nc <= 4; column terms staged per 256 tiles
+FOLD_COL_TILES = 192                         # ... per 192 tiles with the f16x2 contraction (folded, 16 B each)
+FOLD_MAX = np.float32(2.0 ** 30)             # folded column terms are clamped to +-2^30
+FOLD_SCALES = (2.0 ** 15, 2.0 ** 4, 2.0 ** -7)
 SEG_COST_STREAMED, SEG_COST_STAGED = 4, 2    # cost of a row-group boundary in tiles (sk_kernels.hip make_plan)
 ROWS_PER_GROUP = TILE * RB * WAVES
 EMPTY = -1.0e30
@@ -64,6 +67,25 @@ def split3(v):
     a1 = bf16_rne(r1)
     a2 = bf16_rne((r1 - a1).astype(np.float32))
     return a0, a1, a2
+
+
+def fold_split(v):
+    """Streamed tiles with the f16x2 contraction: a column term v as three fp16 pieces, the A operand of one
+    MFMA against B = (2^15, 2^4, 2^-7): v = q0 2^15 + q1 2^4 + q2 2^-7 after clamping to +-2^30
+    (sk_lse_partial.hip, Streamed::run's stage_cols). Returns the pieces as float32 values."""
+    w = (np.clip(np.asarray(v, dtype=np.float32), -FOLD_MAX, FOLD_MAX) * np.float32(2.0 ** -15)).astype(np.float32)
+    q0 = w.astype(np.float16).astype(np.float32)
+    r1 = ((w - q0) * np.float32(2.0 ** 11)).astype(np.float32)
+    q1 = r1.astype(np.float16).astype(np.float32)
+    q2 = ((r1 - q1) * np.float32(2.0 ** 11)).astype(np.float32).astype(np.float16).astype(np.float32)
+    return q0, q1, q2
+
+
+def fold_b_operand():
+    """B of the column MFMA, per lane: the three scales in k = 0, 1, 2 of lanes 0-31, zeros elsewhere."""
+    b = np.zeros((64, 8), dtype=np.float32)
+    b[:32, :3] = FOLD_SCALES
+    return b
 
 
 def pack(src, n, d, contraction="f16x2"):
@@ -181,6 +203,7 @@ def emulate_lse(xa, ya, role=0, ncu=256, per_cu=1, c=np.log2(np.e), contraction=
     with np.errstate(over="ignore"):
         u = np.maximum((u_raw * sigma).astype(np.float32), PAD_SCORE)     # scaled column term, floored
     nrb, nt, ngroups, s, slots = plan(rp, mp, ncu, per_cu, nc=nc)
+    fold = contraction == "f16x2" and nc <= STREAM_MAX_CHUNKS
     part = np.full((slots, rp, 2), np.nan)
     lane = np.arange(64)
     h = lane >> 5
@@ -202,16 +225,22 @@ def emulate_lse(xa, ya, role=0, ncu=256, per_cu=1, c=np.log2(np.e), contraction=
             seen[g, tb:te] += 1
             staged = {}
             if nc <= STREAM_MAX_CHUNKS:
-                # streamed: column terms of runs of COL_TILES tiles into LDS; operands straight from memory
-                lds_col = np.full(COL_TILES * 32, np.nan, dtype=np.float32)
-                for t0 in range(tb, te, COL_TILES):
-                    t1 = min(t0 + COL_TILES, te)
+                # streamed: column terms of runs of col_tiles tiles into LDS; operands straight from memory.
+                # Folded (f16x2): 16 bytes per column, the A operand of the column MFMA (lane l: column l % 32).
+                col_tiles = FOLD_COL_TILES if fold else COL_TILES
+                lds_col = np.full((col_tiles * 32, 8) if fold else col_tiles * 32, np.nan, dtype=np.float32)
+                for t0 in range(tb, te, col_tiles):
+                    t1 = min(t0 + col_tiles, te)
                     k = np.arange((t1 - t0) * 32)
-                    assert k.max() < lds_col.size and (t0 * 32 + k).max() < mp
-                    lds_col[k] = u[t0 * 32 + k]
+                    assert k.max() < lds_col.shape[0] and (t0 * 32 + k).max() < mp
+                    if fold:
+                        lds_col[k] = 0.0
+                        lds_col[k, 0], lds_col[k, 1], lds_col[k, 2] = fold_split(u[t0 * 32 + k])
+                    else:
+                        lds_col[k] = u[t0 * 32 + k]
                     for t in range(t0, t1):
-                        rd = (t - t0) * 32 + np.arange(32)
-                        assert rd.max() < lds_col.size
+                        rd = (t - t0) * 32 + (lane & 31 if fold else np.arange(32))
+                        assert rd.max() < lds_col.shape[0]
                         gi = t * tile16 + np.arange(tile16)
                         assert gi.max() < yc.shape[0]
                         staged[t] = (yc[gi].copy(), lds_col[rd].copy())
@@ -247,14 +276,18 @@ def emulate_lse(xa, ya, role=0, ncu=256, per_cu=1, c=np.log2(np.e), contraction=
                             + lane[None, None, :]
                         assert yi.max() < tile16
                         yv = ybuf[yi]
-                        ci = 8 * np.arange(4)[None, :, None] + 4 * h[:, None, None] + np.arange(4)[None, None, :]
-                        assert ci.max() < 32
-                        col = cbuf[ci].reshape(64, 16)
                         acc = np.zeros((64, 16))
                         for cc in range(nc):
                             for pp in range(len(FIRST_)):
                                 acc += mfma_32x32x16(yv[cc, ca[pp]], xv[cc, ra[pp]])
-                        a = (acc.astype(np.float32) + col).astype(np.float32)
+                        if fold:                                   # the column MFMA, after the dot product
+                            acc += mfma_32x32x16(cbuf, fold_b_operand())
+                            a = acc.astype(np.float32)
+                        else:
+                            ci = 8 * np.arange(4)[None, :, None] + 4 * h[:, None, None] + np.arange(4)[None, None, :]
+                            assert ci.max() < 32
+                            col = cbuf[ci].reshape(64, 16)
+                            a = (acc.astype(np.float32) + col).astype(np.float32)
                         Mn = np.maximum(M, a.max(axis=1))
                         with np.errstate(over="raise", invalid="raise"):
                             S = S * np.exp2(cf * (M - Mn)) + np.exp2(cf * (a - Mn[:, None])).sum(axis=1)
@@ -500,3 +533,31 @@ def test_split3_is_exact_over_the_fp32_range():
         for a in (a0, a1, a2):
             assert np.all((a.view(np.uint32) & 0xFFFF) == 0)
         np.testing.assert_array_equal(a0.astype(np.float64) + a1 + a2, v.astype(np.float64))
+
+
+def test_fold_split_reproduces_column_terms():
+    """The folded column term: three fp16 pieces against (2^15, 2^4, 2^-7) reproduce any fp32 value in
+    [-2^30, 2^30] to within 2^-32 absolute, exactly from magnitude 2^-8 on; beyond, the clamp. The padding
+    floor (-1e30) becomes -2^30, 8 times the largest dot product the kernel forms (below 2^20 d <= 2^27 in its
+    units: pieces below 2^15 and 2^5)."""
+    rng = np.random.default_rng(5)
+    for scale in (1e-30, 1e-9, 1e-3, 0.3, 1.0, 7.3e2, 6.1e4, 1e7, 3e8):
+        v = (rng.normal(size=200_000) * scale).astype(np.float32)
+        v = v[np.abs(v) <= FOLD_MAX]
+        q0, q1, q2 = fold_split(v)
+        for q in (q0, q1, q2):
+            assert np.all(np.isfinite(q)) and np.all(np.abs(q) <= 65504)
+        back = q0.astype(np.float64) * FOLD_SCALES[0] + q1.astype(np.float64) * FOLD_SCALES[1] \
+            + q2.astype(np.float64) * FOLD_SCALES[2]
+        err = np.abs(back - v.astype(np.float64))
+        assert err.max() <= 2.0 ** -32, (scale, err.max())
+        big = np.abs(v) >= 2.0 ** -8
+        np.testing.assert_array_equal(back[big], v[big].astype(np.float64))
+    q0, q1, q2 = fold_split(np.array([-1e30, 1e30, 2.0 ** 30, -3e9], dtype=np.float32))
+    back = q0.astype(np.float64) * FOLD_SCALES[0] + q1 * FOLD_SCALES[1] + q2 * FOLD_SCALES[2]
+    np.testing.assert_array_equal(back, [-2.0 ** 30, 2.0 ** 30, 2.0 ** 30, -2.0 ** 30])
+    # a plausible slip, the middle scale off by one binade, is caught
+    v = (rng.normal(size=1000) * 100).astype(np.float32)
+    q0, q1, q2 = fold_split(v)
+    wrong = q0.astype(np.float64) * 2.0 ** 15 + q1 * 2.0 ** 5 + q2 * 2.0 ** -7
+    assert np.abs(wrong - v).max() > 1e-3

@@ -31,15 +31,18 @@
 // directions agree when they issue the same (x piece, y piece) pairs in the same order (sigma is the same
 // product of the two scales in both directions): `rows_role` says
 // whether the rows are the first or the second cloud, and the pair list is transposed accordingly. The
-// contraction starts from zero and the column term is added afterwards on the VALU; the max is subtracted
-// before scaling, exp2(c (a - M)), so the dominant term is exactly 1.
+// contraction starts from zero and the column term is added afterwards: by one more MFMA per row block and
+// tile in the streamed fp16 variant (the term as three fp16 pieces against (2^15, 2^4, 2^-7), exact for
+// terms in [-2^30, 2^30], clamped beyond; 32 VALU adds per tile fewer), on the VALU otherwise. The max is
+// subtracted before scaling, exp2(c (a - M)), so the dominant term is exactly 1.
 //
 // Layout of one workgroup (4 waves, one per SIMD of a CU): wave w owns kRowBlocks blocks of 32 rows of a
 // row group (its fp16 pieces stay in registers for the whole work segment), and all four waves walk the same
 // column tiles. Two ways to feed the column tiles, chosen by size:
 //   - streamed (kp <= 64): every wave loads the tile's pieces straight into registers one tile ahead; the
 //     four waves of the CU read the same addresses at about the same time and share them through L1. The
-//     column terms of the whole segment are computed once into LDS. No per-tile barrier.
+//     column terms of the whole segment are computed once into LDS (as MFMA operands with the fp16
+//     contraction). No per-tile barrier.
 //   - staged (kp > 64, where a register double buffer no longer fits): the workgroup stages each tile and
 //     its 32 column terms once in LDS (double buffered, one barrier per tile).
 // MFMA orientation: A = 32 columns, B = 32 rows, so lane l's 16 accumulators all belong to row l % 32
@@ -98,6 +101,9 @@ __device__ __forceinline__ void static_for(F&& f) {
 //   j in [41, 56): the sum of the 16 exponentials as a pairwise tree (8 + 4 + 2 + 1 adds), long after the
 //                  exponentials were issued, so no add waits on the transcendental unit
 //   j == 56:       S = S exp2(c (M - m)) + sum, M = m
+// With FOLD the matrix pipe has already added the column terms (one more MFMA per row block and tile, see
+// Streamed) and steps 1-16 are empty; step 0 only starts the running max, costed so that the first reads of
+// the accumulators come a few MFMA slots after the last MFMA of the tile.
 // The max is subtracted before the scaling: a - m is exact for the scores near the maximum, so the dominant
 // term is exactly 1 and S is relative to 2^(c M) exactly, which is what the merge of the slots assumes.
 // (Folding the offset into one fma, exp2(c a - fl(c m)), would leave S relative to the rounded fl(c M): an
@@ -105,27 +111,31 @@ __device__ __forceinline__ void static_for(F&& f) {
 // and holds float32 Sinkhorn several ulps away from its fixed point.)
 // Steps are spread over the MFMA slots of the next tile in proportion to their cost.
 constexpr int kOps = 57;
-constexpr int op_cost(int j) { return j == 0 ? 8 : (j >= 25 && j < 41) ? 4 : j == 56 ? 4 : 1; }
+template <bool FOLD>
+constexpr int op_cost(int j) {
+    return FOLD && j > 0 && j < 17 ? 0 : j == 0 ? (FOLD ? 6 : 8) : (j >= 25 && j < 41) ? 4 : j == 56 ? 4 : 1;
+}
+template <bool FOLD>
 constexpr int block_cost() {
     int s = 0;
-    for (int j = 0; j < kOps; ++j) s += op_cost(j);
+    for (int j = 0; j < kOps; ++j) s += op_cost<FOLD>(j);
     return s;
 }
 // First step of slot i of NS (steps of the row blocks interleaved: step k is step k / RB of block k % RB).
-template <int RB>
+template <int RB, bool FOLD>
 constexpr int op_begin(int i, int NS) {
-    const int target = (int)((long long)i * RB * block_cost() / NS);
+    const int target = (int)((long long)i * RB * block_cost<FOLD>() / NS);
     int cost = 0, k = 0;
     while (k < RB * kOps && cost < target) {
-        cost += op_cost(k / RB);
+        cost += op_cost<FOLD>(k / RB);
         ++k;
     }
     return k;
 }
 
-// col4(q) returns the column terms of accumulators 4q .. 4q + 3 of the tile being updated. With L2 the scores
-// are already in log2 units (the first cloud's log2-unit copy) and c is not applied.
-template <int RB, bool L2>
+// col4(q) returns the column terms of accumulators 4q .. 4q + 3 of the tile being updated (unused with FOLD).
+// With L2 the scores are already in log2 units (the first cloud's log2-unit copy) and c is not applied.
+template <int RB, bool L2, bool FOLD = false>
 struct Online {
     float m[RB];
     f32x4 cv[4];
@@ -133,16 +143,23 @@ struct Online {
     __device__ __forceinline__ void step(f32x16 (&acc)[RB], ColFn&& col4, float (&M)[RB], float (&S)[RB], float c) {
         constexpr int j = k / RB, b = k % RB;
         if constexpr (j == 0) {
-            if constexpr (b == 0)
+            if constexpr (b == 0 && !FOLD)
 #pragma unroll
                 for (int q = 0; q < 4; ++q) cv[q] = col4(q);
             m[b] = M[b];
         } else if constexpr (j < 17) {
-            constexpr int r = j - 1;
-            acc[b][r] = acc[b][r] + cv[r / 4][r % 4];
+            if constexpr (!FOLD) {
+                constexpr int r = j - 1;
+                acc[b][r] = acc[b][r] + cv[r / 4][r % 4];
+            }
         } else if constexpr (j < 25) {
             constexpr int p = j - 17;
-            m[b] = max3(m[b], acc[b][2 * p], acc[b][2 * p + 1]);
+            // With FOLD the operands come straight from the MFMAs: a compiler-visible maximum, so that the
+            // compiler keeps the wait states between the matrix results and their first VALU read.
+            if constexpr (FOLD)
+                m[b] = __builtin_fmaxf(__builtin_fmaxf(m[b], acc[b][2 * p]), acc[b][2 * p + 1]);
+            else
+                m[b] = max3(m[b], acc[b][2 * p], acc[b][2 * p + 1]);
         } else if constexpr (j < 41) {
             constexpr int r = j - 25;
             acc[b][r] = L2 ? ex2(acc[b][r] - m[b]) : ex2(c * (acc[b][r] - m[b]));
@@ -291,7 +308,7 @@ struct Staged {
                 constexpr int cp = ROLE == 0 ? C::second[p] : C::first[p];
                 accN[b] = C::mfma(yv[cc][cp], xv[b][cc][rp], accN[b]);
                 if (epi) {
-                    constexpr int k0 = op_begin<RB>(i, NS), k1 = op_begin<RB>(i + 1, NS);
+                    constexpr int k0 = op_begin<RB, false>(i, NS), k1 = op_begin<RB, false>(i + 1, NS);
                     static_for<k0, k1>([&](auto K) { on.template step<decltype(K)::value>(accP, col4, M, S, c); });
                 }
                 __builtin_amdgcn_sched_barrier(0);
@@ -348,9 +365,12 @@ struct Staged {
     }
 };
 
-// Column terms computed into LDS once per run of kColTiles tiles (streamed variant).
-constexpr int kColTiles = 256;
+// Column terms computed into LDS once per run of col_tiles(fold) tiles (streamed variant), 16 bytes per column
+// with FOLD (98 KB of LDS), 4 without (33 KB).
+constexpr int col_tiles(bool fold) { return fold ? 192 : 256; }
+constexpr int col_floats(bool fold) { return fold ? col_tiles(fold) * 32 * 4 : (col_tiles(fold) + 1) * 32; }
 constexpr int kColBatch = 8;
+constexpr float kFoldMax = 0x1p30f;   // column terms beyond +-2^30 (kernel units) are clamped with FOLD
 constexpr int kStreamMaxChunks = 4;
 
 template <int NC, int ROLE, int CT, bool L2>
@@ -362,6 +382,8 @@ struct Streamed {
     static constexpr int RB = kRowBlocks;
     static constexpr int TILE16 = NC * kPieces * 64;
     static constexpr int NS = kProducts * NC * RB;
+    static constexpr bool FOLD = CT == kF16x2;      // column terms added by the matrix pipe
+    static constexpr int kColTiles = col_tiles(FOLD);
 
     __device__ __forceinline__ static void run(const PartialArgs& a, int rb0, int tb, int te, int slot, const float* cu,
                                                float alpha, float beta, float cs, float c, float inv_sigma,
@@ -391,12 +413,14 @@ struct Streamed {
             S[b] = 0.0f;
         }
 
-        // Column terms of tiles [t0 - 1, t1) into LDS (tile t at (t - cbase) * 32): the update of tile t0 - 1
-        // still runs while tile t0's MFMAs do.
+        // Column terms into LDS, tile t at (t - cbase) * 32. Without FOLD: tiles [t0 - 1, t1), one float per
+        // column (the update of tile t0 - 1 still runs while tile t0's MFMAs do). With FOLD: tiles [t0, t1), each
+        // column term q clamped to [-2^30, 2^30] and stored as the A operand of one MFMA, eight fp16 values
+        // (q0, q1, q2, 0, ...) with q = q0 2^15 + q1 2^4 + q2 2^-7 (exact: each piece takes the next 11 bits).
         int cbase = tb - 1;
         auto stage_cols = [&](int t0, int t1) {
             __syncthreads();
-            const int n = (t1 - t0 + 1) * 32, base = (t0 - 1) * 32;
+            const int n = (t1 - t0 + (FOLD ? 0 : 1)) * 32, base = (t0 - (FOLD ? 0 : 1)) * 32;
             // Eight column terms per thread per batch, all sixteen loads in flight before the first use (a
             // run of up to 256 tiles takes at most five batches, a typical segment one).
             for (int k0 = 0; k0 < n; k0 += kColBatch * kBlock) {
@@ -411,11 +435,23 @@ struct Streamed {
 #pragma unroll
                 for (int q = 0; q < kColBatch; ++q) {
                     const int k = k0 + q * kBlock + tid, j = base + k;
-                    if (k < n && j >= 0) lds_col[k] = fmaxf(cs * fmaf(beta, vv[q], alpha * uu[q]), kPadScore);
+                    if (k < n && j >= 0) {
+                        const float v = fmaxf(cs * fmaf(beta, vv[q], alpha * uu[q]), kPadScore);
+                        if constexpr (FOLD) {
+                            const float w = fminf(fmaxf(v, -kFoldMax), kFoldMax) * 0x1p-15f;   // exact scaling
+                            const _Float16 q0 = (_Float16)w;
+                            const float r1 = (w - (float)q0) * 0x1p11f;
+                            const _Float16 q1 = (_Float16)r1;
+                            const _Float16 q2 = (_Float16)((r1 - (float)q1) * 0x1p11f);
+                            reinterpret_cast<f16x8*>(lds_col)[k] = f16x8{q0, q1, q2, 0, 0, 0, 0, 0};
+                        } else {
+                            lds_col[k] = v;
+                        }
+                    }
                 }
             }
             __syncthreads();
-            cbase = t0 - 1;
+            cbase = t0 - (FOLD ? 0 : 1);
         };
         T yA[NC][kPieces], yB[NC][kPieces];
         auto load_y = [&](int t, T (&yv)[NC][kPieces]) {
@@ -425,12 +461,20 @@ struct Streamed {
                 for (int p = 0; p < kPieces; ++p) yv[cc][p] = yt[(size_t)t * TILE16 + (cc * kPieces + p) * 64 + lane];
         };
         auto colp_of = [&](int t) { return lds_col + (t - cbase) * 32 + 4 * h; };
+        // With FOLD, the A operand of tile t's column MFMA (lane l: column l % 32; lanes 32-63 meet zeros in B)
+        // and the B operand (2^15, 2^4, 2^-7 in k = 0, 1, 2 of every row, zeros elsewhere).
+        auto colA_of = [&](int t) { return reinterpret_cast<const f16x8*>(lds_col)[(t - cbase) * 32 + (lane & 31)]; };
+        const _Float16 e0 = h == 0 ? (_Float16)0x1p15f : (_Float16)0, e1 = h == 0 ? (_Float16)0x1p4f : (_Float16)0,
+                       e2 = h == 0 ? (_Float16)0x1p-7f : (_Float16)0;
+        const f16x8 colB = {e0, e1, e2, 0, 0, 0, 0, 0};
 
         f32x16 accA[RB], accB[RB];
-        Online<RB, L2> on;
+        Online<RB, L2, FOLD> on;
         auto tile = [&](f32x16 (&accN)[RB], f32x16 (&accP)[RB], const float* colp, const T (&yv)[NC][kPieces],
-                        bool epi) {
+                        int t, bool epi) {
             auto col4 = [&](int q) { return *reinterpret_cast<const f32x4*>(colp + 8 * q); };
+            f16x8 colA;
+            if constexpr (FOLD) colA = colA_of(t);
 #pragma unroll
             for (int b = 0; b < RB; ++b) accN[b] = f32x16{};
             static_for<0, NS>([&](auto I) {
@@ -440,11 +484,17 @@ struct Streamed {
                 constexpr int cp = ROLE == 0 ? C::second[p] : C::first[p];
                 accN[b] = C::mfma(yv[cc][cp], xv[b][cc][rp], accN[b]);
                 if (epi) {
-                    constexpr int k0 = op_begin<RB>(i, NS), k1 = op_begin<RB>(i + 1, NS);
+                    constexpr int k0 = op_begin<RB, FOLD>(i, NS), k1 = op_begin<RB, FOLD>(i + 1, NS);
                     static_for<k0, k1>([&](auto K) { on.template step<decltype(K)::value>(accP, col4, M, S, c); });
                 }
                 __builtin_amdgcn_sched_barrier(0);
             });
+            // The column terms last, after the whole dot product: x.y is formed identically in both directions.
+            if constexpr (FOLD) {
+#pragma unroll
+                for (int b = 0; b < RB; ++b)
+                    accN[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(colA, colB, accN[b], 0, 0, 0);
+            }
         };
         auto update = [&](f32x16 (&accP)[RB], const float* colp) {
             auto col4 = [&](int q) { return *reinterpret_cast<const f32x4*>(colp + 8 * q); };
@@ -461,7 +511,7 @@ struct Streamed {
         load_y(t, yA);
         load_y(t + 1 < te ? t + 1 : last, yB);
         stage_cols(tb, cend);
-        tile(accA, accB, nullptr, yA, false);
+        tile(accA, accB, nullptr, yA, t, false);
         ++t;
         while (t < te) {
             if (t >= cend) {
@@ -469,7 +519,7 @@ struct Streamed {
                 stage_cols(t, cend);
             }
             load_y(t + 1 < te ? t + 1 : last, yA);
-            tile(accB, accA, colp_of(t - 1), yB, true);
+            tile(accB, accA, colp_of(t - 1), yB, t, true);
             ++t;
             if (t >= te) {
                 update(accB, colp_of(t - 1));
@@ -480,7 +530,7 @@ struct Streamed {
                 stage_cols(t, cend);
             }
             load_y(t + 1 < te ? t + 1 : last, yB);
-            tile(accA, accB, colp_of(t - 1), yA, true);
+            tile(accA, accB, colp_of(t - 1), yA, t, true);
             ++t;
         }
         update(accA, colp_of(t - 1));
@@ -531,7 +581,7 @@ void lse_partial_kernel(PartialArgs a) {
     if (skip != 0) return;
     constexpr bool kStream = NC <= kStreamMaxChunks;
     constexpr int kLdsY = kStream ? 1 : 2 * NC * Contract<CT>::pieces * 64;
-    constexpr int kLdsCol = kStream ? (kColTiles + 1) * 32 : 3 * 32;
+    constexpr int kLdsCol = kStream ? col_floats(CT == kF16x2) : 3 * 32;
     __shared__ typename Contract<CT>::T lds_y[kLdsY];
     __shared__ __attribute__((aligned(16))) float lds_col[kLdsCol];
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // one value per wave

@@ -7,7 +7,8 @@
 Workload: synthetic balanced 10,000 x 10,000, d = 64, fp32, x ~ N(0, 1) (seed 0), y ~ N(0, 1) + 0.5
 (seed 1), uniform weights, squared-Euclidean cost, no normalisation, eps = 0.1 (the reference's
 examples/sinkhorn_benchmark.py --flashsinkhorn setup). A "step" is one iteration of the on-device loop
-(f half-step, g half-step, loop control: four kernel launches), inputs resident in HBM. W untimed iterations, then
+(f half-step, g half-step, loop control: two kernel launches, the partial kernels merging their row groups),
+inputs resident in HBM. W untimed iterations, then
 exactly K timed iterations between two device synchronisations (defaults 100 and 200: the first ~100 iterations
 of a process run ~8 % slower while the GPU's clocks settle).
 

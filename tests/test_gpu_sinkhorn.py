@@ -127,6 +127,46 @@ def test_both_score_paths_match_reference(monkeypatch, log2):
     assert inf_rel(res.f, r64.f) < 1e-5 and inf_rel(res.g, r64.g) < 1e-5, (inf_rel(res.f, r64.f), inf_rel(res.g, r64.g))
 
 
+def _loop_pair(monkeypatch, x, y, **o):
+    """One solve with the merges inside the partial kernels (the default) and one with the merge launches."""
+    out = []
+    for fused in ("1", "0"):
+        monkeypatch.setenv("TRNOPT_HIP_FUSED_MERGE", fused)
+        out.append(sinkhorn(x, y, opts=hip_opts(**o)))
+    return out
+
+
+@pytest.mark.parametrize("case", ["2048-d64", "eps-schedule", "unbalanced-checks", "tall", "wide"])
+def test_merge_in_partial_kernel_is_bit_identical(monkeypatch, case):
+    """The loop's merge inside the partial kernel (last workgroup of each row group, device-scope atomics) and
+    the merge kernel give bit-identical potentials and iteration counts: fixed iterations; an eps schedule
+    (the log2-unit copy remade by the control); an unbalanced solve stopped by its checks; 100,000 x 64
+    points (391 row groups of one or two tiles: workgroups with several segments) and 64 x 100,000 (one
+    row group of the f update split over 256 workgroups, 256 slots)."""
+    if case == "2048-d64":
+        x, y = data.balanced_gaussian()
+        o = dict(eps=0.1, normalize=False, max_iters=100, fixed_iters=True)
+    elif case == "eps-schedule":
+        x, y = data.clouds(n=600, m=500, d=16, seed=4)
+        o = dict(eps=0.05, eps_start=1.0, eps_decay=0.8, max_iters=60, fixed_iters=True)
+    elif case == "unbalanced-checks":
+        x, y = data.clouds(n=700, m=900, d=10, seed=6)
+        o = dict(eps=0.1, rho=(1.0, 50.0), tol=1e-6, max_iters=3000)
+    elif case == "tall":
+        x, y = data.clouds(n=100_000, m=64, d=8, seed=8)
+        o = dict(eps=0.5, max_iters=20, fixed_iters=True)
+    else:
+        x, y = data.clouds(n=64, m=100_000, d=8, seed=9)
+        o = dict(eps=0.5, max_iters=20, fixed_iters=True)
+    print("merge paths", case, flush=True)
+    fused, launched = _loop_pair(monkeypatch, x, y, **o)
+    assert fused.iterations == launched.iterations and fused.converged == launched.converged
+    np.testing.assert_array_equal(fused.f, launched.f)
+    np.testing.assert_array_equal(fused.g, launched.g)
+    if case == "unbalanced-checks":
+        assert fused.converged
+
+
 @pytest.mark.parametrize("iters", [1, 2, 7])
 def test_first_iterations_match_dense_float64(iters):
     """Iterate-by-iterate: the reference's init (g0 = |y|^2) and update order against the dense brute force."""

@@ -17,7 +17,7 @@ STREAM_MAX_CHUNKS, COL_TILES = 4, 256        # streamed variant: nc <= 4; column
 FOLD_COL_TILES = 192                         # ... per 192 tiles with the f16x2 contraction (folded, 16 B each)
 FOLD_MAX = np.float32(2.0 ** 30)             # folded column terms are clamped to +-2^30
 FOLD_SCALES = (2.0 ** 15, 2.0 ** 4, 2.0 ** -7)
-SEG_COST_STREAMED, SEG_COST_STAGED = 4, 2    # cost of a row-group boundary in tiles (sk_kernels.hip make_plan)
+SEG_COST_STREAMED, SEG_COST_STAGED = 6, 2    # cost of a row-group boundary in tiles (sk_kernels.hip make_plan)
 ROWS_PER_GROUP = TILE * RB * WAVES
 EMPTY = -1.0e30
 FIRST = [0, 0, 1]              # fp16x2 (half-steps): (first-cloud piece, second-cloud piece) of the products

@@ -136,6 +136,8 @@ struct PartialArgs {
     const float* w;     // row weights, with meas
     int n_real;         // real rows, with meas
     int* counters;      // with state: one arrival counter, zero on entry and left zero
+    int* group_counters;  // or null: per row group arrival counters (zero on entry, left zero); the partial
+                          // kernel's last workgroup to finish a row group merges it (no merge kernel)
     int ngroups;
     // ... and, in the last merge workgroup of a g update, the loop control (null: none), which also remakes the
     // log2-unit copy of the first cloud (rebake, the packed first cloud; null: never) when eps changes; the f

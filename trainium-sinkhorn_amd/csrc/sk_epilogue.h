@@ -1,7 +1,12 @@
 // Device code of the merge pass: the merge of a row group's partial (max, sum) slots with the half-step
-// epilogue, and the on-device loop control (src/trnopt/sinkhorn.py:346-378), which the merge pass of a g update
-// runs in its last workgroup. (The merge is a launch of its own: run inside the MFMA kernel, its device-scope
-// fences write back and invalidate each XCD's L2 under the tiles the other workgroups are streaming.)
+// epilogue, and the on-device loop control (src/trnopt/sinkhorn.py:346-378), which runs after the last row
+// group of a g update is merged. Two hosts for it: the merge kernel (sk_kernels.hip), a launch of its own after
+// the partial kernel; or, in the on-device loop, the partial kernel itself, whose last workgroup to finish a
+// row group merges it ("coherent" below). The coherent form passes data between workgroups only through
+// device-scope relaxed atomic loads and stores (global_load / global_store with sc1: coherent across the XCDs'
+// L2 caches without writing back or invalidating them; device-scope fences would invalidate each XCD's L2 under
+// the tiles the other workgroups are still streaming), ordered by the workgroup barrier's wait for the
+// workgroup's stores before the arrival counter's atomic add.
 #pragma once
 
 #include "sk_common.h"
@@ -12,6 +17,42 @@ constexpr float kDeltaCap = 50.0f;     // cap of (g_old - g_new) / eps in the ba
 
 __device__ __forceinline__ float ep_ex2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float ep_lg2(float x) { return __builtin_amdgcn_logf(x); }
+
+// Device-scope relaxed atomic accesses (coherent between workgroups on different XCDs within a launch).
+__device__ __forceinline__ float2 coh_load(const float2* p) {
+    const unsigned long long b =
+        __hip_atomic_load(reinterpret_cast<const unsigned long long*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return make_float2(__uint_as_float((unsigned)b), __uint_as_float((unsigned)(b >> 32)));
+}
+__device__ __forceinline__ void coh_store(float2* p, float2 v) {
+    const unsigned long long b =
+        (unsigned long long)__float_as_uint(v.x) | ((unsigned long long)__float_as_uint(v.y) << 32);
+    __hip_atomic_store(reinterpret_cast<unsigned long long*>(p), b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float coh_load(const float* p) {
+    return __uint_as_float(
+        __hip_atomic_load(reinterpret_cast<const unsigned*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+__device__ __forceinline__ void coh_store(float* p, float v) {
+    __hip_atomic_store(reinterpret_cast<unsigned*>(p), __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int coh_load(const int* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void coh_store(int* p, int v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int coh_add(int* p, int v) {
+    return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <bool COH, class T>
+__device__ __forceinline__ T ld(const T* p) {
+    if constexpr (COH) return coh_load(p); else return *p;
+}
+template <bool COH, class T>
+__device__ __forceinline__ void st(T* p, T v) {
+    if constexpr (COH) coh_store(p, v); else *p = v;
+}
 
 // The first cloud's log2-unit copy for score scale c = (2 / eps) log2(e) = sc[0] log2(e), against the second
 // cloud's scale s2: every coordinate x, as the cloud's own pieces hold it (x = (v0 + v1) / s1, exact), becomes
@@ -93,7 +134,9 @@ __device__ inline void set_scalars(sk_state* st, double e, double rho_x, double 
 // With meas, also the group's convergence partials {max_{i<n_real} |new - old|, sum_i |w (exp(min((old -
 // new) / eps, 50)) - 1)|} (sinkhorn.py:360, 368-373), reduced in a fixed order into meas[g].
 // Returns false, storing nothing, when the loop is done (*skip != 0): the flag is loaded with the launch's other
-// scalars and the row's first slots, and tested once they have arrived.
+// scalars and the row's first slots, and tested once they have arrived. COH: the slots were written in this
+// launch by other workgroups, and the results (out, out2, meas) are read back in it (the loop control).
+template <bool COH>
 __device__ inline bool merge_group(const PartialArgs& a, int g) {
     const int i = g * kRowsPerGroup + (int)threadIdx.x;
     const int* skip_p = a.skip != nullptr ? a.skip : &kNoSkip;
@@ -111,7 +154,7 @@ __device__ inline bool merge_group(const PartialArgs& a, int g) {
     const float2* pp = a.part + ic;
     float2 v0[8];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) v0[k] = p0 + k <= p1 ? pp[(size_t)k * a.rows_pad] : make_float2(kEmpty, 0.0f);
+    for (int k = 0; k < 8; ++k) v0[k] = p0 + k <= p1 ? ld<COH>(pp + (size_t)k * a.rows_pad) : make_float2(kEmpty, 0.0f);
     const int skip = *skip_p;
     asm volatile("" ::"s"(sc0), "s"(sc1), "s"(sc2), "s"(sc3), "s"(cb), "s"(cb_s2), "s"(s2), "v"(x2), "v"(o),
                  "v"(old), "v"(wi), "v"(skip));
@@ -130,7 +173,8 @@ __device__ inline bool merge_group(const PartialArgs& a, int g) {
             float2 v[8];
 #pragma unroll
             for (int k = 0; k < 8; ++k)
-                v[k] = q == p0 ? v0[k] : q + k <= p1 ? pp[(size_t)(q + k - p0) * a.rows_pad] : make_float2(kEmpty, 0.0f);
+                v[k] = q == p0 ? v0[k]
+                               : q + k <= p1 ? ld<COH>(pp + (size_t)(q + k - p0) * a.rows_pad) : make_float2(kEmpty, 0.0f);
             float Mn = M;
 #pragma unroll
             for (int k = 0; k < 8; ++k) Mn = fmaxf(Mn, v[k].x);
@@ -152,7 +196,7 @@ __device__ inline bool merge_group(const PartialArgs& a, int g) {
                 const float X2 = x2 * k2;
                 const float val2 = kappa * ((X2 + o * kLog2e) - (M + l2s)) - X2;
                 val = __fdiv_rn(val2, k2);
-                if (i < a.n_store) a.out2[i] = val2;
+                if (i < a.n_store) st<COH>(a.out2 + i, val2);
             } else {
                 // the max enters exactly, in accumulator units (log2-unit slots: M / c, correctly rounded)
                 const float Ma = l2 ? __fdiv_rn(M, c_hs) : M;
@@ -164,9 +208,9 @@ __device__ inline bool merge_group(const PartialArgs& a, int g) {
                 const float delta = fminf((old - val) * sc1, kDeltaCap);
                 derr = (double)fabsf(wi * (expf(delta) - 1.0f));
             }
-            if (i < a.n_store) a.out[i] = val;
+            if (i < a.n_store) st<COH>(a.out + i, val);
         } else if (i < a.n_store) {
-            a.out[i] = M + kLn2 * l2s;
+            st<COH>(a.out + i, M + kLn2 * l2s);
         }
     }
     if (a.meas != nullptr) {
@@ -190,7 +234,7 @@ __device__ inline bool merge_group(const PartialArgs& a, int g) {
                 mx = fmaxf(mx, smax[k]);
                 sm += ssum[k];
             }
-            a.meas[g] = make_float2(mx, (float)sm);
+            st<COH>(a.meas + g, make_float2(mx, (float)sm));
         }
     }
     return true;
@@ -212,11 +256,12 @@ __device__ inline bool needs_control(int it, int stage, int stage_it, const Loop
 // After the g update of one iteration, by one wave: the body of sinkhorn.py:356-378. With (it, stage_it)
 // already advanced by the f update's merge, runs the balanced / unbalanced check at the reference's cadence,
 // advances the stage, sets `done`, and writes the next iteration's eps and {2/eps, 1/eps, eps, kappa}.
+template <bool COH>
 __device__ inline void control_step(sk_state* st, const float2* meas, int nmeas, const LoopCfg& c) {
     float mx = 0.0f;
     double sm = 0.0;
     for (int k = (int)threadIdx.x; k < nmeas; k += 64) {
-        const float2 v = meas[k];
+        const float2 v = ld<COH>(meas + k);
         mx = fmaxf(mx, v.x);
         sm += (double)v.y;
     }
@@ -258,41 +303,51 @@ __device__ inline void control_step(sk_state* st, const float2* meas, int nmeas,
     st->done = done;
 }
 
-// The merge pass: one workgroup per row group. With a loop state (the g update of the on-device loop), the
-// last workgroup to finish runs the loop control; the counter is zero on entry and reset by that workgroup.
-__global__ __launch_bounds__(kRowsPerGroup) void merge_kernel(PartialArgs a) {
-    // The g update's view of the loop counters, read before any workgroup can reach the control.
-    int it = 0, stage = 0, stage_it = 0;
+// The loop's state counters as a g update sees them on entry (before any workgroup can reach the control).
+struct LoopCounters {
+    int it, stage, stage_it;
+};
+__device__ inline LoopCounters loop_counters(const PartialArgs& a) {
+    LoopCounters k = {0, 0, 0};
     if (a.state != nullptr) {
-        it = a.state->it;
-        stage = a.state->stage;
-        stage_it = a.state->stage_it;
+        k.it = a.state->it;
+        k.stage = a.state->stage;
+        k.stage_it = a.state->stage_it;
     }
-    if (!merge_group(a, (int)blockIdx.x)) return;
+    return k;
+}
+
+// After row group g is merged (all threads of the workgroup; the group's results are stored): the f update
+// counts the iteration (once, by group 0's merge); a g update whose counters call for the loop control runs it in
+// the last workgroup to arrive (counter: zero on entry, left zero), which on a new eps also derives the log2-unit
+// potentials again and remakes the first cloud's log2-unit copy for the next f update. COH as in merge_group:
+// the other groups' results were stored in this launch by other workgroups.
+template <bool COH>
+__device__ inline void loop_step(const PartialArgs& a, int g, const LoopCounters& lc, int* counter) {
     if (a.tick != nullptr) {                   // the f update: count the iteration (nobody reads these meanwhile)
-        if (blockIdx.x == 0 && threadIdx.x == 0) {
+        if (g == 0 && threadIdx.x == 0) {
             a.tick->it += 1;
             a.tick->stage_it += 1;
         }
         return;
     }
-    if (a.state == nullptr || !needs_control(it, stage, stage_it, a.cfg)) return;
+    if (a.state == nullptr || !needs_control(lc.it, lc.stage, lc.stage_it, a.cfg)) return;
     __shared__ int s_last;
-    __threadfence();                       // release: this group's outputs and meas[g]
-    __syncthreads();
-    if (threadIdx.x == 0) s_last = atomicAdd(&a.counters[0], 1) == (int)gridDim.x - 1 ? 1 : 0;
+    if constexpr (!COH) __threadfence();   // release: this group's outputs and meas[g]
+    __syncthreads();                       // (COH: every wave's stores have completed)
+    if (threadIdx.x == 0) s_last = (COH ? coh_add(counter, 1) : atomicAdd(counter, 1)) == a.ngroups - 1 ? 1 : 0;
     __syncthreads();
     if (s_last == 0) return;
-    __threadfence();                       // acquire: every group's meas
+    if constexpr (!COH) __threadfence();   // acquire: every group's meas
     // The loop control, by the first wave; thread 0 keeps the scalars of the iteration that ran and hands the next
     // iteration's over through LDS.
     __shared__ float s_sc[4];
     __shared__ float s_sc0_ran;
     __shared__ int s_done;
     if (threadIdx.x == 0) s_sc0_ran = a.state->sc_x[0];
-    if (threadIdx.x < 64) control_step(a.state, a.meas, a.ngroups, a.cfg);
+    if (threadIdx.x < 64) control_step<COH>(a.state, a.meas, a.ngroups, a.cfg);
     if (threadIdx.x == 0) {
-        a.counters[0] = 0;
+        st<COH>(counter, 0);
         s_done = a.state->done;
         for (int k = 0; k < 4; ++k) s_sc[k] = a.state->sc_x[k];
     }
@@ -304,7 +359,7 @@ __global__ __launch_bounds__(kRowsPerGroup) void merge_kernel(PartialArgs a) {
     // update already finds them. (This is the g update: rows y, columns x.)
     const float k2 = 0.5f * (s_sc[0] * kLog2e);
     const int nx = a.s.nt * SK_TILE;
-    for (int i = (int)threadIdx.x; i < a.rows_pad; i += (int)blockDim.x) a.out2[i] = a.out[i] * k2;
+    for (int i = (int)threadIdx.x; i < a.rows_pad; i += (int)blockDim.x) a.out2[i] = ld<COH>(a.out + i) * k2;
     for (int i = (int)threadIdx.x; i < nx; i += (int)blockDim.x) a.u2[i] = a.u[i] * k2;
     const void* second = a.xr;
     const BakeParams b = bake_params(a.rebake, second, s_sc);
@@ -316,16 +371,6 @@ __global__ __launch_bounds__(kRowsPerGroup) void merge_kernel(PartialArgs a) {
     }
     __syncthreads();
     if (threadIdx.x == 0) bake_header(a.rebake, second, b);
-}
-
-// The on-device loop's log2-unit potentials from the accumulator-unit ones, R = (c / 2) fh, c = sc[0] log2(e).
-__global__ __launch_bounds__(256) void derive_log2_kernel(const float* __restrict__ fh, float* __restrict__ rf, int nx,
-                                                          const float* __restrict__ gh, float* __restrict__ rg, int ny,
-                                                          const float* __restrict__ sc) {
-    const float k2 = 0.5f * (sc[0] * kLog2e);
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < nx) rf[i] = fh[i] * k2;
-    if (i < ny) rg[i] = gh[i] * k2;
 }
 
 }  // namespace sk

@@ -11,7 +11,8 @@
 //
 // the score is c a_ij in log2 units. x_i . y_j is accumulated by fp16 MFMAs from a two-piece fp16 split of
 // the power-of-two scaled fp32 coordinates (sk_lse_partial.hip), bit-identical in the f and g updates; the
-// column term is added on the VALU. The running (max, sum) of a row is kept as
+// column term is added after it (by one more MFMA for kp <= 64, on the VALU above). The running (max, sum) of a
+// row is kept as
 //
 //     eps * lse_i = 2 M_i + eps ln(2) log2 S_i,   S_i = sum_j exp2(c (a_ij - M_i)),  M_i = max_j a_ij,
 //
@@ -36,14 +37,16 @@
 // (workgroup, row group) segment writes a partial (M, S) per row into its own slot, and the merge pass merges
 // the slots of every row and applies the kappa / offset epilogue.
 //
-// A half-step is two launches: the partial kernel, then the merge kernel (sk_epilogue.h), one workgroup per
-// row group, which merges the group's slots and applies the epilogue. The on-device loop
-// (src/trnopt/sinkhorn.py:346-378) is four launches per iteration: the f update's merge counts the iteration;
-// in the g update the merge also produces per-group convergence partials, and at a check, a schedule step or
-// the last iteration its last workgroup to finish runs the balanced / unbalanced checks at the reference's
-// cadence, advances the stage, sets `done`, and writes the next iteration's eps and {2/eps, 1/eps, eps,
-// kappa} into the device state (remaking x's log2-unit copy when eps changes). Every loop kernel returns immediately once `done`
-// is set, so the host may enqueue whole batches of iterations.
+// A half-step is two launches: the partial kernel, then the merge kernel, one workgroup per row group, which
+// merges the group's slots and applies the epilogue (sk_epilogue.h). The on-device loop
+// (src/trnopt/sinkhorn.py:346-378) is two launches per iteration, the f and the g update's partial kernels: in
+// them the last workgroup to finish a row group merges it (per-group arrival counters; TRNOPT_HIP_FUSED_MERGE=0
+// launches the merge kernel after each instead). The f update's merge of group 0 counts the iteration; in the g
+// update the merges also produce per-group convergence partials, and at a check, a schedule step or the last
+// iteration the last group's merge runs the balanced / unbalanced checks at the reference's cadence, advances
+// the stage, sets `done`, and writes the next iteration's eps and {2/eps, 1/eps, eps, kappa} into the device
+// state (remaking x's log2-unit copy when eps changes). Every loop kernel returns immediately once `done` is
+// set, so the host may enqueue whole batches of iterations.
 
 #include <hip/hip_runtime.h>
 
@@ -209,6 +212,23 @@ __global__ void fill_mask_kernel(float* __restrict__ mask, int m, int mpad) {
     if (j < mpad) mask[j] = j < m ? 0.0f : kMaskOut;
 }
 
+// The merge pass: one workgroup per row group, then the loop step (sk_epilogue.h).
+__global__ __launch_bounds__(kRowsPerGroup) void merge_kernel(PartialArgs a) {
+    const LoopCounters lc = loop_counters(a);
+    if (!merge_group<false>(a, (int)blockIdx.x)) return;
+    loop_step<false>(a, (int)blockIdx.x, lc, a.counters);
+}
+
+// The on-device loop's log2-unit potentials from the accumulator-unit ones, R = (c / 2) fh, c = sc[0] log2(e).
+__global__ __launch_bounds__(256) void derive_log2_kernel(const float* __restrict__ fh, float* __restrict__ rf, int nx,
+                                                          const float* __restrict__ gh, float* __restrict__ rg, int ny,
+                                                          const float* __restrict__ sc) {
+    const float k2 = 0.5f * (sc[0] * kLog2e);
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < nx) rf[i] = fh[i] * k2;
+    if (i < ny) rg[i] = gh[i] * k2;
+}
+
 // ---------------------------------------------------------------------------------------------------
 // On-device loop control.
 
@@ -255,9 +275,10 @@ struct Plan {
 };
 
 // The cost of a row-group boundary in tiles (Split::alpha): what a second segment adds to a workgroup, its
-// row operands, column-term staging and stores, measured at about 3 us against 0.84 us per 32-column tile
-// (kp 64, 10k x 10k). TRNOPT_HIP_SEG_COST overrides it.
-constexpr int kSegCostStreamed = 4;
+// row operands, column-term staging and stores (about 3 us against 0.7-0.84 us per 32-column tile at kp 64,
+// 10k x 10k), and in the on-device loop the arrival count (and maybe merge) of the first row group. Swept on
+// the 10k x 10k d 64 loop: 6 tiles, 1.4 % faster than 4, 5 and 7 within 0.3 %. TRNOPT_HIP_SEG_COST overrides it.
+constexpr int kSegCostStreamed = 6;
 constexpr int kSegCostStaged = 2;
 
 Plan make_plan(int rows_pad, int m_pad, int kp) {
@@ -323,6 +344,7 @@ struct Pass {
     int n_real;
     float2* part;   // workspace: partial slots
     int* counters;  // with state: one arrival counter, zero on entry and left zero
+    int* group_counters;  // or null: per row group arrival counters; the partial kernel merges (no merge launch)
     sk_state* tick;   // the loop's state whose iteration counters the merge advances (f update), or null
     sk_state* state;  // loop control after the merge (g update of the loop), or null
     LoopCfg cfg;
@@ -355,13 +377,14 @@ hipError_t run_pass(const Pass& ps, const Plan& pl, hipStream_t st) {
     a.w = ps.w;
     a.n_real = ps.n_real;
     a.counters = ps.counters;
+    a.group_counters = ps.group_counters;
     a.ngroups = pl.ngroups;
     a.tick = ps.tick;
     a.state = ps.state;
     a.cfg = ps.cfg;
     a.rebake = ps.rebake;
     hipError_t e = launch_partial(a, pl.nc, st);
-    if (e != hipSuccess) return e;
+    if (e != hipSuccess || ps.group_counters != nullptr) return e;
     hipLaunchKernelGGL(merge_kernel, dim3(pl.ngroups), dim3(kRowsPerGroup), 0, st, a);
     return hipGetLastError();
 }
@@ -405,6 +428,10 @@ int check_cloud(const sk_cloud_f32& c, const char* name) {
 
 // TRNOPT_HIP_LOG2=0 turns the log2-unit copies off (every half-step then scales on the VALU), to compare the paths.
 bool log2_enabled() { return env_int("TRNOPT_HIP_LOG2", 1) != 0; }
+
+// Whether the on-device loop merges each row group inside the partial kernel (default) or launches the merge
+// kernel after it (TRNOPT_HIP_FUSED_MERGE=0, the form of the single half-step entry points).
+bool fused_merge_enabled() { return env_int("TRNOPT_HIP_FUSED_MERGE", 1) != 0; }
 
 void launch_bake(void* first, const void* second, int npad, int nc, const float* sc, hipStream_t st) {
     if (!log2_enabled()) return;
@@ -586,14 +613,16 @@ size_t sk_loop_workspace_bytes(int nx_pad, int ny_pad, int d) {
     const Plan pf = make_plan(nx_pad, ny_pad, kp), pg = make_plan(ny_pad, nx_pad, kp);
     if (!pf.ok || !pg.ok) return 0;
     return std::max(partial_bytes(pf, nx_pad), partial_bytes(pg, ny_pad)) +
-           align_up((size_t)meas_count(ny_pad) * sizeof(float2)) + align_up(sizeof(int)) +
+           align_up((size_t)meas_count(ny_pad) * sizeof(float2)) +
+           align_up((size_t)(1 + std::max(pf.ngroups, pg.ngroups)) * sizeof(int)) +
            align_up((size_t)nx_pad * sizeof(float)) + align_up((size_t)ny_pad * sizeof(float));
 }
 
 namespace {
 // The loop's workspace: partial slots (shared by the f and g updates), the g update's per-group convergence
-// partials, the arrival counter of the g update's merge (zeroed at init; every merge leaves it zero), and the
-// two potentials in log2 units, R = (c / 2) fh, that the iteration carries when the scores come in log2 units.
+// partials, the arrival counters (zeroed at init, left zero by every launch: [0] the loop control's, then one
+// per row group for the merge inside the partial kernel), and the two potentials in log2 units, R = (c / 2) fh,
+// that the iteration carries when the scores come in log2 units.
 struct LoopLayout {
     Plan pf, pg;
     float2* part;
@@ -613,8 +642,8 @@ LoopLayout loop_layout(const sk_loop_f32* L) {
     o.part = (float2*)L->ws;
     o.meas = (float2*)((char*)L->ws + part_sz);
     o.counters = (int*)((char*)o.meas + align_up((size_t)meas_count(L->y.npad) * sizeof(float2)));
-    o.ncounters = 1;
-    o.rf = (float*)((char*)o.counters + align_up(sizeof(int)));
+    o.ncounters = 1 + std::max(o.pf.ngroups, o.pg.ngroups);
+    o.rf = (float*)((char*)o.counters + align_up((size_t)o.ncounters * sizeof(int)));
     o.rg = (float*)((char*)o.rf + align_up((size_t)L->x.npad * sizeof(float)));
     return o;
 }
@@ -690,6 +719,7 @@ int sk_loop_run_f32(const sk_loop_f32* L, int iters, void* stream) {
     f.n_store = L->x.npad;
     f.tick = st;
     f.part = part;
+    f.group_counters = fused_merge_enabled() ? lo.counters + 1 : nullptr;
 
     Pass g = {};
     g.xr = L->y.pk;
@@ -718,6 +748,7 @@ int sk_loop_run_f32(const sk_loop_f32* L, int iters, void* stream) {
     g.state = st;
     g.cfg = cfg;
     g.rebake = log2_enabled() ? (char*)const_cast<void*>(L->x.pk) : nullptr;
+    g.group_counters = f.group_counters;
 
     for (int k = 0; k < iters; ++k) {
         hipError_t e = run_pass(f, pf, hs);

@@ -57,6 +57,7 @@
 #include <utility>
 
 #include "sk_common.h"
+#include "sk_epilogue.h"
 
 #ifndef SK_PARTIAL_LARGE
 #define SK_PARTIAL_LARGE 0
@@ -216,8 +217,14 @@ __device__ __forceinline__ void store_rows(const PartialArgs& a, const float (&M
         const float Mn = fmaxf(M[b], Mo);
         const float Sn = L2 ? S[b] * ex2(M[b] - Mn) + So * ex2(Mo - Mn)
                             : S[b] * ex2(c * (M[b] - Mn)) + So * ex2(c * (Mo - Mn));
-        if (lane < 32 && rb0 + b < a.nrb)
-            a.part[(size_t)slot * a.rows_pad + (size_t)(rb0 + b) * 32 + lane] = make_float2(L2 ? Mn : Mn * inv_sigma, Sn);
+        if (lane < 32 && rb0 + b < a.nrb) {
+            float2* dst = a.part + (size_t)slot * a.rows_pad + (size_t)(rb0 + b) * 32 + lane;
+            const float2 v = make_float2(L2 ? Mn : Mn * inv_sigma, Sn);
+            if (a.group_counters != nullptr)
+                coh_store(dst, v);           // read back in this launch by the group's last workgroup
+            else
+                *dst = v;
+        }
     }
 }
 
@@ -539,12 +546,34 @@ struct Streamed {
     }
 };
 
+// After a work segment of row group g (every wave has stored its rows of the slot, as device-scope atomic
+// stores): count the workgroup's arrival; the last of the group's workgroups merges the group's slots and runs
+// the loop step (sk_epilogue.h), so that no merge launch follows. Before the count every wave waits for its
+// stores to complete (they are then visible device-wide: sc1 stores are write-through), and the barrier makes
+// thread 0's atomic add follow all of them; the last arrival reads the slots with device-scope loads, which
+// miss the XCD's L2. No fence: a device-scope one would write back and invalidate the L2 under the operand
+// tiles the other workgroups of the XCD are streaming.
+__device__ inline void arrive(const PartialArgs& a, int g, const LoopCounters& lc) {
+    __shared__ int s_last;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int nslots = last_wg(g, a.s) - first_wg(g, a.s) + 1;
+        s_last = coh_add(a.group_counters + g, 1) == nslots - 1 ? 1 : 0;
+    }
+    __syncthreads();
+    if (s_last == 0) return;
+    if (threadIdx.x == 0) coh_store(a.group_counters + g, 0);
+    if (merge_group<true>(a, g)) loop_step<true>(a, g, lc, a.counters);
+    __syncthreads();   // the next segment's column staging reuses LDS the merge does not touch; keep waves together
+}
+
 // The work segments of workgroup p: a_ij = x_i . y_j + cs (alpha cu_j + beta v_j) in the kernel's units, scores
 // exp2(c (a - M)) (with L2: exp2(a - M), a already in log2 units).
 template <int NC, int ROLE, int CT, bool L2>
 __device__ __forceinline__ void segments(const PartialArgs& a, int p, int wv, const float* cu, float alpha, float beta,
                                          float cs, float c, float inv_sigma, typename Contract<CT>::T* lds_y,
-                                         float* lds_col) {
+                                         float* lds_col, const LoopCounters& lc) {
     // The segment bounds are 32-bit integer arithmetic (the divisions expand to vector code); their results are
     // the same in every lane, and readfirstlane hands them to the scalar unit, so the tile loop's counters and
     // operand addresses stay in scalar registers.
@@ -561,6 +590,7 @@ __device__ __forceinline__ void segments(const PartialArgs& a, int p, int wv, co
             Streamed<NC, ROLE, CT, L2>::run(a, rb0, tb, te, slot, cu, alpha, beta, cs, c, inv_sigma, lds_col);
         else
             Staged<NC, ROLE, CT, L2>::run(a, rb0, tb, te, slot, cu, alpha, beta, cs, c, inv_sigma, lds_y, lds_col);
+        if (a.group_counters != nullptr) arrive(a, g, lc);
         u += te - tb;
     }
 }
@@ -577,6 +607,8 @@ void lse_partial_kernel(PartialArgs a) {
     const float sx = packed_scale(a.xr), sy = packed_scale(a.yc);   // 1 for kBF16x3
     const float cb = h1[2], cb_s2 = h1[3];
     const int skip = *skip_p;
+    // the loop's counters as this launch starts (the fused merge's loop step), read with the scalars
+    const LoopCounters lc = a.group_counters != nullptr ? loop_counters(a) : LoopCounters{0, 0, 0};
     asm volatile("" ::"s"(sc0), "s"(sc2), "s"(sx), "s"(sy), "s"(cb), "s"(cb_s2), "v"(skip));
     if (skip != 0) return;
     constexpr bool kStream = NC <= kStreamMaxChunks;
@@ -608,14 +640,14 @@ void lse_partial_kernel(PartialArgs a) {
     if constexpr (CT == kF16x2) {
         if (a.mode == kHalfStep && cb != 0.0f && cb == c && cb_s2 == (ROLE == 0 ? sy : sx)) {
             if (a.u2 != nullptr)
-                segments<NC, ROLE, CT, true>(a, p, wv, a.u2, 1.0f, kLog2e, 1.0f, 1.0f, 1.0f, lds_y, lds_col);
+                segments<NC, ROLE, CT, true>(a, p, wv, a.u2, 1.0f, kLog2e, 1.0f, 1.0f, 1.0f, lds_y, lds_col, lc);
             else
-                segments<NC, ROLE, CT, true>(a, p, wv, a.u, alpha, beta, c, 1.0f, 1.0f, lds_y, lds_col);
+                segments<NC, ROLE, CT, true>(a, p, wv, a.u, alpha, beta, c, 1.0f, 1.0f, lds_y, lds_col, lc);
             return;
         }
     }
     const float sigma = sx * sy, inv_sigma = (1.0f / sx) * (1.0f / sy);
-    segments<NC, ROLE, CT, false>(a, p, wv, a.u, alpha, beta, sigma, c * inv_sigma, inv_sigma, lds_y, lds_col);
+    segments<NC, ROLE, CT, false>(a, p, wv, a.u, alpha, beta, sigma, c * inv_sigma, inv_sigma, lds_y, lds_col, lc);
 }
 
 template <int NC>

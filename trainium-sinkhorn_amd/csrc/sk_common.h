@@ -110,6 +110,12 @@ struct LoopCfg {
     int max_iters, check_every, stage_max_iters, fixed_iters, balanced;
 };
 
+// Work-item and workgroup ids straight from the hardware registers. threadIdx / blockIdx / blockDim call
+// device-library functions, which the compiler stops inlining into kernels as large as the partial kernel;
+// every such call makes the kernel spill its scalars around it.
+__device__ __forceinline__ int tid_x() { return (int)__builtin_amdgcn_workitem_id_x(); }
+__device__ __forceinline__ int wg_x() { return (int)__builtin_amdgcn_workgroup_id_x(); }
+
 struct PartialArgs {
     const void* xr;     // packed rows (header, then two fp16 pieces per scaled coordinate)
     const void* yc;     // packed columns

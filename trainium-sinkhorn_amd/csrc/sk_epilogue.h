@@ -125,7 +125,7 @@ __device__ inline void set_scalars(sk_state* st, double e, double rho_x, double 
     st->sc_y[3] = (float)ky;
 }
 
-// Merge the slots of row i = 256 g + threadIdx.x (one row per thread of the workgroup) and apply the epilogue:
+// Merge the slots of row i = 256 g + t (thread t of the workgroup, one row per thread) and apply the epilogue:
 //     lse = (2 / eps) M + ln S  (half-step, accumulator units) or M + ln S  (plain row-LSE)
 // When the partial kernel took its scores in log2 units (log2_ready, tested on the same header words), the
 // slots hold M in log2 units: they merge without c, and M / c (correctly rounded, so that no constant factor
@@ -138,7 +138,7 @@ __device__ inline void set_scalars(sk_state* st, double e, double rho_x, double 
 // launch by other workgroups, and the results (out, out2, meas) are read back in it (the loop control).
 template <bool COH>
 __device__ inline bool merge_group(const PartialArgs& a, int g) {
-    const int i = g * kRowsPerGroup + (int)threadIdx.x;
+    const int i = g * kRowsPerGroup + tid_x();
     const int* skip_p = a.skip != nullptr ? a.skip : &kNoSkip;
     const float sc0 = a.sc[0], sc1 = a.sc[1], sc2 = a.sc[2], sc3 = a.sc[3];   // valid in both modes
     const float* h1 = reinterpret_cast<const float*>(a.rows_role == 0 ? a.xr : a.yc);   // the first cloud
@@ -221,13 +221,13 @@ __device__ inline bool merge_group(const PartialArgs& a, int g) {
         }
         __shared__ float smax[kRowsPerGroup / 64];
         __shared__ double ssum[kRowsPerGroup / 64];
-        const int wv = (int)threadIdx.x >> 6;
-        if ((threadIdx.x & 63) == 0) {
+        const int wv = tid_x() >> 6;
+        if ((tid_x() & 63) == 0) {
             smax[wv] = dmax;
             ssum[wv] = derr;
         }
         __syncthreads();
-        if (threadIdx.x == 0) {
+        if (tid_x() == 0) {
             float mx = smax[0];
             double sm = ssum[0];
             for (int k = 1; k < kRowsPerGroup / 64; ++k) {
@@ -260,7 +260,7 @@ template <bool COH>
 __device__ inline void control_step(sk_state* st, const float2* meas, int nmeas, const LoopCfg& c) {
     float mx = 0.0f;
     double sm = 0.0;
-    for (int k = (int)threadIdx.x; k < nmeas; k += 64) {
+    for (int k = tid_x(); k < nmeas; k += 64) {
         const float2 v = ld<COH>(meas + k);
         mx = fmaxf(mx, v.x);
         sm += (double)v.y;
@@ -270,7 +270,7 @@ __device__ inline void control_step(sk_state* st, const float2* meas, int nmeas,
         mx = fmaxf(mx, __shfl_xor(mx, o));
         sm += __shfl_xor(sm, o);
     }
-    if (threadIdx.x != 0) return;
+    if (tid_x() != 0) return;
     const float inv_eps = st->sc_x[1];          // 1/eps of the iteration that just ran
     const int it = st->it;
     int stage = st->stage;
@@ -325,7 +325,7 @@ __device__ inline LoopCounters loop_counters(const PartialArgs& a) {
 template <bool COH>
 __device__ inline void loop_step(const PartialArgs& a, int g, const LoopCounters& lc, int* counter) {
     if (a.tick != nullptr) {                   // the f update: count the iteration (nobody reads these meanwhile)
-        if (g == 0 && threadIdx.x == 0) {
+        if (g == 0 && tid_x() == 0) {
             a.tick->it += 1;
             a.tick->stage_it += 1;
         }
@@ -335,7 +335,7 @@ __device__ inline void loop_step(const PartialArgs& a, int g, const LoopCounters
     __shared__ int s_last;
     if constexpr (!COH) __threadfence();   // release: this group's outputs and meas[g]
     __syncthreads();                       // (COH: every wave's stores have completed)
-    if (threadIdx.x == 0) s_last = (COH ? coh_add(counter, 1) : atomicAdd(counter, 1)) == a.ngroups - 1 ? 1 : 0;
+    if (tid_x() == 0) s_last = (COH ? coh_add(counter, 1) : atomicAdd(counter, 1)) == a.ngroups - 1 ? 1 : 0;
     __syncthreads();
     if (s_last == 0) return;
     if constexpr (!COH) __threadfence();   // acquire: every group's meas
@@ -344,9 +344,9 @@ __device__ inline void loop_step(const PartialArgs& a, int g, const LoopCounters
     __shared__ float s_sc[4];
     __shared__ float s_sc0_ran;
     __shared__ int s_done;
-    if (threadIdx.x == 0) s_sc0_ran = a.state->sc_x[0];
-    if (threadIdx.x < 64) control_step<COH>(a.state, a.meas, a.ngroups, a.cfg);
-    if (threadIdx.x == 0) {
+    if (tid_x() == 0) s_sc0_ran = a.state->sc_x[0];
+    if (tid_x() < 64) control_step<COH>(a.state, a.meas, a.ngroups, a.cfg);
+    if (tid_x() == 0) {
         st<COH>(counter, 0);
         s_done = a.state->done;
         for (int k = 0; k < 4; ++k) s_sc[k] = a.state->sc_x[k];
@@ -359,18 +359,18 @@ __device__ inline void loop_step(const PartialArgs& a, int g, const LoopCounters
     // update already finds them. (This is the g update: rows y, columns x.)
     const float k2 = 0.5f * (s_sc[0] * kLog2e);
     const int nx = a.s.nt * SK_TILE;
-    for (int i = (int)threadIdx.x; i < a.rows_pad; i += (int)blockDim.x) a.out2[i] = ld<COH>(a.out + i) * k2;
-    for (int i = (int)threadIdx.x; i < nx; i += (int)blockDim.x) a.u2[i] = a.u[i] * k2;
+    for (int i = tid_x(); i < a.rows_pad; i += kRowsPerGroup) a.out2[i] = ld<COH>(a.out + i) * k2;
+    for (int i = tid_x(); i < nx; i += kRowsPerGroup) a.u2[i] = a.u[i] * k2;
     const void* second = a.xr;
     const BakeParams b = bake_params(a.rebake, second, s_sc);
     const float* h = reinterpret_cast<const float*>(a.rebake);
     if (b.valid ? h[2] == b.c && h[3] == packed_scale(second) : h[2] == 0.0f) return;
     if (b.valid) {
         const long long total = (long long)(nx / SK_TILE) * a.nc * 64;
-        for (long long idx = threadIdx.x; idx < total; idx += blockDim.x) bake_unit(a.rebake, idx, nx, a.nc, b);
+        for (long long idx = tid_x(); idx < total; idx += kRowsPerGroup) bake_unit(a.rebake, idx, nx, a.nc, b);
     }
     __syncthreads();
-    if (threadIdx.x == 0) bake_header(a.rebake, second, b);
+    if (tid_x() == 0) bake_header(a.rebake, second, b);
 }
 
 }  // namespace sk

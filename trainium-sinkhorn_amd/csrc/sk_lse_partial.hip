@@ -243,7 +243,7 @@ struct Staged {
     __device__ __forceinline__ static void run(const PartialArgs& a, int rb0, int tb, int te, int slot, const float* cu,
                                                float alpha, float beta, float cs, float c, float inv_sigma,
                                                T* lds_y, float* lds_col) {
-        const int tid = threadIdx.x;
+        const int tid = tid_x();
         const int lane = tid & 63;
         const int h = lane >> 5;
         // With L2 the first cloud of the pair (the rows for ROLE 0, the columns for ROLE 1) is read from its
@@ -395,7 +395,7 @@ struct Streamed {
     __device__ __forceinline__ static void run(const PartialArgs& a, int rb0, int tb, int te, int slot, const float* cu,
                                                float alpha, float beta, float cs, float c, float inv_sigma,
                                                float* lds_col) {
-        const int tid = threadIdx.x;
+        const int tid = tid_x();
         const int lane = tid & 63;
         const int h = lane >> 5;
         // With L2 the first cloud of the pair (the rows for ROLE 0, the columns for ROLE 1) is read from its
@@ -546,6 +546,14 @@ struct Streamed {
     }
 };
 
+// The kernel's argument block, read where it is used. The merge's and the loop step's fields (epilogue
+// vectors, loop configuration) are read through this reference, so that the compiler loads them there and not
+// at the kernel's entry, where they would crowd the scalar registers the tile loop needs (spilled and reloaded
+// one dependent load at a time).
+__device__ __forceinline__ const PartialArgs& kernel_args() {
+    return *(const PartialArgs*)__builtin_amdgcn_kernarg_segment_ptr();   // address-space conversion
+}
+
 // After a work segment of row group g (every wave has stored its rows of the slot, as device-scope atomic
 // stores): count the workgroup's arrival; the last of the group's workgroups merges the group's slots and runs
 // the loop step (sk_epilogue.h), so that no merge launch follows. Before the count every wave waits for its
@@ -553,18 +561,61 @@ struct Streamed {
 // thread 0's atomic add follow all of them; the last arrival reads the slots with device-scope loads, which
 // miss the XCD's L2. No fence: a device-scope one would write back and invalidate the L2 under the operand
 // tiles the other workgroups of the XCD are streaming.
-__device__ inline void arrive(const PartialArgs& a, int g, const LoopCounters& lc) {
+__device__ inline void arrive(const PartialArgs& a, int g) {
     __shared__ int s_last;
+    // The merge's own argument fields (epilogue vectors, loop state and configuration), requested here in one
+    // batch through a pointer the compiler cannot follow out of this function, so that they arrive while the
+    // stores and the counter make their round trips; the fields the segments use come from `a`, already held.
+    const PartialArgs* kp = &kernel_args();
+    asm volatile("" : "+s"(kp));
+    PartialArgs m = a;
+    m.xsq = kp->xsq;
+    m.off = kp->off;
+    m.out = kp->out;
+    m.out2 = kp->out2;
+    m.n_store = kp->n_store;
+    m.meas = kp->meas;
+    m.w = kp->w;
+    m.n_real = kp->n_real;
+    m.counters = kp->counters;
+    m.ngroups = kp->ngroups;
+    m.tick = kp->tick;
+    m.state = kp->state;
+    m.rebake = kp->rebake;
+    m.rows_role = kp->rows_role;
+    m.contraction = kp->contraction;
+    m.cfg.n_sched = kp->cfg.n_sched;
+    m.cfg.n_stages = kp->cfg.n_stages;
+    m.cfg.max_iters = kp->cfg.max_iters;
+    m.cfg.check_every = kp->cfg.check_every;
+    m.cfg.fixed_iters = kp->cfg.fixed_iters;
+    asm volatile("" ::"s"(m.xsq), "s"(m.off), "s"(m.out), "s"(m.out2), "s"(m.n_store), "s"(m.meas), "s"(m.w),
+                 "s"(m.n_real), "s"(m.counters), "s"(m.ngroups), "s"(m.tick), "s"(m.state), "s"(m.rebake),
+                 "s"(m.rows_role), "s"(m.contraction), "s"(m.cfg.n_sched), "s"(m.cfg.n_stages),
+                 "s"(m.cfg.max_iters), "s"(m.cfg.check_every), "s"(m.cfg.fixed_iters));
+    // (the rest of the loop configuration, read only by the control itself, comes from the argument block)
+    m.cfg.sched = kp->cfg.sched;
+    m.cfg.stages = kp->cfg.stages;
+    m.cfg.eps = kp->cfg.eps;
+    m.cfg.rho_x = kp->cfg.rho_x;
+    m.cfg.rho_y = kp->cfg.rho_y;
+    m.cfg.tol = kp->cfg.tol;
+    m.cfg.stage_tol = kp->cfg.stage_tol;
+    m.cfg.stage_max_iters = kp->cfg.stage_max_iters;
+    m.cfg.balanced = kp->cfg.balanced;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (threadIdx.x == 0) {
+    if (tid_x() == 0) {
         const int nslots = last_wg(g, a.s) - first_wg(g, a.s) + 1;
         s_last = coh_add(a.group_counters + g, 1) == nslots - 1 ? 1 : 0;
     }
     __syncthreads();
     if (s_last == 0) return;
-    if (threadIdx.x == 0) coh_store(a.group_counters + g, 0);
-    if (merge_group<true>(a, g)) loop_step<true>(a, g, lc, a.counters);
+    if (tid_x() == 0) coh_store(a.group_counters + g, 0);
+    // The loop's counters as this launch found them: the control runs only after every group is merged, this
+    // one included, so nothing has changed them yet.
+    const LoopCounters lc = loop_counters(m);
+    if (merge_group<true>(m, g)) loop_step<true>(m, g, lc, m.counters);
     __syncthreads();   // the next segment's column staging reuses LDS the merge does not touch; keep waves together
 }
 
@@ -573,7 +624,7 @@ __device__ inline void arrive(const PartialArgs& a, int g, const LoopCounters& l
 template <int NC, int ROLE, int CT, bool L2>
 __device__ __forceinline__ void segments(const PartialArgs& a, int p, int wv, const float* cu, float alpha, float beta,
                                          float cs, float c, float inv_sigma, typename Contract<CT>::T* lds_y,
-                                         float* lds_col, const LoopCounters& lc) {
+                                         float* lds_col) {
     // The segment bounds are 32-bit integer arithmetic (the divisions expand to vector code); their results are
     // the same in every lane, and readfirstlane hands them to the scalar unit, so the tile loop's counters and
     // operand addresses stay in scalar registers.
@@ -590,10 +641,12 @@ __device__ __forceinline__ void segments(const PartialArgs& a, int p, int wv, co
             Streamed<NC, ROLE, CT, L2>::run(a, rb0, tb, te, slot, cu, alpha, beta, cs, c, inv_sigma, lds_col);
         else
             Staged<NC, ROLE, CT, L2>::run(a, rb0, tb, te, slot, cu, alpha, beta, cs, c, inv_sigma, lds_y, lds_col);
-        if (a.group_counters != nullptr) arrive(a, g, lc);
+        if (a.group_counters != nullptr) arrive(a, g);
         u += te - tb;
     }
 }
+
+static_assert(kBlock == kRowsPerGroup, "the merge inside the partial kernel takes one row per thread");
 
 template <int NC, int ROLE, int CT>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(1, 1)))
@@ -607,8 +660,10 @@ void lse_partial_kernel(PartialArgs a) {
     const float sx = packed_scale(a.xr), sy = packed_scale(a.yc);   // 1 for kBF16x3
     const float cb = h1[2], cb_s2 = h1[3];
     const int skip = *skip_p;
-    // the loop's counters as this launch starts (the fused merge's loop step), read with the scalars
-    const LoopCounters lc = a.group_counters != nullptr ? loop_counters(a) : LoopCounters{0, 0, 0};
+    // The argument fields the segments need, requested with the first batch of argument loads rather than
+    // after the scalars have arrived.
+    asm volatile("" ::"s"(a.nrb), "s"(a.rows_pad), "s"(a.mode), "s"(a.s.nt), "s"(a.s.P), "s"(a.s.alpha),
+                 "s"(a.s.ftot), "s"(a.s.q), "s"(a.s.r), "s"(a.group_counters));
     asm volatile("" ::"s"(sc0), "s"(sc2), "s"(sx), "s"(sy), "s"(cb), "s"(cb_s2), "v"(skip));
     if (skip != 0) return;
     constexpr bool kStream = NC <= kStreamMaxChunks;
@@ -616,8 +671,8 @@ void lse_partial_kernel(PartialArgs a) {
     constexpr int kLdsCol = kStream ? col_floats(CT == kF16x2) : 3 * 32;
     __shared__ typename Contract<CT>::T lds_y[kLdsY];
     __shared__ __attribute__((aligned(16))) float lds_col[kLdsCol];
-    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // one value per wave
-    const int p = xcd_contiguous(blockIdx.x, a.s.P);
+    const int wv = __builtin_amdgcn_readfirstlane(tid_x() >> 6);   // one value per wave
+    const int p = xcd_contiguous(wg_x(), a.s.P);
 
     // a_ij = x_i . y_j + alpha u_j + beta v_j in accumulator units, scores exp2(c (a - M)):
     // half-step: a = x . y + (gh + eps log b) / 2, c = (2 / eps) log2(e); plain row-LSE: a = xa . ya + mask,
@@ -640,14 +695,14 @@ void lse_partial_kernel(PartialArgs a) {
     if constexpr (CT == kF16x2) {
         if (a.mode == kHalfStep && cb != 0.0f && cb == c && cb_s2 == (ROLE == 0 ? sy : sx)) {
             if (a.u2 != nullptr)
-                segments<NC, ROLE, CT, true>(a, p, wv, a.u2, 1.0f, kLog2e, 1.0f, 1.0f, 1.0f, lds_y, lds_col, lc);
+                segments<NC, ROLE, CT, true>(a, p, wv, a.u2, 1.0f, kLog2e, 1.0f, 1.0f, 1.0f, lds_y, lds_col);
             else
-                segments<NC, ROLE, CT, true>(a, p, wv, a.u, alpha, beta, c, 1.0f, 1.0f, lds_y, lds_col, lc);
+                segments<NC, ROLE, CT, true>(a, p, wv, a.u, alpha, beta, c, 1.0f, 1.0f, lds_y, lds_col);
             return;
         }
     }
     const float sigma = sx * sy, inv_sigma = (1.0f / sx) * (1.0f / sy);
-    segments<NC, ROLE, CT, false>(a, p, wv, a.u, alpha, beta, sigma, c * inv_sigma, inv_sigma, lds_y, lds_col, lc);
+    segments<NC, ROLE, CT, false>(a, p, wv, a.u, alpha, beta, sigma, c * inv_sigma, inv_sigma, lds_y, lds_col);
 }
 
 template <int NC>

@@ -319,7 +319,8 @@ size_t partial_bytes(const Plan& pl, int rows_pad) { return align_up((size_t)pl.
 // Row groups of rows_pad rows: the number of convergence partials.
 int meas_count(int rows_pad) { return (rows_pad + kRowsPerGroup - 1) / kRowsPerGroup; }
 
-// One LSE pass over packed rows and columns: the partial kernel writes the slots, the merge kernel merges them.
+// One LSE pass over packed rows and columns: the partial kernel writes the slots, the merge kernel merges them
+// (with group_counters the partial kernel's last workgroup of each row group does, and no merge kernel follows).
 struct Pass {
     const void* xr;
     int rows_pad;

@@ -136,13 +136,13 @@ def _loop_pair(monkeypatch, x, y, **o):
     return out
 
 
-@pytest.mark.parametrize("case", ["2048-d64", "eps-schedule", "unbalanced-checks", "tall", "wide"])
+@pytest.mark.parametrize("case", ["2048-d64", "eps-schedule", "unbalanced-checks", "tall", "wide", "staged-d100"])
 def test_merge_in_partial_kernel_is_bit_identical(monkeypatch, case):
     """The loop's merge inside the partial kernel (last workgroup of each row group, device-scope atomics) and
     the merge kernel give bit-identical potentials and iteration counts: fixed iterations; an eps schedule
     (the log2-unit copy remade by the control); an unbalanced solve stopped by its checks; 100,000 x 64
-    points (391 row groups of one or two tiles: workgroups with several segments) and 64 x 100,000 (one
-    row group of the f update split over 256 workgroups, 256 slots)."""
+    points (391 row groups of one or two tiles: workgroups with several segments), 64 x 100,000 (one
+    row group of the f update split over 256 workgroups, 256 slots), and d 100 (the staged kernel)."""
     if case == "2048-d64":
         x, y = data.balanced_gaussian()
         o = dict(eps=0.1, normalize=False, max_iters=100, fixed_iters=True)
@@ -155,9 +155,12 @@ def test_merge_in_partial_kernel_is_bit_identical(monkeypatch, case):
     elif case == "tall":
         x, y = data.clouds(n=100_000, m=64, d=8, seed=8)
         o = dict(eps=0.5, max_iters=20, fixed_iters=True)
-    else:
+    elif case == "wide":
         x, y = data.clouds(n=64, m=100_000, d=8, seed=9)
         o = dict(eps=0.5, max_iters=20, fixed_iters=True)
+    else:
+        x, y = data.clouds(n=3000, m=2500, d=100, seed=10)
+        o = dict(eps=0.5, max_iters=30, fixed_iters=True)
     print("merge paths", case, flush=True)
     fused, launched = _loop_pair(monkeypatch, x, y, **o)
     assert fused.iterations == launched.iterations and fused.converged == launched.converged

@@ -132,7 +132,8 @@ __device__ inline void set_scalars(sk_state* st, double e, double rho_x, double 
 // enters the potentials) gives the accumulator units.
 //     fh  = kappa ((|x|^2 + eps off) - eps lse) - |x|^2
 // With meas, also the group's convergence partials {max_{i<n_real} |new - old|, sum_i |w (exp(min((old -
-// new) / eps, 50)) - 1)|} (sinkhorn.py:360, 368-373), reduced in a fixed order into meas[g].
+// new) / eps, 50)) - 1)|} (sinkhorn.py:360, 368-373), reduced in a fixed order into meas[g] (in the on-device
+// loop only when the iteration's control will run: the callers drop meas otherwise).
 // Returns false, storing nothing, when the loop is done (*skip != 0): the flag is loaded with the launch's other
 // scalars and the row's first slots, and tested once they have arrived. COH: the slots were written in this
 // launch by other workgroups, and the results (out, out2, meas) are read back in it (the loop control).

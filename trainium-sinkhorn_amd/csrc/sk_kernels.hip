@@ -215,6 +215,8 @@ __global__ void fill_mask_kernel(float* __restrict__ mask, int m, int mpad) {
 // The merge pass: one workgroup per row group, then the loop step (sk_epilogue.h).
 __global__ __launch_bounds__(kRowsPerGroup) void merge_kernel(PartialArgs a) {
     const LoopCounters lc = loop_counters(a);
+    // The loop's convergence partials are read only by a control that checks: skip them otherwise.
+    if (a.state != nullptr && !needs_control(lc.it, lc.stage, lc.stage_it, a.cfg)) a.meas = nullptr;
     if (!merge_group<false>(a, (int)blockIdx.x)) return;
     loop_step<false>(a, (int)blockIdx.x, lc, a.counters);
 }

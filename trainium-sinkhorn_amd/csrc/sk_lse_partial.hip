@@ -615,6 +615,7 @@ __device__ inline void arrive(const PartialArgs& a, int g) {
     // The loop's counters as this launch found them: the control runs only after every group is merged, this
     // one included, so nothing has changed them yet.
     const LoopCounters lc = loop_counters(m);
+    if (m.state != nullptr && !needs_control(lc.it, lc.stage, lc.stage_it, m.cfg)) m.meas = nullptr;   // no check
     if (merge_group<true>(m, g)) loop_step<true>(m, g, lc, m.counters);
     __syncthreads();   // the next segment's column staging reuses LDS the merge does not touch; keep waves together
 }

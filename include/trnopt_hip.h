@@ -182,8 +182,9 @@ size_t sk_loop_workspace_bytes(int nx_pad, int ny_pad, int d);
 /* Write the initial state (it = 0, first eps and its scalars); make x's log2-unit copy for that eps
  * (sk_bake_log2_f32) and the loop's log2-unit potentials (c / 2) fh, (c / 2) gh in ws from fh and gh. */
 int sk_loop_init_f32(const sk_loop_f32* L, void* stream);
-/* Enqueue `iters` iterations (f update, g update with the loop control in its merge: two launches each, the
- * partial kernels merging their own row groups);
+/* Enqueue `iters` iterations (f update, g update with the loop control in its merge: a partial-kernel launch
+ * each, which merges its own row groups from 40 row groups (10k rows) up, and a merge-kernel launch after it
+ * below that);
  * iterations after `done` do nothing. ws (sk_loop_workspace_bytes) must be 256-byte aligned. */
 int sk_loop_run_f32(const sk_loop_f32* L, int iters, void* stream);
 

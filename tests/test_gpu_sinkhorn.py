@@ -127,19 +127,23 @@ def test_both_score_paths_match_reference(monkeypatch, log2):
     assert inf_rel(res.f, r64.f) < 1e-5 and inf_rel(res.g, r64.g) < 1e-5, (inf_rel(res.f, r64.f), inf_rel(res.g, r64.g))
 
 
-def _loop_pair(monkeypatch, x, y, **o):
-    """One solve with the merges inside the partial kernels (the default) and one with the merge launches."""
+def _loop_forms(monkeypatch, x, y, **o):
+    """One solve with the merges inside the partial kernels, one with the merge launches, and one with the
+    per-pass default (in-kernel from 40 row groups: the tall and wide cases mix the two forms)."""
     out = []
-    for fused in ("1", "0"):
-        monkeypatch.setenv("TRNOPT_HIP_FUSED_MERGE", fused)
+    for fused in ("1", "0", None):
+        if fused is None:
+            monkeypatch.delenv("TRNOPT_HIP_FUSED_MERGE", raising=False)
+        else:
+            monkeypatch.setenv("TRNOPT_HIP_FUSED_MERGE", fused)
         out.append(sinkhorn(x, y, opts=hip_opts(**o)))
     return out
 
 
 @pytest.mark.parametrize("case", ["2048-d64", "eps-schedule", "unbalanced-checks", "tall", "wide", "staged-d100"])
 def test_merge_in_partial_kernel_is_bit_identical(monkeypatch, case):
-    """The loop's merge inside the partial kernel (last workgroup of each row group, device-scope atomics) and
-    the merge kernel give bit-identical potentials and iteration counts: fixed iterations; an eps schedule
+    """The loop's merge inside the partial kernel (last workgroup of each row group, device-scope atomics), the
+    merge kernel, and the default choice per pass give bit-identical potentials and iteration counts: fixed iterations; an eps schedule
     (the log2-unit copy remade by the control); an unbalanced solve stopped by its checks; 100,000 x 64
     points (391 row groups of one or two tiles: workgroups with several segments), 64 x 100,000 (one
     row group of the f update split over 256 workgroups, 256 slots), and d 100 (the staged kernel)."""
@@ -162,10 +166,11 @@ def test_merge_in_partial_kernel_is_bit_identical(monkeypatch, case):
         x, y = data.clouds(n=3000, m=2500, d=100, seed=10)
         o = dict(eps=0.5, max_iters=30, fixed_iters=True)
     print("merge paths", case, flush=True)
-    fused, launched = _loop_pair(monkeypatch, x, y, **o)
-    assert fused.iterations == launched.iterations and fused.converged == launched.converged
-    np.testing.assert_array_equal(fused.f, launched.f)
-    np.testing.assert_array_equal(fused.g, launched.g)
+    fused, launched, auto = _loop_forms(monkeypatch, x, y, **o)
+    for r in (launched, auto):
+        assert fused.iterations == r.iterations and fused.converged == r.converged
+        np.testing.assert_array_equal(fused.f, r.f)
+        np.testing.assert_array_equal(fused.g, r.g)
     if case == "unbalanced-checks":
         assert fused.converged
 

@@ -14,6 +14,7 @@
 namespace sk {
 
 constexpr float kDeltaCap = 50.0f;     // cap of (g_old - g_new) / eps in the balanced check (sinkhorn.py:60)
+constexpr int kMergeBatch = 16;        // partial slots a merging thread loads at once (their latencies overlap)
 
 __device__ __forceinline__ float ep_ex2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float ep_lg2(float x) { return __builtin_amdgcn_logf(x); }
@@ -150,12 +151,13 @@ __device__ inline bool merge_group(const PartialArgs& a, int g) {
     const float o = a.off != nullptr ? a.off[ic] : 0.0f;
     const float old = a.meas != nullptr ? a.out[ic] : 0.0f;
     const float wi = a.meas != nullptr ? a.w[ic] : 0.0f;
-    // The first eight slots of the row (all there are up to 8 workgroups per row group) come with the scalars.
+    // The first kMergeBatch slots of the row (all there are up to that many workgroups per row group) come with
+    // the scalars.
     const int p0 = first_wg(g, a.s), p1 = last_wg(g, a.s);
     const float2* pp = a.part + ic;
-    float2 v0[8];
+    float2 v0[kMergeBatch];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) v0[k] = p0 + k <= p1 ? ld<COH>(pp + (size_t)k * a.rows_pad) : make_float2(kEmpty, 0.0f);
+    for (int k = 0; k < kMergeBatch; ++k) v0[k] = p0 + k <= p1 ? ld<COH>(pp + (size_t)k * a.rows_pad) : make_float2(kEmpty, 0.0f);
     const int skip = *skip_p;
     asm volatile("" ::"s"(sc0), "s"(sc1), "s"(sc2), "s"(sc3), "s"(cb), "s"(cb_s2), "s"(s2), "v"(x2), "v"(o),
                  "v"(old), "v"(wi), "v"(skip));
@@ -167,21 +169,21 @@ __device__ inline bool merge_group(const PartialArgs& a, int g) {
     float dmax = 0.0f;
     double derr = 0.0;
     if (i < a.rows_pad) {
-        // One pass, online: (M, S) <- (max(M, m_k), S 2^(c (M - M')) + s_k 2^(c (m_k - M'))), slots loaded eight
-        // at a time so that their latencies overlap.
+        // One pass, online: (M, S) <- (max(M, m_k), S 2^(c (M - M')) + s_k 2^(c (m_k - M'))), slots loaded
+        // kMergeBatch at a time so that their latencies overlap.
         float M = kEmpty, S = 0.0f;
-        for (int q = p0; q <= p1; q += 8) {
-            float2 v[8];
+        for (int q = p0; q <= p1; q += kMergeBatch) {
+            float2 v[kMergeBatch];
 #pragma unroll
-            for (int k = 0; k < 8; ++k)
+            for (int k = 0; k < kMergeBatch; ++k)
                 v[k] = q == p0 ? v0[k]
                                : q + k <= p1 ? ld<COH>(pp + (size_t)(q + k - p0) * a.rows_pad) : make_float2(kEmpty, 0.0f);
             float Mn = M;
 #pragma unroll
-            for (int k = 0; k < 8; ++k) Mn = fmaxf(Mn, v[k].x);
+            for (int k = 0; k < kMergeBatch; ++k) Mn = fmaxf(Mn, v[k].x);
             float Sn = S * ep_ex2(c * (M - Mn));
 #pragma unroll
-            for (int k = 0; k < 8; ++k) Sn += v[k].y * ep_ex2(c * (v[k].x - Mn));
+            for (int k = 0; k < kMergeBatch; ++k) Sn += v[k].y * ep_ex2(c * (v[k].x - Mn));
             M = Mn;
             S = Sn;
         }

@@ -39,9 +39,10 @@
 //
 // A half-step is two launches: the partial kernel, then the merge kernel, one workgroup per row group, which
 // merges the group's slots and applies the epilogue (sk_epilogue.h). The on-device loop
-// (src/trnopt/sinkhorn.py:346-378) is two launches per iteration, the f and the g update's partial kernels: in
-// them the last workgroup to finish a row group merges it (per-group arrival counters; TRNOPT_HIP_FUSED_MERGE=0
-// launches the merge kernel after each instead). The f update's merge of group 0 counts the iteration; in the g
+// (src/trnopt/sinkhorn.py:346-378) runs the f and the g update's partial kernels per iteration; in a pass of 40
+// row groups or more the last workgroup to finish a row group merges it (per-group arrival counters), and a
+// smaller pass launches the merge kernel after its partial kernel (fused_merge below): two to four launches
+// per iteration. The f update's merge of group 0 counts the iteration; in the g
 // update the merges also produce per-group convergence partials, and at a check, a schedule step or the last
 // iteration the last group's merge runs the balanced / unbalanced checks at the reference's cadence, advances
 // the stage, sets `done`, and writes the next iteration's eps and {2/eps, 1/eps, eps, kappa} into the device
@@ -432,9 +433,19 @@ int check_cloud(const sk_cloud_f32& c, const char* name) {
 // TRNOPT_HIP_LOG2=0 turns the log2-unit copies off (every half-step then scales on the VALU), to compare the paths.
 bool log2_enabled() { return env_int("TRNOPT_HIP_LOG2", 1) != 0; }
 
-// Whether the on-device loop merges each row group inside the partial kernel (default) or launches the merge
-// kernel after it (TRNOPT_HIP_FUSED_MERGE=0, the form of the single half-step entry points).
-bool fused_merge_enabled() { return env_int("TRNOPT_HIP_FUSED_MERGE", 1) != 0; }
+// Whether a pass of the on-device loop merges its row groups inside the partial kernel or launches the merge
+// kernel after it (the form of the single half-step entry points). Merging in the partial kernel saves the
+// merge launch and overlaps each group's merge with the other groups' tiles, but adds the arrival (a wait for
+// the slot stores and an atomic round trip) and device-coherent slot loads to the tail of every row group.
+// Measured on the loop at d 30 and d 64, it breaks even at 40 row groups (10k rows) and costs 1-1.5 us per
+// half-step from 2k to 9k rows, so it is taken from 40 row groups up. TRNOPT_HIP_FUSED_MERGE=1 or 0 forces
+// either form for every pass.
+constexpr int kFuseMinGroups = 40;
+
+bool fused_merge(const Plan& pl) {
+    const int v = env_int("TRNOPT_HIP_FUSED_MERGE", -1);
+    return v < 0 ? pl.ngroups >= kFuseMinGroups : v != 0;
+}
 
 void launch_bake(void* first, const void* second, int npad, int nc, const float* sc, hipStream_t st) {
     if (!log2_enabled()) return;
@@ -722,7 +733,7 @@ int sk_loop_run_f32(const sk_loop_f32* L, int iters, void* stream) {
     f.n_store = L->x.npad;
     f.tick = st;
     f.part = part;
-    f.group_counters = fused_merge_enabled() ? lo.counters + 1 : nullptr;
+    f.group_counters = fused_merge(pf) ? lo.counters + 1 : nullptr;
 
     Pass g = {};
     g.xr = L->y.pk;
@@ -751,7 +762,7 @@ int sk_loop_run_f32(const sk_loop_f32* L, int iters, void* stream) {
     g.state = st;
     g.cfg = cfg;
     g.rebake = log2_enabled() ? (char*)const_cast<void*>(L->x.pk) : nullptr;
-    g.group_counters = f.group_counters;
+    g.group_counters = fused_merge(pg) ? lo.counters + 1 : nullptr;
 
     for (int k = 0; k < iters; ++k) {
         hipError_t e = run_pass(f, pf, hs);

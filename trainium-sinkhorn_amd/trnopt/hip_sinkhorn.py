@@ -329,7 +329,8 @@ def cost_median(xc: np.ndarray, yc: np.ndarray, device) -> float:
 class DeviceLoop:
     """The iteration loop of src/trnopt/sinkhorn.py:346-378 on the GPU.
 
-    Each enqueued iteration is two partial-kernel launches, each merging its own row groups: f update (X rows
+    Each enqueued iteration is two partial-kernel launches (each merging its own row groups from 40 row
+    groups up, followed by a merge-kernel launch below that): f update (X rows
     against Y; counts the iteration), g update (Y rows against X, which also reduces the convergence measures;
     the last row group's merge runs the reference's checks at its cadence, sets `done` and writes the next
     eps's scalars). Kernels enqueued after
@@ -337,7 +338,7 @@ class DeviceLoop:
     next batch already queued behind it (no per-iteration synchronisation).
 
     With TRNOPT_HIP_GRAPH=1, whole batches of GRAPH_BATCH iterations are replayed from one captured HIP graph
-    (20 kernels, no memset nodes): fewer host calls, for callers whose host enqueue is the bottleneck. Graph
+    (20 to 40 kernels, no memset nodes): fewer host calls, for callers whose host enqueue is the bottleneck. Graph
     and eager launches run the same kernels with the same arguments, so the results are bit-identical. The
     default is eager: the GPU-bound loop measured no faster from graphs, and each solve would pay a capture."""
 

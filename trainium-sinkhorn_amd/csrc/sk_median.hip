@@ -9,9 +9,9 @@
 //
 // Radix select on the fused cost stream: non-negative doubles order like their bit patterns, so the k-th
 // smallest cost is found digit by digit from the top (11, 11, 11, 11, 11, 9 bits). Each pass recomputes every
-// C_ij tile by tile (256 rows x 32 columns per step: the 32 column points in LDS, one row per thread, the
-// dot products in registers), keeps the pairs whose high bits equal the prefix found so far, and histograms
-// their next digit in LDS; a one-workgroup scan then picks the digit holding rank k and narrows the prefix.
+// C_ij tile by tile (256 rows x 32 columns per step: one row per thread, the dot products in registers, the
+// column coordinates from zero-padded copies through the scalar cache), keeps the pairs whose high bits equal
+// the prefix found so far, and histograms their next digit in LDS; a one-workgroup scan then picks the digit holding rank k and narrows the prefix.
 // The two ranks k0 and k1 share one histogram while their prefixes agree. Nothing is stored per pair: the
 // cost never reaches memory, and every launch goes on the caller's stream with no host round trip.
 
@@ -29,8 +29,8 @@ using sk::hip_fail;
 constexpr int kBins = 2048;                 // 11-bit digits
 constexpr int kRowsPerBlock = 256;          // one row per thread
 constexpr int kColTile = 32;                // column points per LDS tile
-constexpr int kColsPerBlock = 256;          // column points per workgroup (8 tiles)
-constexpr int kChunk = 32;                  // coordinates per register chunk of the row
+constexpr int kTargetBlocks = 1024;         // workgroups a pass aims for (4 per CU): columns per workgroup follow
+constexpr int kChunk = 8;                   // coordinates per register chunk of the row
 constexpr int kPasses = 6;
 constexpr int kShift[kPasses] = {53, 42, 31, 20, 9, 0};
 constexpr int kWidth[kPasses] = {11, 11, 11, 11, 11, 9};
@@ -67,12 +67,26 @@ __device__ __forceinline__ unsigned long long cost_key(double c) {
     return b & 0x7fffffffffffffffull;
 }
 
-// One digit pass over the workgroup's 256 x 256 block of pairs.
+// Row-major copy of p (n x d) with rows of dp coordinates (zeros after d) and zero rows up to n_pad.
+__global__ void pad_kernel(const double* __restrict__ p, int n, int d, int n_pad, int dp, double* __restrict__ out) {
+    const long long total = (long long)n_pad * dp;
+    for (long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (long long)gridDim.x * blockDim.x) {
+        const long long i = e / dp;
+        const int k = (int)(e - i * dp);
+        out[e] = i < n && k < d ? p[i * d + k] : 0.0;
+    }
+}
+
+// One digit pass over the workgroup's block of 256 rows x `cols` columns, on the zero-padded copies (rows of
+// dp coordinates, a multiple of 8; the column copy padded to whole tiles of 32 points). Each thread keeps its
+// row's dot products with a tile of 32 column points in registers and takes the row's coordinates 8 at a
+// time; the column coordinates are the same for every lane, so they come through the scalar cache as
+// operands of the fma (no LDS traffic). The dot products sum over k in ascending order, one fma each; the
+// padding adds 0 * 0.
 __global__ __launch_bounds__(kRowsPerBlock) void select_pass_kernel(
-    const double* __restrict__ x, const double* __restrict__ y, const double* __restrict__ xx,
-    const double* __restrict__ yy, int n, int m, int d, const SelectState* __restrict__ st,
+    const double* __restrict__ xp, const double* __restrict__ yp, const double* __restrict__ xx,
+    const double* __restrict__ yy, int n, int m, int dp, int cols, const SelectState* __restrict__ st,
     unsigned* __restrict__ hist, int shift, int width) {
-    __shared__ double ys[kColTile * 129];          // kColTile points, row stride d + 1 (d <= 128)
     __shared__ unsigned h[2][kBins];
     const int tid = threadIdx.x;
     const int same = st->same;
@@ -80,52 +94,45 @@ __global__ __launch_bounds__(kRowsPerBlock) void select_pass_kernel(
     const unsigned long long p0 = st->prefix[0] & high, p1 = st->prefix[1] & high;
     const unsigned dmask = (1u << width) - 1u;
     for (int b = tid; b < 2 * kBins; b += kRowsPerBlock) (&h[0][0])[b] = 0u;
+    __syncthreads();
 
     const int i = blockIdx.x * kRowsPerBlock + tid;
     const bool row_ok = i < n;
     const double xi2 = row_ok ? xx[i] : 0.0;
-    const double* xr = x + (size_t)(row_ok ? i : 0) * d;
-    const int ld = d + 1;
-    const int j_begin = blockIdx.y * kColsPerBlock;
-    const int j_end = j_begin + kColsPerBlock < m ? j_begin + kColsPerBlock : m;
+    const double* xr = xp + (size_t)(row_ok ? i : 0) * dp;
+    const int j_begin = blockIdx.y * cols;
+    const long long j_lim = (long long)j_begin + cols;
+    const int j_end = j_lim < m ? (int)j_lim : m;
 
     for (int j0 = j_begin; j0 < j_end; j0 += kColTile) {
         const int nj = j_end - j0 < kColTile ? j_end - j0 : kColTile;
-        __syncthreads();                           // previous tile's reads (and the histogram clear) done
-        for (int e = tid; e < nj * d; e += kRowsPerBlock) {
-            const int jj = e / d, kk = e - jj * d;
-            ys[jj * ld + kk] = y[(size_t)(j0 + jj) * d + kk];
-        }
-        __syncthreads();
+        const double* yt = yp + (size_t)j0 * dp;
         double acc[kColTile];
 #pragma unroll
         for (int jj = 0; jj < kColTile; ++jj) acc[jj] = 0.0;
-        for (int k0 = 0; k0 < d; k0 += kChunk) {
-            const int kn = d - k0 < kChunk ? d - k0 : kChunk;
+        for (int k0 = 0; k0 < dp; k0 += kChunk) {
             double xv[kChunk];
 #pragma unroll
-            for (int kk = 0; kk < kChunk; ++kk) xv[kk] = kk < kn ? xr[k0 + kk] : 0.0;
+            for (int e = 0; e < kChunk; ++e) xv[e] = xr[k0 + e];
 #pragma unroll
             for (int jj = 0; jj < kColTile; ++jj) {
-                const double* yr = ys + jj * ld + k0;
+                const double* yr = yt + (size_t)jj * dp + k0;
                 double a = acc[jj];
 #pragma unroll
-                for (int kk = 0; kk < kChunk; ++kk)
-                    if (kk < kn) a = fma(xv[kk], yr[kk], a);
+                for (int e = 0; e < kChunk; ++e) a = fma(xv[e], yr[e], a);
                 acc[jj] = a;
             }
         }
-        if (row_ok) {
 #pragma unroll
-            for (int jj = 0; jj < kColTile; ++jj) {
-                if (jj < nj) {
-                    const double c = (xi2 + yy[j0 + jj]) - 2.0 * acc[jj];
-                    const unsigned long long key = cost_key(c);
-                    const unsigned digit = (unsigned)(key >> shift) & dmask;
-                    if ((key & high) == p0) atomicAdd(&h[0][digit], 1u);
-                    if (!same && (key & high) == p1) atomicAdd(&h[1][digit], 1u);
-                }
-            }
+        for (int jj = 0; jj < kColTile; ++jj) {
+            const bool ok = row_ok && jj < nj;
+            const double c = (xi2 + (jj < nj ? yy[j0 + jj] : 0.0)) - 2.0 * acc[jj];
+            const unsigned long long key = cost_key(c);
+            const unsigned digit = (unsigned)(key >> shift) & dmask;
+            const bool m0 = ok && (key & high) == p0;
+            const bool m1 = ok && !same && (key & high) == p1;
+            if (m0) atomicAdd(&h[0][digit], 1u);
+            if (m1) atomicAdd(&h[1][digit], 1u);
         }
     }
     __syncthreads();
@@ -191,6 +198,8 @@ __global__ void select_finish_kernel(const SelectState* st, double* out) {
 }
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+int padded_dim(int d) { return (d + kChunk - 1) / kChunk * kChunk; }
+int padded_cols(int m) { return (m + kColTile - 1) / kColTile * kColTile; }
 
 }  // namespace
 
@@ -198,8 +207,9 @@ extern "C" {
 
 size_t sk_cost_median_workspace_bytes(int n, int m, int d) {
     if (n < 1 || m < 1 || d < 1 || d > SK_MEDIAN_D_MAX) return 0;
+    const size_t dp = (size_t)padded_dim(d);
     return align256(sizeof(SelectState)) + align256(2 * kBins * sizeof(unsigned)) + align256((size_t)n * 8) +
-           align256((size_t)m * 8);
+           align256((size_t)m * 8) + align256((size_t)n * dp * 8) + align256((size_t)padded_cols(m) * dp * 8);
 }
 
 int sk_cost_median_f64(const double* xc, const double* yc, int n, int m, int d, double* out, void* ws,
@@ -221,15 +231,28 @@ int sk_cost_median_f64(const double* xc, const double* yc, int n, int m, int d, 
     double* xx = (double*)p;
     p += align256((size_t)n * 8);
     double* yy = (double*)p;
+    p += align256((size_t)m * 8);
+    const int dp = padded_dim(d), mp = padded_cols(m);
+    double* xp = (double*)p;
+    p += align256((size_t)n * dp * 8);
+    double* yp = (double*)p;
     hipStream_t s = (hipStream_t)stream;
     hipLaunchKernelGGL(norms_kernel, dim3((n + 255) / 256), dim3(256), 0, s, xc, n, d, xx);
     hipLaunchKernelGGL(norms_kernel, dim3((m + 255) / 256), dim3(256), 0, s, yc, m, d, yy);
+    hipLaunchKernelGGL(pad_kernel, dim3(1024), dim3(256), 0, s, xc, n, d, n, dp, xp);
+    hipLaunchKernelGGL(pad_kernel, dim3(1024), dim3(256), 0, s, yc, m, d, mp, dp, yp);
     hipLaunchKernelGGL(select_init_kernel, dim3(1), dim3(1024), 0, s, st, hist,
                        (unsigned long long)n * (unsigned long long)m);
-    const dim3 grid((n + kRowsPerBlock - 1) / kRowsPerBlock, (m + kColsPerBlock - 1) / kColsPerBlock);
+    // 256 rows per workgroup; the columns split into blocks (multiples of a tile) so that a pass has about
+    // kTargetBlocks workgroups, each flushing its nonzero bins once.
+    const int rb = (n + kRowsPerBlock - 1) / kRowsPerBlock;
+    const int want = (kTargetBlocks + rb - 1) / rb;
+    int cols = (m + want - 1) / want;
+    cols = (cols + kColTile - 1) / kColTile * kColTile;
+    const dim3 grid(rb, (m + cols - 1) / cols);
     for (int q = 0; q < kPasses; ++q) {
-        hipLaunchKernelGGL(select_pass_kernel, grid, dim3(kRowsPerBlock), 0, s, xc, yc, xx, yy, n, m, d, st, hist,
-                           kShift[q], kWidth[q]);
+        hipLaunchKernelGGL(select_pass_kernel, grid, dim3(kRowsPerBlock), 0, s, xp, yp, xx, yy, n, m, dp, cols, st,
+                           hist, kShift[q], kWidth[q]);
         hipLaunchKernelGGL(select_scan_kernel, dim3(1), dim3(1024), 0, s, st, hist, kShift[q], kWidth[q]);
     }
     hipLaunchKernelGGL(select_finish_kernel, dim3(1), dim3(64), 0, s, st, out);

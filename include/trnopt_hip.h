@@ -194,8 +194,10 @@ int sk_loop_run_f32(const sk_loop_f32* L, int iters, void* stream);
  * over the materialised n x m float64 matrix:
  *     median over i < n, j < m of max((|xc_i|^2 + |yc_j|^2) - 2 xc_i . yc_j, 0)   (float64),
  * np.median's definition (mean of the two middle values when n m is even). xc (n, d), yc (m, d): row-major
- * float64 device arrays, already centred; out: one device double. The cost is recomputed in each of six
- * radix-select passes and never stored. n m < 2^32, d <= SK_MEDIAN_D_MAX; ws 256-byte aligned.
+ * float64 device arrays, already centred; out: one device double. Six radix-select passes over the cost
+ * keys: the first three recompute every cost, the third keeping the keys that can still hold the answer
+ * (up to 2^22 of them, 8 bytes each, in ws) for the last three. ws (sk_cost_median_workspace_bytes) also
+ * holds zero-padded copies of xc and yc. n m < 2^32, d <= SK_MEDIAN_D_MAX; ws 256-byte aligned.
  */
 #define SK_MEDIAN_D_MAX 128
 size_t sk_cost_median_workspace_bytes(int n, int m, int d);

@@ -37,6 +37,19 @@ def test_identical_clouds_have_zero_costs(hip):
     assert got == dense_median(x, x)
 
 
+@pytest.mark.parametrize("n", [2000, 2100])
+def test_two_tied_costs_across_the_middle_ranks(hip, n):
+    """n x n pairs of two costs, 0 and 1, split so that the two middle ranks fall on different ones (median 0.5).
+    Every key matches a rank's prefix in the third pass, which collects them for the last three: 4.0M keys fit
+    the 2^22 it keeps; 4.41M do not, and the last passes recompute every cost instead."""
+    x = np.tile([1.0, 2.0, 3.0], (n, 1))
+    y = x.copy()
+    y[n // 2:, 2] = 4.0
+    print("tied median", n, flush=True)
+    got = hip.cost_median(x, y, "cuda")
+    assert got == dense_median(x, y) == 0.5
+
+
 def test_single_cell_shaped_median_matches_the_reference_host_routine(hip):
     """The unbalanced single-cell workload's cost (7,355 x 8,962, d 30): the GPU median against the host
     normalisation the reference runs (one 527 MB float64 matrix)."""

@@ -130,6 +130,22 @@ int sk_half_step_f32(const void* x_pk, const float* xsq, const float* off, int r
                      void* ws, size_t ws_bytes, void* stream);
 
 /*
+ * sk_half_step_f32 without a workspace argument, for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the reference.
+ * The partial (max, sum) slots live in a static device array of SK_NOALLOC_SCRATCH_BYTES that the library
+ * holds on every GPU it runs on until the process ends; the call itself allocates nothing. Same arguments,
+ * results and launches as sk_half_step_f32 (bit-identical output); a shape whose
+ * sk_half_step_workspace_bytes() exceeds SK_NOALLOC_SCRATCH_BYTES is rejected with SK_E_WORKSPACE before
+ * anything is enqueued. Every call on one GPU shares that GPU's array: calls that overlap on one GPU
+ * (several host threads, or several streams running at once) race and must be serialised by the caller.
+ */
+#define SK_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
+int sk_half_step_noalloc_f32(const void* x_pk, const float* xsq, const float* off, int rows_pad,
+                             const void* y_pk, const float* gh, const float* log_b, int m_pad, int d,
+                             int rows_role, const float* sc, const int* skip, float* fh,
+                             float* meas, const float* w, int n_real, void* stream);
+
+/*
  * On-device Sinkhorn loop: the body of src/trnopt/sinkhorn.py:346-378 (eps schedule or stages, f then
  * g update, stage advance, balanced / unbalanced checks every check_every iterations, fp32 floors).
  */

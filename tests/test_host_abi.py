@@ -107,6 +107,27 @@ def test_half_step_shape_rules(hk):
     assert b"rows_role" in lb.sk_last_error()
 
 
+def test_noalloc_half_step_validates_like_the_workspace_entry_point(hk):
+    """sk_half_step_noalloc_f32 applies sk_half_step_f32's checks and refuses shapes whose partial slots would
+    not fit its static scratch (SK_NOALLOC_SCRATCH_BYTES), all before any device call."""
+    lb = hk.lib()
+    fake = 4096
+    limit = int(re.search(r"#define SK_NOALLOC_SCRATCH_BYTES \(\(size_t\)(\d+) << (\d+)\)", HEADER.read_text())
+                .group(1)) << 20
+    assert limit == 16 << 20
+    assert lb.sk_half_step_noalloc_f32(None, None, None, 32, None, None, None, 32, 4, 0, None, None, None, None, None,
+                                       1, None) == -1
+    assert lb.sk_half_step_noalloc_f32(fake, fake, None, 33, fake, fake + 256, fake, 32, 4, 0, fake, None, fake + 512,
+                                       None, None, 1, None) == -2
+    assert lb.sk_half_step_noalloc_f32(fake, fake, None, 32, fake, fake, fake, 32, 4, 0, fake, None, fake, None, None,
+                                       1, None) == -1
+    rows_pad = (1 << 21) + 32                      # one slot per row: 8 bytes x rows_pad > 16 MiB
+    assert lb.sk_half_step_workspace_bytes(rows_pad, 32, 4) > limit
+    assert lb.sk_half_step_noalloc_f32(fake, fake, None, rows_pad, fake, fake + 256, fake, 32, 4, 0, fake, None,
+                                       fake + 512, None, None, 1, None) == -3
+    assert b"static scratch" in lb.sk_last_error()
+
+
 # ---------------------------------------------------------------------------------------------------------
 # Selection and validation of the Python API (src/trnopt/sinkhorn.py:196-208, 254-276; backend.py:30-48)
 

@@ -59,6 +59,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
 
 #include "sk_common.h"
 #include "sk_epilogue.h"
@@ -575,26 +576,36 @@ size_t sk_half_step_workspace_bytes(int rows_pad, int m_pad, int d) {
 
 int sk_half_step_meas_count(int rows_pad) { return rows_pad < 1 ? 0 : meas_count(rows_pad); }
 
-int sk_half_step_f32(const void* x_pk, const float* xsq, const float* off, int rows_pad, const void* y_pk,
-                     const float* gh, const float* log_b, int m_pad, int d, int rows_role, const float* sc,
-                     const int* skip, float* fh, float* meas, const float* w, int n_real, void* ws, size_t ws_bytes,
-                     void* stream) {
+}  // extern "C"
+
+namespace {
+
+// Argument checks shared by the two half-step entry points (everything but the workspace).
+int check_half_step(const char* who, const void* x_pk, const float* xsq, int rows_pad, const void* y_pk,
+                    const float* gh, const float* log_b, int m_pad, int d, int rows_role, const float* sc,
+                    const float* fh, const float* meas, const float* w) {
     if (x_pk == nullptr || xsq == nullptr || y_pk == nullptr || gh == nullptr || log_b == nullptr || sc == nullptr ||
-        fh == nullptr || ws == nullptr)
-        return fail(SK_E_ARG, "sk_half_step_f32: null pointer");
-    if (meas != nullptr && w == nullptr) return fail(SK_E_ARG, "sk_half_step_f32: meas needs w");
-    if (fh == gh) return fail(SK_E_ARG, "sk_half_step_f32: fh must not alias gh");
+        fh == nullptr)
+        return fail(SK_E_ARG, "%s: null pointer", who);
+    if (meas != nullptr && w == nullptr) return fail(SK_E_ARG, "%s: meas needs w", who);
+    if (fh == gh) return fail(SK_E_ARG, "%s: fh must not alias gh", who);
     if (rows_pad < SK_TILE || rows_pad % SK_TILE != 0 || m_pad < SK_TILE || m_pad % SK_TILE != 0)
-        return fail(SK_E_SHAPE, "sk_half_step_f32: rows_pad %d and m_pad %d must be positive multiples of %d",
-                    rows_pad, m_pad, SK_TILE);
+        return fail(SK_E_SHAPE, "%s: rows_pad %d and m_pad %d must be positive multiples of %d", who, rows_pad, m_pad,
+                    SK_TILE);
     if (int r = check_kp(d)) return r;
-    if (rows_role != 0 && rows_role != 1) return fail(SK_E_ARG, "sk_half_step_f32: rows_role %d not 0 or 1", rows_role);
+    if (rows_role != 0 && rows_role != 1) return fail(SK_E_ARG, "%s: rows_role %d not 0 or 1", who, rows_role);
     if (!aligned16(x_pk) || !aligned16(y_pk) || !aligned16(gh) || !aligned16(log_b))
-        return fail(SK_E_ARG, "sk_half_step_f32: packed clouds, gh and log_b must be 16-byte aligned");
-    const size_t need = sk_half_step_workspace_bytes(rows_pad, m_pad, d);
-    if (need == 0) return fail(SK_E_SHAPE, "sk_half_step_f32: %d x %d is too large for one launch", rows_pad, m_pad);
-    if (ws_bytes < need) return fail(SK_E_WORKSPACE, "sk_half_step_f32: workspace %zu < %zu bytes", ws_bytes, need);
-    if (((uintptr_t)ws & 255) != 0) return fail(SK_E_ARG, "sk_half_step_f32: workspace must be 256-byte aligned");
+        return fail(SK_E_ARG, "%s: packed clouds, gh and log_b must be 16-byte aligned", who);
+    if (sk_half_step_workspace_bytes(rows_pad, m_pad, d) == 0)
+        return fail(SK_E_SHAPE, "%s: %d x %d is too large for one launch", who, rows_pad, m_pad);
+    return SK_OK;
+}
+
+// The partial kernel and the merge kernel of one half-step, partial slots at `part`.
+hipError_t launch_half_step(const void* x_pk, const float* xsq, const float* off, int rows_pad, const void* y_pk,
+                            const float* gh, const float* log_b, int m_pad, int d, int rows_role, const float* sc,
+                            const int* skip, float* fh, float* meas, const float* w, int n_real, void* part,
+                            hipStream_t stream) {
     const Plan pl = make_plan(rows_pad, m_pad, sk_pad_dim(d));
     Pass ps = {};
     ps.xr = x_pk;
@@ -616,9 +627,74 @@ int sk_half_step_f32(const void* x_pk, const float* xsq, const float* off, int r
     ps.meas = (float2*)meas;
     ps.w = w;
     ps.n_real = n_real;
-    ps.part = (float2*)ws;
-    const hipError_t e = run_pass(ps, pl, (hipStream_t)stream);
+    ps.part = (float2*)part;
+    return run_pass(ps, pl, stream);
+}
+
+// The no-allocation entry point's partial slots: a file-scope device array, one per GPU. In host code `scratch`
+// names a host-side stand-in, not device memory; its device address is looked up once per device
+// (hipGetSymbolAddress, with that device current) and only that address is handed to kernels.
+constexpr size_t kScratchBytes = SK_NOALLOC_SCRATCH_BYTES;
+__device__ __align__(256) char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's copy of `scratch` (looked up on the first call on that device).
+int scratch_on_current_device(void** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "sk_half_step_noalloc_f32: hipGetDevice");
+    if (dev < 0 || dev >= kMaxDevices) return fail(SK_E_DEVICE, "sk_half_step_noalloc_f32: device %d", dev);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_fail(e, "sk_half_step_noalloc_f32: hipGetSymbolAddress(scratch)");
+        if (p == nullptr || ((uintptr_t)p & 255) != 0)
+            return fail(SK_E_DEVICE, "sk_half_step_noalloc_f32: scratch address %p is not 256-byte aligned", p);
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return SK_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int sk_half_step_f32(const void* x_pk, const float* xsq, const float* off, int rows_pad, const void* y_pk,
+                     const float* gh, const float* log_b, int m_pad, int d, int rows_role, const float* sc,
+                     const int* skip, float* fh, float* meas, const float* w, int n_real, void* ws, size_t ws_bytes,
+                     void* stream) {
+    if (int r = check_half_step("sk_half_step_f32", x_pk, xsq, rows_pad, y_pk, gh, log_b, m_pad, d, rows_role, sc, fh,
+                                meas, w))
+        return r;
+    if (ws == nullptr) return fail(SK_E_ARG, "sk_half_step_f32: null pointer");
+    const size_t need = sk_half_step_workspace_bytes(rows_pad, m_pad, d);
+    if (ws_bytes < need) return fail(SK_E_WORKSPACE, "sk_half_step_f32: workspace %zu < %zu bytes", ws_bytes, need);
+    if (((uintptr_t)ws & 255) != 0) return fail(SK_E_ARG, "sk_half_step_f32: workspace must be 256-byte aligned");
+    const hipError_t e = launch_half_step(x_pk, xsq, off, rows_pad, y_pk, gh, log_b, m_pad, d, rows_role, sc, skip, fh,
+                                          meas, w, n_real, ws, (hipStream_t)stream);
     return e == hipSuccess ? SK_OK : hip_fail(e, "sk_half_step_f32");
+}
+
+int sk_half_step_noalloc_f32(const void* x_pk, const float* xsq, const float* off, int rows_pad, const void* y_pk,
+                             const float* gh, const float* log_b, int m_pad, int d, int rows_role, const float* sc,
+                             const int* skip, float* fh, float* meas, const float* w, int n_real, void* stream) {
+    if (int r = check_half_step("sk_half_step_noalloc_f32", x_pk, xsq, rows_pad, y_pk, gh, log_b, m_pad, d, rows_role,
+                                sc, fh, meas, w))
+        return r;
+    const size_t need = sk_half_step_workspace_bytes(rows_pad, m_pad, d);
+    if (need > kScratchBytes)
+        return fail(SK_E_WORKSPACE, "sk_half_step_noalloc_f32: %d x %d needs %zu bytes of slots, above the %zu-byte "
+                    "static scratch (use sk_half_step_f32 with a workspace)", rows_pad, m_pad, need, kScratchBytes);
+    void* part = nullptr;
+    if (int r = scratch_on_current_device(&part)) return r;
+    const hipError_t e = launch_half_step(x_pk, xsq, off, rows_pad, y_pk, gh, log_b, m_pad, d, rows_role, sc, skip, fh,
+                                          meas, w, n_real, part, (hipStream_t)stream);
+    return e == hipSuccess ? SK_OK : hip_fail(e, "sk_half_step_noalloc_f32");
 }
 
 size_t sk_loop_workspace_bytes(int nx_pad, int ny_pad, int d) {

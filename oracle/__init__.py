@@ -20,8 +20,11 @@ How each function is pinned (tests/test_oracle.py):
       iterate-by-iterate equality with brute.sinkhorn_dense (no shifted potentials, no padding, dense C) for
       balanced / unbalanced / targets / eps_start / stages / blocks; plans against the converged brute force
       and wot's scaling form; row sums == a exactly after an f update.
-  reference.sinkhorn_ref, float32 -- within float32 rounding of the float64 run; the published float32 cost
-      of the same problem (0.8971549341961733, csv:5) to the float32 level.
+  reference.sinkhorn_ref, float32 -- within float32 rounding of the float64 run; the published float32 costs
+      of the same problem (0.8971549341961733 torch, 0.8971549319624892 NKI; csv:5,10) to the float32 level
+      (test_published_float32_cost_10k).
+  reference.eps_schedule -- its closed form eps_start decay^k (strictly above eps, capped at max_iters) and the
+      stage override (test_eps_schedule_closed_form), for the oracle and the product alike.
   brute.* -- closed forms and special cases (m = 1, identical columns, translation of the potentials,
       comparison against scipy on random inputs), and mutation tests that plant a wrong sign / index in the
       oracle and require a pin to fail.

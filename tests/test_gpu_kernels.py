@@ -220,7 +220,7 @@ def test_half_step_with_log2_copy_matches_float64(hip, rows, m, d, eps, kappa, m
 @pytest.mark.parametrize("eps,gscale,bake", [(0.1, 1e-3, False), (0.1, 1e-3, True), (0.1, 3e2, True),
                                              (0.01, 3e4, True), (1.0, 1e6, False), (1.0, 1e6, True)])
 def test_half_step_column_terms_across_magnitudes(hip, eps, gscale, bake):
-    """The matrix pipe adds each column term (gh_j + eps log b_j) / 2, in the kernel's units, as three fp16
+    """The matrix pipe adds each column term (gh_j + eps log b_j) / 2, in the kernel's units, as three bf16
     pieces: column terms from 1e-3 to 1e6 times the dot products, and a fifth of the columns masked by
     log b = -1e9 (weight exactly 0), meet the float64 known answer, with and without the log2-unit copy."""
     rows, m, d = 300, 2000, 16
@@ -250,6 +250,61 @@ def test_half_step_column_terms_across_magnitudes(hip, eps, gscale, bake):
                                     log_b.astype(np.float32)[keep], eps, 1.0)
     np.testing.assert_allclose(want, want_kept, rtol=1e-13, atol=0)
     assert inf_rel(out, want) < 2e-6, inf_rel(out, want)
+
+
+def _f32_floor(x, y, gh, log_b, eps, kappa, xsq, off):
+    """A float32 half-step's rounding floor on these inputs: a few ulps of the largest score
+    |z| = |(2 x.y + gh) / eps + log b| (times eps), plus the epilogue's roundings at |x|^2 and eps |off|."""
+    z = np.abs(2.0 * x.astype(np.float64) @ y.astype(np.float64).T + gh[None, :]) / eps + np.abs(log_b)[None, :]
+    return 8 * 2.0 ** -24 * (eps * z.max() + np.abs(xsq).max() + eps * np.abs(off).max()) + 1e-30
+
+
+@pytest.mark.parametrize("case,rows,m,d,eps,kappa", [("tiny", 500, 500, 16, 0.1, 1.0), ("tiny", 333, 777, 5, 0.02, 0.9),
+                                                     ("mixed", 300, 470, 64, 0.1, 1.0),
+                                                     ("mixed-rows-y", 470, 300, 64, 0.1, 1.0),
+                                                     ("mixed", 1000, 2100, 30, 0.05, 50 / 50.05)])
+def test_half_step_small_and_mixed_scale_clouds(hip, case, rows, m, d, eps, kappa):
+    """normalize=False inputs whose column terms dwarf the dot products in the kernel's units: clouds at 1e-4
+    (both scales 2^16, so sigma = 2^32 and eps log b / 2 = -0.31 is -1.3e9 kernel units) and x at 1e-6 against
+    y ~ N(0, 1) with gh ~ -|y|^2 (sigma |gh| / 2 ~ 1e9), m not a multiple of 32. The matrix pipe adds each
+    column term as three exact bf16 pieces (no range limit): the half-step meets the float64 known answer to
+    the float32 floor of its inputs, and the reference's float32 torch half-step as closely. (A column term
+    clamped to +-2^30 gave 0.12 here where |fh| ~ 1e-8.)"""
+    rng = np.random.default_rng(rows + m + d)
+    if case == "tiny":
+        x = rng.normal(size=(rows, d)) * 1e-4
+        y = rng.normal(size=(m, d)) * 1e-4
+        gh = np.zeros(m)
+    elif case == "mixed":
+        x = rng.normal(size=(rows, d)) * 1e-6
+        y = rng.normal(size=(m, d))
+        gh = -(y * y).sum(1) + rng.normal(scale=0.05, size=m)
+    else:                                              # the g update's direction: rows at N(0, 1), columns tiny
+        x = rng.normal(size=(rows, d))
+        y = rng.normal(size=(m, d)) * 1e-6
+        gh = rng.normal(scale=1e-6, size=m)
+    log_b = np.log(rng.uniform(0.5, 1.5, m) / m)
+    off = rng.normal(scale=0.3, size=rows) if kappa != 1.0 else np.zeros(rows)
+    role = 1 if case == "mixed-rows-y" else 0
+    X = hip.HipCloud(x, np.zeros(rows), DEV, off=off, role=role)
+    Y = hip.HipCloud(y, log_b, DEV, role=1 - role)
+    ghp = torch.zeros(Y.npad, dtype=torch.float32, device=DEV)
+    ghp[:m] = torch.as_tensor(gh, dtype=torch.float32)
+    sc = hip.scalars(eps, kappa, DEV)
+    print(f"small/mixed scales {case} rows={rows} m={m} d={d} eps={eps}", flush=True)
+    out = hip.half_step(X, Y, ghp, sc).cpu().numpy()[:rows].astype(np.float64)
+    x32, y32 = x.astype(np.float32), y.astype(np.float32)
+    xsq32 = (x * x).sum(1).astype(np.float32)
+    gh32, lb32, off32 = gh.astype(np.float32), log_b.astype(np.float32), off.astype(np.float32)
+    want = brute.half_step_f64(x32, xsq32, off32, y32, gh32, lb32, eps, float(np.float32(kappa)))
+    t = lambda a: torch.as_tensor(np.asarray(a), dtype=torch.float32)  # noqa: E731
+    got32 = ref.half_step(t(x32), t(xsq32), t(off32), t(y32).T.contiguous(), t(gh32), t(lb32),
+                          torch.tensor(1.0 / eps, dtype=torch.float32), torch.tensor(eps, dtype=torch.float32),
+                          torch.tensor(kappa, dtype=torch.float32)).double().numpy()
+    tol = _f32_floor(x32, y32, gh32, lb32, eps, kappa, xsq32, off32)
+    err, err32 = np.abs(out - want).max(), np.abs(got32 - want).max()
+    print(f"  |hip - f64| {err:.3e}, |torch f32 - f64| {err32:.3e}, floor {tol:.3e}, |fh| {np.abs(want).max():.3e}")
+    assert err <= tol, (err, err32, tol)
 
 
 @pytest.mark.parametrize("d", [3, 16, 64, 128])

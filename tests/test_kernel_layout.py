@@ -1,7 +1,8 @@
 """CPU emulation of the HIP kernels' index arithmetic (trainium-sinkhorn_amd/csrc).
 
 Every load and store of pack_cloud_kernel, lse_partial_kernel (global loads, LDS staging and reads, partial
-slots) and lse_finalize_kernel is replayed in numpy with the kernels' own formulas (workgroup renumbering,
+slots) and the merge of the slots (merge_group, sk_epilogue.h) is replayed in numpy with the kernels' own
+formulas (workgroup renumbering,
 stream-K ranges, partial slots, the power-of-two scale and two-piece fp16 packing, the
 v_mfma_f32_32x32x16_f16 operand and accumulator lane mapping, the product order of both row roles, the
 scaled accumulator units), asserting that every index is inside its buffer and that the emulated result
@@ -15,8 +16,6 @@ from scipy.special import logsumexp
 TILE, WAVES, XCDS, RB, BLOCK = 32, 4, 8, 2, 256
 STREAM_MAX_CHUNKS, COL_TILES = 4, 256        # streamed variant: nc <= 4; column terms staged per 256 tiles
 FOLD_COL_TILES = 192                         # ... per 192 tiles with the f16x2 contraction (folded, 16 B each)
-FOLD_MAX = np.float32(2.0 ** 30)             # folded column terms are clamped to +-2^30
-FOLD_SCALES = (2.0 ** 15, 2.0 ** 4, 2.0 ** -7)
 SEG_COST_STREAMED, SEG_COST_STAGED = 6, 2    # cost of a row-group boundary in tiles (sk_kernels.hip make_plan)
 ROWS_PER_GROUP = TILE * RB * WAVES
 EMPTY = -1.0e30
@@ -70,10 +69,28 @@ def split3(v):
 
 
 def fold_split(v):
-    """Streamed tiles with the f16x2 contraction: a column term v as three fp16 pieces, the A operand of one
-    MFMA against B = (2^15, 2^4, 2^-7): v = q0 2^15 + q1 2^4 + q2 2^-7 after clamping to +-2^30
+    """Streamed tiles with the f16x2 contraction: a column term v as three bf16 pieces, the A operand of one
+    v_mfma_f32_32x32x16_bf16 against B = (1, 1, 1): v = q0 + q1 + q2 exactly for every fp32 v
     (sk_lse_partial.hip, Streamed::run's stage_cols). Returns the pieces as float32 values."""
-    w = (np.clip(np.asarray(v, dtype=np.float32), -FOLD_MAX, FOLD_MAX) * np.float32(2.0 ** -15)).astype(np.float32)
+    return split3(v)
+
+
+def fold_b_operand():
+    """B of the column MFMA, per lane: ones in k = 0, 1, 2 of lanes 0-31, zeros elsewhere."""
+    b = np.zeros((64, 8), dtype=np.float32)
+    b[:32, :3] = 1.0
+    return b
+
+
+FP16_FOLD_MAX = np.float32(2.0 ** 30)
+FP16_FOLD_SCALES = (2.0 ** 15, 2.0 ** 4, 2.0 ** -7)
+
+
+def fp16_fold_split(v):
+    """An earlier form of the folded column term, kept here as a planted mistake: three fp16 pieces against
+    B = (2^15, 2^4, 2^-7), which only reach +-2^30 (terms beyond are clamped)."""
+    w = (np.clip(np.asarray(v, dtype=np.float32), -FP16_FOLD_MAX, FP16_FOLD_MAX) * np.float32(2.0 ** -15)
+         ).astype(np.float32)
     q0 = w.astype(np.float16).astype(np.float32)
     r1 = ((w - q0) * np.float32(2.0 ** 11)).astype(np.float32)
     q1 = r1.astype(np.float16).astype(np.float32)
@@ -81,10 +98,9 @@ def fold_split(v):
     return q0, q1, q2
 
 
-def fold_b_operand():
-    """B of the column MFMA, per lane: the three scales in k = 0, 1, 2 of lanes 0-31, zeros elsewhere."""
+def fp16_fold_b_operand():
     b = np.zeros((64, 8), dtype=np.float32)
-    b[:32, :3] = FOLD_SCALES
+    b[:32, :3] = FP16_FOLD_SCALES
     return b
 
 
@@ -185,10 +201,14 @@ def mfma_32x32x16(Aop, Bop):
     return D[m, (lane % 32)[:, None]]
 
 
-def emulate_lse(xa, ya, role=0, ncu=256, per_cu=1, c=np.log2(np.e), contraction="bf16x3"):
+def emulate_lse(xa, ya, role=0, ncu=256, per_cu=1, c=np.log2(np.e), contraction="bf16x3", col=None,
+                fold_rule=(fold_split, fold_b_operand)):
     """Row LSE (plain mode: alpha = 1 on a 0 / -1e30 mask, beta = 0) through the kernels' index math, the
     score / max / sum arithmetic in float32 as on the GPU (overflow or NaN raises). The product's row-LSE entry
-    point uses bf16x3; f16x2 (the half-steps' packing) runs through the same index math here."""
+    point uses bf16x3; f16x2 (the half-steps' packing) runs through the same index math here.
+    With `col` (pad_points(m) column terms in accumulator units, padding included), the half-step's scores
+    c (x.y + col_j) instead: the result is then L_i = M_i + log2(S_i) / c in accumulator units (the plain mode's
+    natural-log LSE for c = log2(e)). `fold_rule` is the (pieces, B operand) pair of the folded column term."""
     PIECES, FIRST_, SECOND_ = CONTRACTIONS[contraction]
     rows, K = xa.shape
     m = ya.shape[0]
@@ -199,7 +219,11 @@ def emulate_lse(xa, ya, role=0, ncu=256, per_cu=1, c=np.log2(np.e), contraction=
     sx, xr = pack(xa, rows, K, contraction)
     sy, yc = pack(ya, m, K, contraction)
     sigma, inv_sigma = np.float32(sx * sy), np.float32((1 / sx) * (1 / sy))
-    u_raw = np.where(np.arange(mp) < m, 0.0, -1.0e30).astype(np.float32)
+    if col is None:
+        u_raw = np.where(np.arange(mp) < m, 0.0, -1.0e30).astype(np.float32)
+    else:
+        u_raw = np.asarray(col, dtype=np.float32)
+        assert u_raw.shape == (mp,)
     with np.errstate(over="ignore"):
         u = np.maximum((u_raw * sigma).astype(np.float32), PAD_SCORE)     # scaled column term, floored
     nrb, nt, ngroups, s, slots = plan(rp, mp, ncu, per_cu, nc=nc)
@@ -235,7 +259,7 @@ def emulate_lse(xa, ya, role=0, ncu=256, per_cu=1, c=np.log2(np.e), contraction=
                     assert k.max() < lds_col.shape[0] and (t0 * 32 + k).max() < mp
                     if fold:
                         lds_col[k] = 0.0
-                        lds_col[k, 0], lds_col[k, 1], lds_col[k, 2] = fold_split(u[t0 * 32 + k])
+                        lds_col[k, 0], lds_col[k, 1], lds_col[k, 2] = fold_rule[0](u[t0 * 32 + k])
                     else:
                         lds_col[k] = u[t0 * 32 + k]
                     for t in range(t0, t1):
@@ -281,7 +305,7 @@ def emulate_lse(xa, ya, role=0, ncu=256, per_cu=1, c=np.log2(np.e), contraction=
                             for pp in range(len(FIRST_)):
                                 acc += mfma_32x32x16(yv[cc, ca[pp]], xv[cc, ra[pp]])
                         if fold:                                   # the column MFMA, after the dot product
-                            acc += mfma_32x32x16(cbuf, fold_b_operand())
+                            acc += mfma_32x32x16(cbuf, fold_rule[1]())
                             a = acc.astype(np.float32)
                         else:
                             ci = 8 * np.arange(4)[None, :, None] + 4 * h[:, None, None] + np.arange(4)[None, None, :]
@@ -299,7 +323,8 @@ def emulate_lse(xa, ya, role=0, ncu=256, per_cu=1, c=np.log2(np.e), contraction=
                     if rb0 + bb < nrb:
                         idx = (rb0 + bb) * 32 + lane[:32]
                         assert idx.max() < rp
-                        part[slot, idx, 0], part[slot, idx, 1] = Mn[:32] * inv_sigma, Sn[:32]
+                        part[slot, idx, 0] = np.maximum(Mn[:32] * inv_sigma, np.float32(EMPTY))
+                        part[slot, idx, 1] = Sn[:32]
             uu += te - tb
     assert np.all(seen == 1), "every (row group, tile) unit exactly once"
     out = np.empty(rp)
@@ -310,7 +335,7 @@ def emulate_lse(xa, ya, role=0, ncu=256, per_cu=1, c=np.log2(np.e), contraction=
         v = part[: p1 - p0 + 1, i]
         assert not np.isnan(v).any(), (i, g, p0, p1)
         Mx = v[:, 0].max()
-        out[i] = Mx + np.log(np.sum(v[:, 1] * np.exp2(c * (v[:, 0] - Mx))))
+        out[i] = Mx + np.log2(np.sum(v[:, 1] * np.exp2(c * (v[:, 0] - Mx)))) / c
     return out[:rows], dict(slots=slots, P=s.P, work=s.work)
 
 
@@ -536,28 +561,70 @@ def test_split3_is_exact_over_the_fp32_range():
 
 
 def test_fold_split_reproduces_column_terms():
-    """The folded column term: three fp16 pieces against (2^15, 2^4, 2^-7) reproduce any fp32 value in
-    [-2^30, 2^30] to within 2^-32 absolute, exactly from magnitude 2^-8 on; beyond, the clamp. The padding
-    floor (-1e30) becomes -2^30, 8 times the largest dot product the kernel forms (below 2^20 d <= 2^27 in its
-    units: pieces below 2^15 and 2^5)."""
+    """The folded column term: three bf16 pieces summed against B = (1, 1, 1) reproduce every fp32 value of
+    magnitude 2^-100 or more exactly (bf16 has fp32's exponent range: no clamp, the -1e30 padding floor
+    included), and smaller ones within 2^-126 (the third piece then falls among bf16's subnormals); a plausible
+    slip, a piece dropped, is caught."""
     rng = np.random.default_rng(5)
-    for scale in (1e-30, 1e-9, 1e-3, 0.3, 1.0, 7.3e2, 6.1e4, 1e7, 3e8):
+    b = fold_b_operand()[0, :3]
+    for scale in (1e-35, 1e-29, 1e-9, 1e-3, 0.3, 1.0, 7.3e2, 6.1e4, 1e7, 3e8, 1.3e9, 4e12, 1e30):
         v = (rng.normal(size=200_000) * scale).astype(np.float32)
-        v = v[np.abs(v) <= FOLD_MAX]
         q0, q1, q2 = fold_split(v)
         for q in (q0, q1, q2):
-            assert np.all(np.isfinite(q)) and np.all(np.abs(q) <= 65504)
-        back = q0.astype(np.float64) * FOLD_SCALES[0] + q1.astype(np.float64) * FOLD_SCALES[1] \
-            + q2.astype(np.float64) * FOLD_SCALES[2]
-        err = np.abs(back - v.astype(np.float64))
-        assert err.max() <= 2.0 ** -32, (scale, err.max())
-        big = np.abs(v) >= 2.0 ** -8
+            assert np.all(np.isfinite(q)) and np.all((q.view(np.uint32) & 0xFFFF) == 0)
+        back = q0.astype(np.float64) * b[0] + q1.astype(np.float64) * b[1] + q2.astype(np.float64) * b[2]
+        big = np.abs(v) >= 2.0 ** -100
         np.testing.assert_array_equal(back[big], v[big].astype(np.float64))
-    q0, q1, q2 = fold_split(np.array([-1e30, 1e30, 2.0 ** 30, -3e9], dtype=np.float32))
-    back = q0.astype(np.float64) * FOLD_SCALES[0] + q1 * FOLD_SCALES[1] + q2 * FOLD_SCALES[2]
-    np.testing.assert_array_equal(back, [-2.0 ** 30, 2.0 ** 30, 2.0 ** 30, -2.0 ** 30])
-    # a plausible slip, the middle scale off by one binade, is caught
+        assert np.abs(back - v.astype(np.float64)).max() <= 2.0 ** -126
+    edge = np.array([-1e30, 2.0 ** 30, -3e9, 3.0e38], dtype=np.float32)
+    q0, q1, q2 = fold_split(edge)
+    np.testing.assert_array_equal(q0.astype(np.float64) + q1 + q2, edge.astype(np.float64))
     v = (rng.normal(size=1000) * 100).astype(np.float32)
     q0, q1, q2 = fold_split(v)
-    wrong = q0.astype(np.float64) * 2.0 ** 15 + q1 * 2.0 ** 5 + q2 * 2.0 ** -7
-    assert np.abs(wrong - v).max() > 1e-3
+    assert np.abs((q0.astype(np.float64) + q1) - v).max() > 1e-4
+
+
+def _half_step_lse_f64(x, y, col):
+    """float64 L_i = (eps / 2) LSE_j((2 x_i.y_j + gh_j) / eps + log b_j) = LSE in accumulator units
+    (a_ij = x_i.y_j + col_j, col_j = (gh_j + eps log b_j) / 2) with c = (2 / eps) log2(e): returned for the
+    caller's c as max_j a_ij + log2(sum_j 2^(c (a_ij - max))) / c."""
+    a = x.astype(np.float64) @ y.astype(np.float64).T + col[None, :]
+    mx = a.max(axis=1)
+    return mx, a
+
+
+@pytest.mark.parametrize("case", ["tiny", "mixed"])
+def test_folded_column_terms_cover_small_and_mixed_scale_clouds(case):
+    """Regression for the folded column term's range: clouds at 1e-4 scale (d 16, 500 x 500: every cloud scale
+    2^16, so sigma = 2^32 and eps log b / 2 = -0.31 becomes -1.3e9 in kernel units) and mixed scales (x at 2e-7,
+    y ~ N(0, 1), gh ~ -|y|^2: sigma = 2^27, sigma |gh| / 2 ~ 6e9), normalize=False, m not a multiple of 32. The bf16 fold
+    gives the float64 log-sum-exp; the earlier fp16 fold, clamped at +-2^30, loses every column's identity."""
+    rng = np.random.default_rng(11)
+    eps = 0.1
+    c = np.float32(2.0 / eps * np.log2(np.e))
+    if case == "tiny":
+        n, m, d = 500, 500, 16
+        x = (rng.normal(size=(n, d)) * 1e-4).astype(np.float32)
+        y = (rng.normal(size=(m, d)) * 1e-4).astype(np.float32)
+        gh = np.zeros(m)
+    else:
+        n, m, d = 300, 470, 64
+        x = (rng.normal(size=(n, d)) * 2e-7).astype(np.float32)
+        y = rng.normal(size=(m, d)).astype(np.float32)
+        gh = -(y.astype(np.float64) ** 2).sum(1) + rng.normal(scale=0.05, size=m)
+    log_b = np.log(rng.uniform(0.5, 1.5, m) / m)
+    mp = pad_points(m)
+    col = np.full(mp, 0.5 * eps * -1e9)                       # padding: gh 0, log weight -1e9
+    col[:m] = 0.5 * (gh + eps * log_b)
+    col32 = col.astype(np.float32)
+    mx, a = _half_step_lse_f64(x, y, col32[:m].astype(np.float64))
+    want = mx + np.log2(np.exp2(c * (a - mx[:, None])).sum(1)) / c
+    sx = pack_scale(np.abs(x).max())
+    sy = pack_scale(np.abs(y).max())
+    assert np.abs(col32[:m]).max() * sx * sy > 2.0 ** 30        # the terms the fp16 fold had to clamp
+    got, _ = emulate_lse(x, y, col=col32, c=c, contraction="f16x2")
+    # (eps / 2) of a float32 half-step's rounding: the float32 scores' ulp, c |a| 2^-24, in accumulator units
+    tol = 4 * np.abs(a).max() * 2.0 ** -24 + 1e-12
+    assert np.abs(got - want).max() <= tol, (np.abs(got - want).max(), tol)
+    bad, _ = emulate_lse(x, y, col=col32, c=c, contraction="f16x2", fold_rule=(fp16_fold_split, fp16_fold_b_operand))
+    assert np.abs(bad - want).max() > 1e3 * tol

@@ -63,6 +63,55 @@ def test_published_float64_cost_10k():
     assert abs(r.cost - pub["cost_float64"]) <= 1e-12 * abs(pub["cost_float64"]), r.cost
 
 
+@pytest.mark.slow
+def test_published_float32_cost_10k():
+    """The same problem in float32 (preset "cpu-float32"): the reference's float32 runs converged in 20
+    iterations with costs 0.8971549341961733 (torch), 0.8971549319624892 (NKI, 1 core), 0.8971549320295445
+    (NKI, 2 cores) and final errors 5.8e-8, 5.2e-8, 6.2e-8 (results/sinkhorn_trn1.2xlarge_2026-10-30.csv:5,10,17):
+    all within 1.2e-8 relative of the float64 cost. The float32 oracle (another BLAS, another summation order)
+    must land in that band: 20 iterations, cost within 1.5e-8 of both the float64 and the float32 torch cost,
+    final error of the same order."""
+    pub = _published()["mixture_10k_eps0.05"]
+    x = data.mixture(10_000, 64, k=20, seed=0)
+    y = data.mixture(10_000, 64, k=20, seed=1, shift=0.3)
+    r = ref.sinkhorn_ref(x, y, eps=0.05, tol=1e-4, max_iters=2000, block=2048, dtype=torch.float32)
+    assert r.converged and r.iterations == pub["iterations"]
+    c64, c32 = pub["cost_float64"], pub["cost_float32_torch"]
+    assert abs(c32 - c64) <= 1.5e-8 * c64 and abs(pub["cost_float32_nki"] - c64) <= 1.5e-8 * c64
+    assert abs(r.cost - c64) <= 1.5e-8 * c64, r.cost
+    assert abs(r.cost - c32) <= 1.5e-8 * c64, r.cost
+    assert pub["error_float32_nki"] / 3 <= r.error <= pub["error_float32_torch"] * 3, r.error
+
+
+def test_eps_schedule_closed_form():
+    """The eps_start schedule (src/trnopt/sinkhorn.py:313-320) against its closed form, not against itself:
+    eps_start decay^k for k = 0, 1, ... while the value exceeds eps (strictly), at most max_iters values;
+    eps_stages above eps replace it. Both the oracle's and the product's (trnopt.sinkhorn._prepare) schedules.
+    A schedule that kept the first value <= eps, or started at eps_start decay, fails here."""
+    from trnopt.sinkhorn import SinkhornOptions, _prepare
+    x, y = data.clouds(n=20, m=15, d=3, seed=1)
+
+    def product(eps, max_iters, eps_start, decay, stages=None):
+        p = _prepare(x, y, None, None, SinkhornOptions(eps=eps, max_iters=max_iters, eps_start=eps_start,
+                                                       eps_decay=decay, eps_stages=stages), None, None)
+        return p.sched, p.stages
+
+    for sched_fn in (ref.eps_schedule, product):
+        sched, stages = sched_fn(0.05, 100, 1.0, 0.7)
+        assert stages == [] and len(sched) == 9                      # 0.7^8 = 0.0576 > 0.05 > 0.7^9 = 0.0404
+        np.testing.assert_allclose(sched, [0.7 ** k for k in range(9)], rtol=1e-15, atol=0)
+        assert sched_fn(0.25, 100, 1.0, 0.5) == ([1.0, 0.5], [])     # 0.25 = eps exactly: not scheduled
+        sched, _ = sched_fn(0.05, 5, 1.0, 0.7)                       # the max_iters cap
+        np.testing.assert_allclose(sched, [0.7 ** k for k in range(5)], rtol=1e-15, atol=0)
+        assert sched_fn(0.05, 100, 0.05, 0.7) == ([], [])            # eps_start not above eps
+        assert sched_fn(0.05, 100, None, 0.7) == ([], [])
+        assert sched_fn(0.05, 100, 1.0, 0.7, (1.0, 0.5, 0.05, 0.01)) == ([], [1.0, 0.5])
+        sched, _ = sched_fn(0.01, 1000, 2.0, 0.8)
+        k = np.arange(len(sched))
+        np.testing.assert_allclose(sched, 2.0 * 0.8 ** k, rtol=1e-14, atol=0)
+        assert sched[-1] > 0.01 >= sched[-1] * 0.8 and len(sched) == int(np.ceil(np.log(0.01 / 2.0) / np.log(0.8)))
+
+
 def test_published_float64_cost_needs_reference_init():
     """The same solve's first iterate from g0 = |y|^2 (the reference's init) differs from g0 = 0 (the
     reference's test oracle's init): the fixed-iteration workloads depend on the distinction."""

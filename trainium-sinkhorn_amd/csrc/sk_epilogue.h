@@ -14,10 +14,33 @@
 namespace sk {
 
 constexpr float kDeltaCap = 50.0f;     // cap of (g_old - g_new) / eps in the balanced check (sinkhorn.py:60)
-constexpr int kMergeBatch = 16;        // partial slots a merging thread loads at once (their latencies overlap)
+constexpr int kMergeBatch = 16;
+constexpr double kLog2eD = 1.4426950408889634074;   // log2(e) in double
+constexpr double kLn2D = 0.69314718055994530942;     // ln(2) in double        // partial slots a merging thread loads at once (their latencies overlap)
 
 __device__ __forceinline__ float ep_ex2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float ep_lg2(float x) { return __builtin_amdgcn_logf(x); }
+
+// log2 S of a row's merged sum of exponentials (S >= 1: the row's largest term is exactly 1), as an exact
+// integer part e plus log2 m: the caller adds them in double. The hardware log2 (v_log_f32) truncates instead of
+// rounding: on gfx950 its mean error is -0.47 ulp of the result, i.e. about -2e-7 for S near 2^6 and -9e-7 near
+// 2^20. Applied to S directly, that biases every half-step's log-sum-exp low by eps ln2 times as much,
+// differently in the f and g updates (their rows' S differ), which offsets the cost of a balanced problem (1.6e-8
+// of it on the 10k x 10k d 64 mixture clouds at eps 0.05). The exponent is split off exactly and the hardware
+// log2 takes only the mantissa, centred on 1, so its error is at most one ulp of a number below 1/2 (2^-25).
+struct Log2Split {
+    int e;
+    float lm;        // log2 m, m in [sqrt(1/2), sqrt(2))
+};
+__device__ __forceinline__ Log2Split lse_log2(float S) {
+    int e;
+    float m = frexpf(S, &e);                   // S = m 2^e, m in [1/2, 1)
+    if (m < 0.70710678f) {
+        m *= 2.0f;                              // exact
+        e -= 1;
+    }
+    return {e, ep_lg2(m)};
+}
 
 // Device-scope relaxed atomic accesses (coherent between workgroups on different XCDs within a launch).
 __device__ __forceinline__ float2 coh_load(const float2* p) {
@@ -187,24 +210,36 @@ __device__ inline bool merge_group(const PartialArgs& a, int g) {
             M = Mn;
             S = Sn;
         }
-        const float l2s = ep_lg2(S);
+        // The row's log-sum-exp and the epilogue in double, rounded once: f may be far smaller than the max score
+        // and the log of the sum it is the difference of (clouds far from unit scale under normalize=False), so
+        // each float rounding of those would cost f relative precision.
+        const Log2Split ls = lse_log2(S);
+        const double l2s = (double)ls.e + (double)ls.lm;
         if (a.mode == kHalfStep) {
-            const float eps = sc2, kappa = sc3;
+            const double kappa = sc3, x2d = x2, od = o;
             float val;
+            // fh = kappa (|x|^2 + eps off - eps lse) - |x|^2 (src/trnopt/sinkhorn.py:119) is evaluated as
+            //     fh = kappa (eps off - eps lse) + (kappa - 1) |x|^2,
+            // the same number in the mathematics (kappa - 1 is exact), rounded at fh's own magnitude. Rounded the
+            // reference's way, the state fh = f - |x|^2 is carried on the grid of f (|x|^2 - eps lse rounded at
+            // |x|^2's magnitude, then |x|^2 subtracted exactly): a coarser quantisation that, iterated, pushes
+            // the balanced potentials along their neutral mode (f + t, g - t) by a fraction of f's ulp per
+            // iteration (2e-8 on the 10k x 10k d 64 mixture clouds at eps 0.05, whose f is near 0.4; the
+            // reference's float32 sequence drifts the same way, less), which shows as a floor of the balanced
+            // error (4.5e-7 there) and an offset of the cost. For kappa = 1 and no offset it is -eps lse, exact.
             if (l2 && a.out2 != nullptr) {
                 // In log2 units, R = (c / 2) fh (the loop's state): (c / 2) eps lse = M + log2 S exactly in the
-                // mathematics, so R = kappa ((X2 + O) - (M + log2 S)) - X2 with X2 = (c / 2) |x|^2 and
-                // O = log2(e) off: sums only, as the accumulator-unit form below, and fh = R / (c / 2).
-                const float k2 = 0.5f * c_hs;
-                const float X2 = x2 * k2;
-                const float val2 = kappa * ((X2 + o * kLog2e) - (M + l2s)) - X2;
-                val = __fdiv_rn(val2, k2);
-                if (i < a.n_store) st<COH>(a.out2 + i, val2);
+                // mathematics, so R = kappa (O - (M + log2 S)) + (kappa - 1) X2 with X2 = (c / 2) |x|^2 and
+                // O = log2(e) off, and fh = R / (c / 2), each rounded once from the double.
+                const double k2 = 0.5 * (double)c_hs;
+                const double R = kappa * (od * (double)kLog2eD - ((double)M + l2s)) + (kappa - 1.0) * (x2d * k2);
+                val = (float)(R / k2);
+                if (i < a.n_store) st<COH>(a.out2 + i, (float)R);
             } else {
-                // the max enters exactly, in accumulator units (log2-unit slots: M / c, correctly rounded)
-                const float Ma = l2 ? __fdiv_rn(M, c_hs) : M;
-                const float eps_lse = 2.0f * Ma + (eps * kLn2) * l2s;
-                val = kappa * ((x2 + eps * o) - eps_lse) - x2;
+                // eps lse = 2 M + eps ln(S) in accumulator units (log2-unit slots: M / c), with the caller's eps
+                // (float) as the reference's epilogue multiplies by it (src/trnopt/sinkhorn.py:119)
+                const double eps_lse = 2.0 * (l2 ? (double)M / (double)c_hs : (double)M) + (double)sc2 * kLn2D * l2s;
+                val = (float)(kappa * ((double)sc2 * od - eps_lse) + (kappa - 1.0) * x2d);
             }
             if (a.meas != nullptr) {
                 if (i < a.n_real) dmax = fabsf(val - old);
@@ -213,7 +248,7 @@ __device__ inline bool merge_group(const PartialArgs& a, int g) {
             }
             if (i < a.n_store) st<COH>(a.out + i, val);
         } else if (i < a.n_store) {
-            st<COH>(a.out + i, M + kLn2 * l2s);
+            st<COH>(a.out + i, (float)((double)M + l2s / (double)kLog2e));   // natural log: l2s / c, c = log2(e)
         }
     }
     if (a.meas != nullptr) {

@@ -11,7 +11,7 @@
 //
 // the score is c a_ij in log2 units. x_i . y_j is accumulated by fp16 MFMAs from a two-piece fp16 split of
 // the power-of-two scaled fp32 coordinates (sk_lse_partial.hip), bit-identical in the f and g updates; the
-// column term is added after it (by one more MFMA for kp <= 64, on the VALU above). The running (max, sum) of a
+// column term is added after it (for kp <= 64 by one more MFMA, as three exact bf16 pieces; on the VALU above). The running (max, sum) of a
 // row is kept as
 //
 //     eps * lse_i = 2 M_i + eps ln(2) log2 S_i,   S_i = sum_j exp2(c (a_ij - M_i)),  M_i = max_j a_ij,
@@ -91,7 +91,6 @@ using namespace sk;
 constexpr float kMaskOut = -1.0e30f;   // column term of a padding column in the plain row-LSE mode
 
 __device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
-__device__ __forceinline__ float lg2(float x) { return __builtin_amdgcn_logf(x); }
 
 // ---------------------------------------------------------------------------------------------------
 // Pack a row-major (n, d) cloud into the tile-interleaved layout.

@@ -32,9 +32,10 @@
 // product of the two scales in both directions): `rows_role` says
 // whether the rows are the first or the second cloud, and the pair list is transposed accordingly. The
 // contraction starts from zero and the column term is added afterwards: by one more MFMA per row block and
-// tile in the streamed fp16 variant (the term as three fp16 pieces against (2^15, 2^4, 2^-7), exact for
-// terms in [-2^30, 2^30], clamped beyond; 32 VALU adds per tile fewer), on the VALU otherwise. The max is
-// subtracted before scaling, exp2(c (a - M)), so the dominant term is exactly 1.
+// tile in the streamed fp16 variant (the fp32 term split exactly into three bf16 pieces, summed against
+// B = (1, 1, 1): exact for every fp32 value, since bf16 has fp32's exponent range; 32 VALU adds per tile
+// fewer), on the VALU otherwise. The max is subtracted before scaling, exp2(c (a - M)), so the dominant term
+// is exactly 1.
 //
 // Layout of one workgroup (4 waves, one per SIMD of a CU): wave w owns kRowBlocks blocks of 32 rows of a
 // row group (its fp16 pieces stay in registers for the whole work segment), and all four waves walk the same
@@ -219,7 +220,9 @@ __device__ __forceinline__ void store_rows(const PartialArgs& a, const float (&M
                             : S[b] * ex2(c * (M[b] - Mn)) + So * ex2(c * (Mo - Mn));
         if (lane < 32 && rb0 + b < a.nrb) {
             float2* dst = a.part + (size_t)slot * a.rows_pad + (size_t)(rb0 + b) * 32 + lane;
-            const float2 v = make_float2(L2 ? Mn : Mn * inv_sigma, Sn);
+            // (a segment whose columns all have zero weight has M near the -1e30 floor; kept finite when
+            // rescaled, as an empty slot)
+            const float2 v = make_float2(L2 ? Mn : fmaxf(Mn * inv_sigma, kEmpty), Sn);
             if (a.group_counters != nullptr)
                 coh_store(dst, v);           // read back in this launch by the group's last workgroup
             else
@@ -377,7 +380,6 @@ struct Staged {
 constexpr int col_tiles(bool fold) { return fold ? 192 : 256; }
 constexpr int col_floats(bool fold) { return fold ? col_tiles(fold) * 32 * 4 : (col_tiles(fold) + 1) * 32; }
 constexpr int kColBatch = 8;
-constexpr float kFoldMax = 0x1p30f;   // column terms beyond +-2^30 (kernel units) are clamped with FOLD
 constexpr int kStreamMaxChunks = 4;
 
 template <int NC, int ROLE, int CT, bool L2>
@@ -422,8 +424,9 @@ struct Streamed {
 
         // Column terms into LDS, tile t at (t - cbase) * 32. Without FOLD: tiles [t0 - 1, t1), one float per
         // column (the update of tile t0 - 1 still runs while tile t0's MFMAs do). With FOLD: tiles [t0, t1), each
-        // column term q clamped to [-2^30, 2^30] and stored as the A operand of one MFMA, eight fp16 values
-        // (q0, q1, q2, 0, ...) with q = q0 2^15 + q1 2^4 + q2 2^-7 (exact: each piece takes the next 11 bits).
+        // column term q stored as the A operand of one bf16 MFMA, eight bf16 values (q0, q1, q2, 0, ...) with
+        // q = q0 + q1 + q2 exactly (each piece the nearest bf16 to what the previous ones leave: 8 + 8 + 8
+        // significand bits, all of fp32's; bf16 has fp32's exponent range, so no term is out of range).
         int cbase = tb - 1;
         auto stage_cols = [&](int t0, int t1) {
             __syncthreads();
@@ -445,12 +448,11 @@ struct Streamed {
                     if (k < n && j >= 0) {
                         const float v = fmaxf(cs * fmaf(beta, vv[q], alpha * uu[q]), kPadScore);
                         if constexpr (FOLD) {
-                            const float w = fminf(fmaxf(v, -kFoldMax), kFoldMax) * 0x1p-15f;   // exact scaling
-                            const _Float16 q0 = (_Float16)w;
-                            const float r1 = (w - (float)q0) * 0x1p11f;
-                            const _Float16 q1 = (_Float16)r1;
-                            const _Float16 q2 = (_Float16)((r1 - (float)q1) * 0x1p11f);
-                            reinterpret_cast<f16x8*>(lds_col)[k] = f16x8{q0, q1, q2, 0, 0, 0, 0, 0};
+                            const __bf16 q0 = (__bf16)v;
+                            const float r1 = v - (float)q0;                 // exact
+                            const __bf16 q1 = (__bf16)r1;
+                            const __bf16 q2 = (__bf16)(r1 - (float)q1);     // exact: at most 8 bits remain
+                            reinterpret_cast<bf16x8*>(lds_col)[k] = bf16x8{q0, q1, q2, 0, 0, 0, 0, 0};
                         } else {
                             lds_col[k] = v;
                         }
@@ -469,18 +471,17 @@ struct Streamed {
         };
         auto colp_of = [&](int t) { return lds_col + (t - cbase) * 32 + 4 * h; };
         // With FOLD, the A operand of tile t's column MFMA (lane l: column l % 32; lanes 32-63 meet zeros in B)
-        // and the B operand (2^15, 2^4, 2^-7 in k = 0, 1, 2 of every row, zeros elsewhere).
-        auto colA_of = [&](int t) { return reinterpret_cast<const f16x8*>(lds_col)[(t - cbase) * 32 + (lane & 31)]; };
-        const _Float16 e0 = h == 0 ? (_Float16)0x1p15f : (_Float16)0, e1 = h == 0 ? (_Float16)0x1p4f : (_Float16)0,
-                       e2 = h == 0 ? (_Float16)0x1p-7f : (_Float16)0;
-        const f16x8 colB = {e0, e1, e2, 0, 0, 0, 0, 0};
+        // and the B operand (1 in k = 0, 1, 2 of every row, zeros elsewhere): the MFMA adds q0 + q1 + q2 = q.
+        auto colA_of = [&](int t) { return reinterpret_cast<const bf16x8*>(lds_col)[(t - cbase) * 32 + (lane & 31)]; };
+        const __bf16 one = h == 0 ? (__bf16)1.0f : (__bf16)0.0f;
+        const bf16x8 colB = {one, one, one, 0, 0, 0, 0, 0};
 
         f32x16 accA[RB], accB[RB];
         Online<RB, L2, FOLD> on;
         auto tile = [&](f32x16 (&accN)[RB], f32x16 (&accP)[RB], const float* colp, const T (&yv)[NC][kPieces],
                         int t, bool epi) {
             auto col4 = [&](int q) { return *reinterpret_cast<const f32x4*>(colp + 8 * q); };
-            f16x8 colA;
+            bf16x8 colA;
             if constexpr (FOLD) colA = colA_of(t);
 #pragma unroll
             for (int b = 0; b < RB; ++b) accN[b] = f32x16{};
@@ -500,7 +501,7 @@ struct Streamed {
             if constexpr (FOLD) {
 #pragma unroll
                 for (int b = 0; b < RB; ++b)
-                    accN[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(colA, colB, accN[b], 0, 0, 0);
+                    accN[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(colA, colB, accN[b], 0, 0, 0);
             }
         };
         auto update = [&](f32x16 (&accP)[RB], const float* colp) {

@@ -22,6 +22,7 @@ import shutil
 import subprocess
 import sys
 import tempfile
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 PKG = Path(__file__).resolve().parent
@@ -59,12 +60,16 @@ def build(verbose: bool = False) -> Path:
     cc = hipcc()
     LIB_DIR.mkdir(parents=True, exist_ok=True)
     with tempfile.TemporaryDirectory(prefix="trnopt_build_") as tmp:
-        objs = []
+        cmds, objs = [], []
         for src, name, extra in UNITS:
             obj = Path(tmp) / (name + ".o")
-            cmd = [cc, *COMMON, *extra, "-c", str(CSRC / src), "-o", str(obj)]
-            _run(cmd, verbose)
+            cmds.append([cc, *COMMON, *extra, "-c", str(CSRC / src), "-o", str(obj)])
             objs.append(str(obj))
+        # the translation units compile independently: one hipcc process each, at most MAX_JOBS at once
+        jobs = max(1, min(len(cmds), int(os.environ.get("MAX_JOBS", "") or os.cpu_count() or 1)))
+        with ThreadPoolExecutor(max_workers=jobs) as ex:
+            for f in [ex.submit(_run, c, verbose) for c in cmds]:
+                f.result()
         out_tmp = Path(tmp) / LIB_NAME
         _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", str(out_tmp)], verbose)
         # Replace atomically so a process that has the old library mapped keeps a valid file.

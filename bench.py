@@ -1,30 +1,32 @@
 """Benchmark: ms per Sinkhorn iteration (f half-step + g half-step) on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-    python bench.py --profile [--reps R]     # for rocprofv3: R half-steps, then a 256 MiB copy
+    python bench.py --profile [--reps R]     # for rocprofv3: R loop iterations, then a 256 MiB copy
     python bench.py --workload {single-cell, single-cell-pipeline, stress-65k} [--no-cpu]
 
 Workload: synthetic balanced 10,000 x 10,000, d = 64, fp32, x ~ N(0, 1) (seed 0), y ~ N(0, 1) + 0.5
 (seed 1), uniform weights, squared-Euclidean cost, no normalisation, eps = 0.1 (the reference's
 examples/sinkhorn_benchmark.py --flashsinkhorn setup). A "step" is one iteration of the on-device loop
-(f half-step, g half-step, loop control: two kernel launches, the partial kernels merging their row groups),
-inputs resident in HBM. W untimed iterations, then
-exactly K timed iterations between two device synchronisations (defaults 100 and 200: the first ~100 iterations
-of a process run ~8 % slower while the GPU's clocks settle).
+(f half-step, g half-step, loop control), inputs resident in HBM: two launches of the fused partial kernel
+(lse_partial_kernel), each merging its own row groups. W untimed iterations, then exactly K timed iterations
+between two device synchronisations (defaults 100 and 200: the first ~100 iterations of a process run ~8 %
+slower while the GPU's clocks settle).
 
 Also reported on the same JSON line:
-* roofline -- the dominant kernel pair, sk_half_step_f32 (lse_partial_kernel, then merge_kernel), timed with
-  HIP events on the stream it runs on. `achieved` is the algorithmic count 2 n m (d + 1) of one half-step
-  (the augmented fp32 contraction) per second, against the 157.3 TFLOP/s fp32 MFMA peak; `frac` exceeds 1
-  because the fp32-accurate contraction runs on the fp16 matrix pipe (three products of a two-piece split of
-  the coordinates). `mfma_f16` gives the executed fp16 MFMA work (3 x 2 x n_pad m_pad kp per half-step)
-  against the 2.5 PFLOP/s fp16 dense peak, `exp` the exponentials (n m per half-step) against the
-  9.83e12/s transcendental peak (quarter rate on 256 CUs x 4 SIMDs x 16 lanes at 2.4 GHz); `traffic` is the
-  fabric bytes per half-step from the committed counter summary;
-* iteration_roofline_frac -- max(4 n m (d + 1) / 157.3e12, 2 n m / 9.83e12) seconds over the measured
-  ms/iteration: the exp + fp32-MFMA roofline fraction the metric names;
+* roofline -- the dominant kernel, lse_partial_kernel (every launch of the timed region is one): its average
+  launch time from HIP events recorded on its stream around the timed region, divided by the 2 K launches.
+  The kernel forms the fp32-accurate contraction on the fp16 matrix pipe as three products of a two-piece
+  split of the coordinates, so `achieved` counts those fp16 MFMA FLOP (3 x 2 x n m kp per launch, padding
+  excluded) against the 2.5 PFLOP/s fp16 dense peak; `exp` gives the n m exponentials per launch against the
+  9.83e12/s transcendental peak (quarter rate, 256 CUs x 4 SIMDs x 16 lanes at 2.4 GHz), and `fp32_equivalent`
+  the algorithmic 2 n m (d + 1) per launch against the 157.3 TFLOP/s fp32 MFMA peak (a ratio above 1: the
+  contraction does not run on the fp32 pipe). `traffic` is the HBM bytes per launch from the committed
+  counter summary (FETCH_SIZE and WRITE_SIZE passes, scaled by a plain copy's readings);
+* iteration_roofline -- per iteration, max(executed fp16 MFMA FLOP / 2.5e15, 2 n m / 9.83e12) seconds over the
+  measured ms/iteration (the exp + MFMA roofline the metric names, on the pipe the kernel runs on), and beside
+  it the fp32-MFMA form max(4 n m (d + 1) / 157.3e12, 2 n m / 9.83e12) as a ratio;
 * cpu_baseline -- the reference's plain-PyTorch CPU path (the oracle's restatement, float32, block 2048,
-  all host cores) on a bounded sample of the same workload;
+  all host cores) on the same workload: best of 3 runs of 10 fixed iterations after 1 warm-up iteration;
 * end_to_end_s -- sinkhorn() wall time for 10 fixed iterations, host arrays in, float64 potentials out
   (setup, H2D, packing, loop, read-back).
 """
@@ -49,10 +51,10 @@ PRODUCTS = 3          # fp16 piece products per K chunk of the half-step contrac
 
 
 def profiled_traffic():
-    """Fabric bytes per half-step from the committed counter summary (FETCH_SIZE and WRITE_SIZE passes,
-    scaled by the copy calibration), or None if the summary is absent."""
+    """HBM bytes per launch of the dominant kernel from the committed counter summary (FETCH_SIZE and
+    WRITE_SIZE passes, scaled by the copy calibration), or None if the summary is absent."""
     import re
-    p = ROOT / "profiles" / "half_step_10k_d64_counters.md"
+    p = ROOT / "profiles" / "loop_10k_d64_counters.md"
     m = re.search(r"traffic_bytes_per_launch:\s*(\d+)", p.read_text()) if p.exists() else None
     return int(m.group(1)) if m else None
 
@@ -64,67 +66,8 @@ def make_inputs():
     return x, y
 
 
-def gpu_run(steps, warmup, kernel_reps=50):
-    import numpy as np
-    import torch
-    from trnopt import hip_sinkhorn as hk
-
-    hk.lib()
-    dev = torch.device("cuda", 0)
-    torch.cuda.set_device(dev)
-    x, y = make_inputs()
-    la, lb = np.full(N, -np.log(N)), np.full(M, -np.log(M))
-    X = hk.HipCloud(x, la, dev, role=0)
-    Y = hk.HipCloud(y, lb, dev, role=1)
-    loop = hk.DeviceLoop(X, Y, eps=EPS, rho_x=None, rho_y=None, sched=[], stages=[], tol=1e-4, stage_tol=1e-5,
-                         max_iters=warmup + steps + 1, check_every=10, stage_max_iters=1000, fixed_iters=True,
-                         balanced=True)
-    loop.init()
-    loop.capture()                       # with TRNOPT_HIP_GRAPH=1: the graph of a batch, before any timing
-    loop.enqueue(warmup)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    loop.enqueue(steps)
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    ms_per_it = (t1 - t0) * 1e3 / steps
-    st = loop.read_state()
-    assert st.it == warmup + steps and not st.done, (st.it, st.done)
-
-    # dominant kernel pair: one half-step (f update), HIP events on the current stream
-    sc = hk.scalars(EPS, 1.0, dev)
-    out = torch.empty(X.npad, dtype=torch.float32, device=dev)
-    for _ in range(3):
-        hk.half_step(X, Y, loop.gh, sc, out=out)
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    ev0.record()
-    for _ in range(kernel_reps):
-        hk.half_step(X, Y, loop.gh, sc, out=out)
-    ev1.record()
-    torch.cuda.synchronize()
-    half_ms = ev0.elapsed_time(ev1) / kernel_reps
-    flop = 2.0 * N * M * (D + 1)
-    achieved = flop / (half_ms * 1e-3)
-    executed = PRODUCTS * 2.0 * X.npad * Y.npad * hk.pad_dim(D)
-
-    # end to end: sinkhorn() with host arrays, 10 fixed iterations
-    from trnopt import Backend, SinkhornOptions, sinkhorn
-    o = SinkhornOptions(eps=EPS, normalize=False, max_iters=10, fixed_iters=True, kernel="hip",
-                        backend=Backend.preset("rocm"))
-    sinkhorn(x, y, opts=o)
-    torch.cuda.synchronize()
-    te = time.perf_counter()
-    r = sinkhorn(x, y, opts=o)
-    e2e = time.perf_counter() - te
-    return dict(ms_per_it=ms_per_it, half_ms=half_ms, achieved=achieved, flop=flop, executed=executed, e2e=e2e,
-                loop_s=r.seconds)
-
-
-def profile_run(reps):
-    """What the rocprofv3 summaries are taken from: `reps` half-steps (f update) of the workload, then one
-    plain device copy of 256 MiB (two copy dispatches of 128 MiB), whose FETCH_SIZE / WRITE_SIZE calibrate the
-    counters (each dispatch reads and writes exactly 131072 KiB)."""
+def _loop(n_iters):
+    """The benchmark's on-device loop, initialised (x's log2-unit copy made, the state written)."""
     import numpy as np
     import torch
     from trnopt import hip_sinkhorn as hk
@@ -135,23 +78,74 @@ def profile_run(reps):
     x, y = make_inputs()
     X = hk.HipCloud(x, np.full(N, -np.log(N)), dev, role=0)
     Y = hk.HipCloud(y, np.full(M, -np.log(M)), dev, role=1)
-    gh = torch.zeros(Y.npad, dtype=torch.float32, device=dev)
-    sc = hk.scalars(EPS, 1.0, dev)
-    hk.bake_log2(X, Y, sc)               # as the loop does: scores in log2 units from the matrix cores
-    out = torch.empty(X.npad, dtype=torch.float32, device=dev)
-    for _ in range(reps):
-        hk.half_step(X, Y, gh, sc, out=out)
-    src = torch.ones(64 << 20, dtype=torch.float32, device=dev)
+    loop = hk.DeviceLoop(X, Y, eps=EPS, rho_x=None, rho_y=None, sched=[], stages=[], tol=1e-4, stage_tol=1e-5,
+                         max_iters=n_iters, check_every=10, stage_max_iters=1000, fixed_iters=True, balanced=True)
+    loop.init()
+    return x, y, loop
+
+
+def gpu_run(steps, warmup):
+    import torch
+    from trnopt import hip_sinkhorn as hk
+
+    x, y, loop = _loop(warmup + steps + 1)
+    loop.capture()                       # with TRNOPT_HIP_GRAPH=1: the graph of a batch, before any timing
+    loop.enqueue(warmup)
+    stream = torch.cuda.current_stream()   # the stream every loop kernel is launched on
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    loop.enqueue(steps)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ms_per_it = (t1 - t0) * 1e3 / steps
+    kernel_ms = ev0.elapsed_time(ev1) / (2 * steps)     # two lse_partial_kernel launches per iteration
+    st = loop.read_state()
+    assert st.it == warmup + steps and not st.done, (st.it, st.done)
+
+    # end to end: sinkhorn() with host arrays, 10 fixed iterations
+    from trnopt import Backend, SinkhornOptions, sinkhorn
+    o = SinkhornOptions(eps=EPS, normalize=False, max_iters=10, fixed_iters=True, kernel="hip",
+                        backend=Backend.preset("rocm"))
+    sinkhorn(x, y, opts=o)
+    torch.cuda.synchronize()
+    te = time.perf_counter()
+    sinkhorn(x, y, opts=o)
+    e2e = time.perf_counter() - te
+    return dict(ms_per_it=ms_per_it, kernel_ms=kernel_ms, e2e=e2e, kp=hk.pad_dim(D))
+
+
+def profile_run(reps):
+    """What the rocprofv3 summaries are taken from: `reps` iterations of the benchmark's on-device loop (2 reps
+    launches of the dominant kernel), then one plain device copy of 256 MiB (two copy dispatches of 128 MiB),
+    whose FETCH_SIZE / WRITE_SIZE calibrate the counters (each dispatch reads and writes exactly 131072 KiB)."""
+    import torch
+    _, _, loop = _loop(reps + 1)
+    loop.enqueue(reps)
+    src = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
     dst = torch.empty_like(src)
     torch.cuda.synchronize()
     dst.copy_(src)
     torch.cuda.synchronize()
-    print(f"profile: {reps} half-steps of {N} x {M} d {D}, then a 256 MiB copy", flush=True)
+    print(f"profile: {reps} loop iterations of {N} x {M} d {D}, then a 256 MiB copy", flush=True)
 
 
-def cpu_baseline(iters=2):
+def _cpu_model():
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(iters=10, reps=3):
     """The reference's plain-PyTorch CPU path (oracle restatement), float32, block 2048, all host cores:
-    `iters` fixed iterations after one untimed warm-up iteration, best of 2."""
+    best of `reps` runs of `iters` fixed iterations, after one untimed warm-up iteration."""
     import torch
     sys.path.insert(0, str(ROOT))
     from oracle.reference import sinkhorn_ref
@@ -160,10 +154,11 @@ def cpu_baseline(iters=2):
     x, y = make_inputs()
     o = dict(eps=EPS, normalize=False, fixed_iters=True, block=2048, dtype=torch.float32)
     sinkhorn_ref(x, y, max_iters=1, **o)
-    best = min(sinkhorn_ref(x, y, max_iters=iters, **o).seconds for _ in range(2))
-    return dict(value=best * 1e3 / iters, unit="ms/iteration", cores=cores, kind="port",
-                sample=f"{iters} fixed iterations of the 10k x 10k d64 workload (block 2048), best of 2, "
-                       f"after 1 warm-up iteration; torch {torch.__version__} CPU float32")
+    best = min(sinkhorn_ref(x, y, max_iters=iters, **o).seconds for _ in range(reps))
+    return dict(value=round(best * 1e3 / iters, 3), unit="ms/iteration", cores=cores, kind="port",
+                sample=f"best of {reps} runs of {iters} fixed iterations of the 10k x 10k d64 workload (block 2048), "
+                       f"after 1 warm-up iteration; torch {torch.__version__} CPU float32 on {cores} threads of "
+                       f"{_cpu_model()}")
 
 
 # ---------------------------------------------------------------------------------------------------------
@@ -332,7 +327,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--cpu-iters", type=int, default=2)
+    ap.add_argument("--cpu-iters", type=int, default=10)
+    ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--profile", action="store_true", help="only the launches the rocprofv3 summaries use")
     ap.add_argument("--reps", type=int, default=20)
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default=None,
@@ -349,8 +345,15 @@ def main():
         print(json.dumps(WORKLOADS[a.workload](not a.no_cpu)), flush=True)
         return
     g = gpu_run(a.steps, a.warmup)
-    cpu = None if a.no_cpu else cpu_baseline(a.cpu_iters)
-    t_roof = max(4.0 * N * M * (D + 1) / MFMA_F32_PEAK, 2.0 * N * M / EXP_PEAK)
+    cpu = None if a.no_cpu else cpu_baseline(a.cpu_iters, a.cpu_reps)
+    kp = g["kp"]
+    t_launch = g["kernel_ms"] * 1e-3
+    executed = PRODUCTS * 2.0 * N * M * kp            # fp16 MFMA FLOP of one launch's contraction (no padding)
+    alg = 2.0 * N * M * (D + 1)                       # the augmented fp32 contraction of one half-step
+    exps = float(N * M)
+    t_it = g["ms_per_it"] * 1e-3
+    t_roof = max(2 * executed / MFMA_F16_PEAK, 2 * exps / EXP_PEAK)
+    t_roof32 = max(2 * alg / MFMA_F32_PEAK, 2 * exps / EXP_PEAK)
     line = {
         "metric": "ms/iteration, 10k x 10k d=64 fp32 Sinkhorn; fraction of exp+MFMA roofline",
         "value": round(g["ms_per_it"], 5),
@@ -366,16 +369,18 @@ def main():
         "data": "synthetic (seeded N(0,1) clouds, y shifted by 0.5)",
         "config": {"workload": "balanced Sinkhorn 10000 x 10000, d 64, eps 0.1, fixed iterations", "n": N, "m": M,
                    "d": D, "eps": EPS},
-        "roofline": {"bound": "mfma", "achieved": round(g["achieved"] / 1e12, 3), "peak": MFMA_F32_PEAK / 1e12,
-                     "unit": "TFLOP/s", "frac": round(g["achieved"] / MFMA_F32_PEAK, 4), "traffic": profiled_traffic(),
-                     "kernel": "sk_half_step_f32 (lse_partial_kernel + merge_kernel)",
-                     "kernel_ms": round(g["half_ms"], 5), "flop_per_launch": g["flop"],
-                     "mfma_f16": {"executed_flop_per_launch": g["executed"],
-                                  "achieved": round(g["executed"] / (g["half_ms"] * 1e-3) / 1e12, 1),
-                                  "peak": MFMA_F16_PEAK / 1e12,
-                                  "frac": round(g["executed"] / (g["half_ms"] * 1e-3) / MFMA_F16_PEAK, 4)},
-                     "exp": {"per_launch": N * M, "frac": round(N * M / (g["half_ms"] * 1e-3) / EXP_PEAK, 4)}},
-        "iteration_roofline_frac": round(t_roof * 1e3 / g["ms_per_it"], 4),
+        "roofline": {"bound": "mfma", "achieved": round(executed / t_launch / 1e12, 1), "peak": MFMA_F16_PEAK / 1e12,
+                     "unit": "TFLOP/s", "frac": round(executed / t_launch / MFMA_F16_PEAK, 4),
+                     "traffic": profiled_traffic(),
+                     "kernel": "lse_partial_kernel (fp16 MFMA three-product contraction, row groups merged in-kernel)",
+                     "kernel_ms": round(g["kernel_ms"], 5), "flop_per_launch": executed,
+                     "exp": {"per_launch": exps, "achieved": round(exps / t_launch / 1e12, 3), "peak": EXP_PEAK / 1e12,
+                             "unit": "Texp/s", "frac": round(exps / t_launch / EXP_PEAK, 4)},
+                     "fp32_equivalent": {"flop_per_launch": alg, "achieved": round(alg / t_launch / 1e12, 1),
+                                         "peak": MFMA_F32_PEAK / 1e12, "ratio": round(alg / t_launch / MFMA_F32_PEAK, 4)}},
+        "iteration_roofline": {"t_roof_ms": round(t_roof * 1e3, 5), "frac": round(t_roof / t_it, 4),
+                               "fp32_mfma_t_roof_ms": round(t_roof32 * 1e3, 5),
+                               "fp32_mfma_ratio": round(t_roof32 / t_it, 4)},
         "end_to_end_s": round(g["e2e"], 4),
         "cpu_baseline": cpu,
     }

@@ -166,3 +166,15 @@ def test_load_pair_refuses_other_files(tmp_path):
     np.savez(p, f=np.zeros(3))
     with pytest.raises(ValueError, match="not a pair file"):
         load_pair(p)
+
+
+def test_wot_eps_stages_closed_form():
+    """wot's stage schedule (src/trnopt/singlecell.py:46-50) against its closed form: eps0 eps^(e / scalings) for
+    e = 0 .. scalings - 1 (sf = eps^(-1 / scalings)), so 1, 0.5493, 0.3017, 0.1657, 0.0910 at eps 0.05."""
+    from trnopt.singlecell import wot_eps_stages
+    st = wot_eps_stages(0.05)
+    np.testing.assert_allclose(st, [0.05 ** (e / 5) for e in range(5)], rtol=1e-14)
+    np.testing.assert_allclose(st, [1.0, 0.5493, 0.3017, 0.1657, 0.0910], atol=5e-5)
+    np.testing.assert_allclose(wot_eps_stages(0.01, eps0=2.0, scalings=4), [2.0 * 0.01 ** (e / 4) for e in range(4)],
+                               rtol=1e-14)
+    assert all(e > 0.05 for e in st)           # every stage lies above the final eps: the solver keeps them all

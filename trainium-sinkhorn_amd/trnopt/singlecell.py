@@ -2,8 +2,8 @@
 
 The interface of the reference's src/trnopt/singlecell.py (wot, Schiebinger et al. 2019, OTModel defaults):
 
-* local_pca_coords: per pair, PCA of both time points' centred expression (sklearn PCA on the transpose),
-  components scaled by the singular values (wot.ot.compute_pca + compute_default_cost_matrix);
+* input: each time point's cells in a per-pair embedding (the reference computes it with sklearn PCA from the
+  expression data, src/trnopt/singlecell.py:30-43; that step needs the data and is left to the caller);
 * cost: squared Euclidean distance divided by its median (normalize="median"), computed once per pair;
 * formulation: uniform reference (1/I, 1/J), row target G / I (the cells' growth), column target
   mean(G) / J, KL penalties (lambda1, lambda2), entropy eps;
@@ -30,20 +30,6 @@ from .sinkhorn import (SinkhornOptions, SinkhornResult, _gpu_device, _use_hip, n
 
 PAIR_KEYS = ("f", "g", "eps", "center", "cost_scale", "row_mass", "col_mass", "learned_growth", "cells0",
              "cells1", "x0", "x1")
-
-
-def local_pca_coords(X0, X1, n_components: int = 30) -> tuple[np.ndarray, np.ndarray]:
-    """wot's per-pair embedding (src/trnopt/singlecell.py:30-43): (cells0 x k, cells1 x k)."""
-    import scipy.sparse as sp
-    from sklearn.decomposition import PCA
-    a = X0.toarray() if sp.issparse(X0) else np.asarray(X0)
-    b = X1.toarray() if sp.issparse(X1) else np.asarray(X1)
-    both = np.vstack([a, b]).astype(np.float64)
-    both -= both.mean(axis=0)
-    k = min(n_components, both.shape[0])
-    pca = PCA(n_components=k, random_state=58951).fit(both.T)
-    coords = pca.components_.T * pca.singular_values_[None, :]
-    return coords[:len(a)], coords[len(a):]
 
 
 def wot_eps_stages(eps: float, eps0: float = 1.0, scalings: int = 5) -> tuple:

@@ -160,9 +160,12 @@ __device__ inline void set_scalars(sk_state* st, double e, double rho_x, double 
 // loop only when the iteration's control will run: the callers drop meas otherwise).
 // Returns false, storing nothing, when the loop is done (*skip != 0): the flag is loaded with the launch's other
 // scalars and the row's first slots, and tested once they have arrived. COH: the slots were written in this
-// launch by other workgroups, and the results (out, out2, meas) are read back in it (the loop control).
-template <bool COH>
+// launch by other workgroups, and the results (out, out2, meas) are read back in it (the loop control). NT: the
+// workgroup's threads (kRowsPerGroup or more: threads past the group's rows take part in its barriers only).
+template <bool COH, int NT>
 __device__ inline bool merge_group(const PartialArgs& a, int g) {
+    static_assert(NT >= kRowsPerGroup && NT % 64 == 0, "one thread per row of the group");
+    const bool live = tid_x() < kRowsPerGroup;
     const int i = g * kRowsPerGroup + tid_x();
     const int* skip_p = a.skip != nullptr ? a.skip : &kNoSkip;
     const float sc0 = a.sc[0], sc1 = a.sc[1], sc2 = a.sc[2], sc3 = a.sc[3];   // valid in both modes
@@ -191,7 +194,7 @@ __device__ inline bool merge_group(const PartialArgs& a, int g) {
     const float c = l2 ? 1.0f : a.mode == kHalfStep ? c_hs : kLog2e;
     float dmax = 0.0f;
     double derr = 0.0;
-    if (i < a.rows_pad) {
+    if (live && i < a.rows_pad) {
         // One pass, online: (M, S) <- (max(M, m_k), S 2^(c (M - M')) + s_k 2^(c (m_k - M'))), slots loaded
         // kMergeBatch at a time so that their latencies overlap.
         float M = kEmpty, S = 0.0f;
@@ -257,8 +260,8 @@ __device__ inline bool merge_group(const PartialArgs& a, int g) {
             dmax = fmaxf(dmax, __shfl_xor(dmax, o));
             derr += __shfl_xor(derr, o);
         }
-        __shared__ float smax[kRowsPerGroup / 64];
-        __shared__ double ssum[kRowsPerGroup / 64];
+        __shared__ float smax[NT / 64];
+        __shared__ double ssum[NT / 64];
         const int wv = tid_x() >> 6;
         if ((tid_x() & 63) == 0) {
             smax[wv] = dmax;
@@ -268,7 +271,7 @@ __device__ inline bool merge_group(const PartialArgs& a, int g) {
         if (tid_x() == 0) {
             float mx = smax[0];
             double sm = ssum[0];
-            for (int k = 1; k < kRowsPerGroup / 64; ++k) {
+            for (int k = 1; k < NT / 64; ++k) {
                 mx = fmaxf(mx, smax[k]);
                 sm += ssum[k];
             }
@@ -359,8 +362,8 @@ __device__ inline LoopCounters loop_counters(const PartialArgs& a) {
 // counts the iteration (once, by group 0's merge); a g update whose counters call for the loop control runs it in
 // the last workgroup to arrive (counter: zero on entry, left zero), which on a new eps also derives the log2-unit
 // potentials again and remakes the first cloud's log2-unit copy for the next f update. COH as in merge_group:
-// the other groups' results were stored in this launch by other workgroups.
-template <bool COH>
+// the other groups' results were stored in this launch by other workgroups. NT: the workgroup's threads.
+template <bool COH, int NT>
 __device__ inline void loop_step(const PartialArgs& a, int g, const LoopCounters& lc, int* counter) {
     if (a.tick != nullptr) {                   // the f update: count the iteration (nobody reads these meanwhile)
         if (g == 0 && tid_x() == 0) {
@@ -397,15 +400,15 @@ __device__ inline void loop_step(const PartialArgs& a, int g, const LoopCounters
     // update already finds them. (This is the g update: rows y, columns x.)
     const float k2 = 0.5f * (s_sc[0] * kLog2e);
     const int nx = a.s.nt * SK_TILE;
-    for (int i = tid_x(); i < a.rows_pad; i += kRowsPerGroup) a.out2[i] = ld<COH>(a.out + i) * k2;
-    for (int i = tid_x(); i < nx; i += kRowsPerGroup) a.u2[i] = a.u[i] * k2;
+    for (int i = tid_x(); i < a.rows_pad; i += NT) a.out2[i] = ld<COH>(a.out + i) * k2;
+    for (int i = tid_x(); i < nx; i += NT) a.u2[i] = a.u[i] * k2;
     const void* second = a.xr;
     const BakeParams b = bake_params(a.rebake, second, s_sc);
     const float* h = reinterpret_cast<const float*>(a.rebake);
     if (b.valid ? h[2] == b.c && h[3] == packed_scale(second) : h[2] == 0.0f) return;
     if (b.valid) {
         const long long total = (long long)(nx / SK_TILE) * a.nc * 64;
-        for (long long idx = tid_x(); idx < total; idx += kRowsPerGroup) bake_unit(a.rebake, idx, nx, a.nc, b);
+        for (long long idx = tid_x(); idx < total; idx += NT) bake_unit(a.rebake, idx, nx, a.nc, b);
     }
     __syncthreads();
     if (tid_x() == 0) bake_header(a.rebake, second, b);

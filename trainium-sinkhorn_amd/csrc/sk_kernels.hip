@@ -218,8 +218,8 @@ __global__ __launch_bounds__(kRowsPerGroup) void merge_kernel(PartialArgs a) {
     const LoopCounters lc = loop_counters(a);
     // The loop's convergence partials are read only by a control that checks: skip them otherwise.
     if (a.state != nullptr && !needs_control(lc.it, lc.stage, lc.stage_it, a.cfg)) a.meas = nullptr;
-    if (!merge_group<false>(a, (int)blockIdx.x)) return;
-    loop_step<false>(a, (int)blockIdx.x, lc, a.counters);
+    if (!merge_group<false, kRowsPerGroup>(a, (int)blockIdx.x)) return;
+    loop_step<false, kRowsPerGroup>(a, (int)blockIdx.x, lc, a.counters);
 }
 
 // The on-device loop's log2-unit potentials from the accumulator-unit ones, R = (c / 2) fh, c = sc[0] log2(e).

@@ -32,27 +32,28 @@
 // product of the two scales in both directions): `rows_role` says
 // whether the rows are the first or the second cloud, and the pair list is transposed accordingly. The
 // contraction starts from zero and the column term is added afterwards: by one more MFMA per row block and
-// tile in the streamed fp16 variant (the fp32 term split exactly into three bf16 pieces, summed against
+// tile with the fp16 contraction (the fp32 term split exactly into three bf16 pieces, summed against
 // B = (1, 1, 1): exact for every fp32 value, since bf16 has fp32's exponent range; 32 VALU adds per tile
 // fewer), on the VALU otherwise. The max is subtracted before scaling, exp2(c (a - M)), so the dominant term
 // is exactly 1.
 //
-// Layout of one workgroup (4 waves, one per SIMD of a CU): wave w owns kRowBlocks blocks of 32 rows of a
-// row group (its fp16 pieces stay in registers for the whole work segment), and all four waves walk the same
-// column tiles. Two ways to feed the column tiles, chosen by size:
-//   - streamed (kp <= 64): every wave loads the tile's pieces straight into registers one tile ahead; the
-//     four waves of the CU read the same addresses at about the same time and share them through L1. The
-//     column terms of the whole segment are computed once into LDS (as MFMA operands with the fp16
-//     contraction). No per-tile barrier.
-//   - staged (kp > 64, where a register double buffer no longer fits): the workgroup stages each tile and
-//     its 32 column terms once in LDS (double buffered, one barrier per tile).
+// Layout of one workgroup (one row group of 256 rows): wave w owns kRowBlocksK blocks of 32 rows of the
+// group (its fp16 pieces stay in registers for the whole work segment), and all waves walk the same column
+// tiles. Two ways to feed the column tiles, chosen by size and built as separate variants:
+//   - streamed (kp <= 64; 4 waves, one per SIMD, 2 row blocks each): every wave loads the tile's pieces
+//     straight into registers one tile ahead; the four waves of the CU read the same addresses at about the
+//     same time and share them through L1. The column terms of the whole segment are computed once into LDS
+//     (as MFMA operands with the fp16 contraction). No per-tile barrier.
+//   - staged (kp > 64, where a register double buffer no longer fits; 8 waves, two per SIMD, 1 row block
+//     each): the workgroup stages each tile and its 32 column terms (as bf16 MFMA operands with the fp16
+//     contraction) once in LDS, double buffered, one barrier per tile.
 // MFMA orientation: A = 32 columns, B = 32 rows, so lane l's 16 accumulators all belong to row l % 32
 // (columns 8 (r / 4) + 4 (l / 32) + r % 4); row reductions stay inside a lane and lanes l, l + 32 are merged
 // once per segment.
 //
-// This file is compiled twice: SK_PARTIAL_LARGE = 0 builds the streamed instantiations (nc <= 4) with MFMA
-// results forced into VGPRs (-mllvm -amdgpu-mfma-vgpr-form: the epilogue reads them without copies),
-// SK_PARTIAL_LARGE = 1 the staged ones (nc > 4) with the compiler's default register classes.
+// This file is compiled twice: SK_PARTIAL_LARGE = 0 builds the streamed instantiations (nc <= 4),
+// SK_PARTIAL_LARGE = 1 the staged ones (nc > 4), both with MFMA results forced into VGPRs
+// (-mllvm -amdgpu-mfma-vgpr-form: the epilogue reads them without copies).
 
 #include <type_traits>
 #include <utility>
@@ -66,6 +67,21 @@
 
 namespace sk {
 namespace {
+
+// Waves per workgroup and 32-row blocks per wave of this build's variant; a row group is 256 rows in both.
+//   streamed (kp <= 64): 4 waves, one per SIMD, 2 row blocks each (64 rows of operands and two accumulator chains
+//     per wave, the epilogue interleaved with the MFMAs at compile time);
+//   staged (kp > 64): 8 waves, two per SIMD, one row block each. A wave then holds its row operands (kp / 2
+//     registers), one column tile (kp / 2) and two accumulator sets (32) within 256 registers with the MFMA results
+//     in VGPRs, where two row blocks per wave needed ~370 and moved every result out of AGPRs (about 90 VALU
+//     instructions per tile); and the two waves of a SIMD overlap one's exponentials with the other's MFMAs.
+#if SK_PARTIAL_LARGE
+constexpr int kWavesK = 8, kRowBlocksK = 1, kWavesPerSimd = 2;
+#else
+constexpr int kWavesK = 4, kRowBlocksK = 2, kWavesPerSimd = 1;
+#endif
+constexpr int kBlockK = 64 * kWavesK;
+static_assert(32 * kRowBlocksK * kWavesK == kRowsPerGroup, "a row group is 256 rows in both variants");
 
 __device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -237,10 +253,11 @@ struct Staged {
     using T = typename C::T;
     static constexpr int kPieces = C::pieces;
     static constexpr int kProducts = C::products;
-    static constexpr int RB = kRowBlocks;
+    static constexpr int RB = kRowBlocksK;
     static constexpr int TILE16 = NC * kPieces * 64;   // 16-byte units per packed 32-point tile
-    static constexpr int PER_THREAD = (TILE16 + kBlock - 1) / kBlock;
+    static constexpr int PER_THREAD = (TILE16 + kBlockK - 1) / kBlockK;
     static constexpr int NS = kProducts * NC * RB;     // MFMA slots per tile
+    static constexpr bool FOLD = CT == kF16x2;         // column terms added by the matrix pipe
 
     // Rows rb0 .. rb0 + RB - 1 against column tiles [tb, te); writes one (M, S) per row into `slot`.
     __device__ __forceinline__ static void run(const PartialArgs& a, int rb0, int tb, int te, int slot, const float* cu,
@@ -275,14 +292,16 @@ struct Staged {
         // term of column j. Branch-free (clamped indices; threads mapped to the same element write the same
         // value), so that a whole tile is one basic block and the epilogue stays between the MFMAs. The
         // operands are double buffered (read into registers before the tile's MFMAs); the column terms are
-        // triple buffered, since the update of tile t - 1 reads them while tile t + 1 is staged.
+        // triple buffered, since (without FOLD) the update of tile t - 1 reads them while tile t + 1 is staged.
+        // With FOLD each column term is staged as the A operand of the column MFMA, three exact bf16 pieces
+        // (q = q0 + q1 + q2), 16 bytes per column.
         const int cj = tid & 31;
         T pf[PER_THREAD];
         float pc = 0.0f;
         auto prefetch = [&](int t) {
 #pragma unroll
             for (int k = 0; k < PER_THREAD; ++k) {
-                const int idx = tid + k * kBlock < TILE16 ? tid + k * kBlock : TILE16 - 1;
+                const int idx = tid + k * kBlockK < TILE16 ? tid + k * kBlockK : TILE16 - 1;
                 pf[k] = yt[(size_t)t * TILE16 + idx];
             }
             pc = fmaxf(cs * fmaf(beta, a.v[t * 32 + cj], alpha * cu[t * 32 + cj]), kPadScore);
@@ -290,10 +309,18 @@ struct Staged {
         auto stage = [&](int buf, int cbuf) {
 #pragma unroll
             for (int k = 0; k < PER_THREAD; ++k) {
-                const int idx = tid + k * kBlock < TILE16 ? tid + k * kBlock : TILE16 - 1;
+                const int idx = tid + k * kBlockK < TILE16 ? tid + k * kBlockK : TILE16 - 1;
                 lds_y[buf * TILE16 + idx] = pf[k];
             }
-            lds_col[cbuf * 32 + cj] = pc;
+            if constexpr (FOLD) {
+                const __bf16 q0 = (__bf16)pc;
+                const float r1 = pc - (float)q0;                  // exact
+                const __bf16 q1 = (__bf16)r1;
+                const __bf16 q2 = (__bf16)(r1 - (float)q1);       // exact: at most 8 bits remain
+                reinterpret_cast<bf16x8*>(lds_col)[cbuf * 32 + cj] = bf16x8{q0, q1, q2, 0, 0, 0, 0, 0};
+            } else {
+                lds_col[cbuf * 32 + cj] = pc;
+            }
         };
         T yv[NC][kPieces];
         auto read_tile = [&](int buf) {
@@ -302,12 +329,16 @@ struct Staged {
 #pragma unroll
                 for (int p = 0; p < kPieces; ++p) yv[cc][p] = lds_y[buf * TILE16 + (cc * kPieces + p) * 64 + lane];
         };
+        // With FOLD, the B operand of the column MFMA: 1 in k = 0, 1, 2 of every row (lanes 0-31), zeros elsewhere.
+        const __bf16 one = h == 0 ? (__bf16)1.0f : (__bf16)0.0f;
+        const bf16x8 colB = {one, one, one, 0, 0, 0, 0, 0};
 
         f32x16 accA[RB], accB[RB];
-        Online<RB, L2> on;
-        // One tile: MFMAs into accN from zero; with `epi`, the update of the previous tile (accP, its column
-        // terms at colp) is spread between them, one slot per MFMA, fenced so the compiler keeps the interleave.
-        auto tile = [&](f32x16 (&accN)[RB], f32x16 (&accP)[RB], const float* colp, bool epi) {
+        Online<RB, L2, FOLD> on;
+        // One tile: MFMAs into accN from zero, then (FOLD) the column MFMA with the tile's column terms from column
+        // buffer cbn; with `epi`, the update of the previous tile (accP, its column terms at colp) is spread between
+        // them, one slot per MFMA, fenced so the compiler keeps the interleave.
+        auto tile = [&](f32x16 (&accN)[RB], f32x16 (&accP)[RB], const float* colp, int cbn, bool epi) {
             auto col4 = [&](int q) { return *reinterpret_cast<const f32x4*>(colp + 8 * q); };
 #pragma unroll
             for (int b = 0; b < RB; ++b) accN[b] = f32x16{};
@@ -318,11 +349,18 @@ struct Staged {
                 constexpr int cp = ROLE == 0 ? C::second[p] : C::first[p];
                 accN[b] = C::mfma(yv[cc][cp], xv[b][cc][rp], accN[b]);
                 if (epi) {
-                    constexpr int k0 = op_begin<RB, false>(i, NS), k1 = op_begin<RB, false>(i + 1, NS);
+                    constexpr int k0 = op_begin<RB, FOLD>(i, NS), k1 = op_begin<RB, FOLD>(i + 1, NS);
                     static_for<k0, k1>([&](auto K) { on.template step<decltype(K)::value>(accP, col4, M, S, c); });
                 }
                 __builtin_amdgcn_sched_barrier(0);
             });
+            // The column terms last, after the whole dot product: x.y is formed identically in both directions.
+            if constexpr (FOLD) {
+                const bf16x8 colA = reinterpret_cast<const bf16x8*>(lds_col)[cbn * 32 + (lane & 31)];
+#pragma unroll
+                for (int b = 0; b < RB; ++b)
+                    accN[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(colA, colB, accN[b], 0, 0, 0);
+            }
         };
         auto update = [&](f32x16 (&accP)[RB], const float* colp) {
             auto col4 = [&](int q) { return *reinterpret_cast<const f32x4*>(colp + 8 * q); };
@@ -341,7 +379,7 @@ struct Staged {
         int cb = 0;                            // column buffer of tile t
         read_tile(0);
         prefetch(t + 1 < te ? t + 1 : last);
-        tile(accA, accB, nullptr, false);
+        tile(accA, accB, nullptr, 0, false);
         stage(1, 1);
         __syncthreads();
         ++t;
@@ -350,7 +388,7 @@ struct Staged {
             int cn2 = cn == 2 ? 0 : cn + 1;    // tile t + 1
             read_tile((t - tb) & 1);
             prefetch(t + 1 < te ? t + 1 : last);
-            tile(accB, accA, colp_of(cb), true);
+            tile(accB, accA, colp_of(cb), cn, true);
             stage((t + 1 - tb) & 1, cn2);
             __syncthreads();
             ++t;
@@ -363,7 +401,7 @@ struct Staged {
             cn2 = cn == 2 ? 0 : cn + 1;
             read_tile((t - tb) & 1);
             prefetch(t + 1 < te ? t + 1 : last);
-            tile(accA, accB, colp_of(cb), true);
+            tile(accA, accB, colp_of(cb), cn, true);
             stage((t + 1 - tb) & 1, cn2);
             __syncthreads();
             ++t;
@@ -388,7 +426,7 @@ struct Streamed {
     using T = typename C::T;
     static constexpr int kPieces = C::pieces;
     static constexpr int kProducts = C::products;
-    static constexpr int RB = kRowBlocks;
+    static constexpr int RB = kRowBlocksK;
     static constexpr int TILE16 = NC * kPieces * 64;
     static constexpr int NS = kProducts * NC * RB;
     static constexpr bool FOLD = CT == kF16x2;      // column terms added by the matrix pipe
@@ -433,18 +471,18 @@ struct Streamed {
             const int n = (t1 - t0 + (FOLD ? 0 : 1)) * 32, base = (t0 - (FOLD ? 0 : 1)) * 32;
             // Eight column terms per thread per batch, all sixteen loads in flight before the first use (a
             // run of up to 256 tiles takes at most five batches, a typical segment one).
-            for (int k0 = 0; k0 < n; k0 += kColBatch * kBlock) {
+            for (int k0 = 0; k0 < n; k0 += kColBatch * kBlockK) {
                 float uu[kColBatch], vv[kColBatch];
 #pragma unroll
                 for (int q = 0; q < kColBatch; ++q) {
-                    const int k = k0 + q * kBlock + tid, j = base + k;
+                    const int k = k0 + q * kBlockK + tid, j = base + k;
                     const int jc = (k < n && j >= 0) ? j : 0;     // clamped in bounds; not stored
                     uu[q] = cu[jc];
                     vv[q] = a.v[jc];
                 }
 #pragma unroll
                 for (int q = 0; q < kColBatch; ++q) {
-                    const int k = k0 + q * kBlock + tid, j = base + k;
+                    const int k = k0 + q * kBlockK + tid, j = base + k;
                     if (k < n && j >= 0) {
                         const float v = fmaxf(cs * fmaf(beta, vv[q], alpha * uu[q]), kPadScore);
                         if constexpr (FOLD) {
@@ -617,7 +655,7 @@ __device__ inline void arrive(const PartialArgs& a, int g) {
     // one included, so nothing has changed them yet.
     const LoopCounters lc = loop_counters(m);
     if (m.state != nullptr && !needs_control(lc.it, lc.stage, lc.stage_it, m.cfg)) m.meas = nullptr;   // no check
-    if (merge_group<true>(m, g)) loop_step<true>(m, g, lc, m.counters);
+    if (merge_group<true, kBlockK>(m, g)) loop_step<true, kBlockK>(m, g, lc, m.counters);
     __syncthreads();   // the next segment's column staging reuses LDS the merge does not touch; keep waves together
 }
 
@@ -638,7 +676,7 @@ __device__ __forceinline__ void segments(const PartialArgs& a, int p, int wv, co
         const int slot = __builtin_amdgcn_readfirstlane(p - first_wg(g, a.s));
         // Waves past the last row block recompute it (their rows are not stored) so that every wave takes part
         // in the workgroup's barriers.
-        const int rb0 = (g * kWaves + wv) * kRowBlocks;
+        const int rb0 = (g * kWavesK + wv) * kRowBlocksK;
         if constexpr (NC <= kStreamMaxChunks)
             Streamed<NC, ROLE, CT, L2>::run(a, rb0, tb, te, slot, cu, alpha, beta, cs, c, inv_sigma, lds_col);
         else
@@ -648,10 +686,8 @@ __device__ __forceinline__ void segments(const PartialArgs& a, int p, int wv, co
     }
 }
 
-static_assert(kBlock == kRowsPerGroup, "the merge inside the partial kernel takes one row per thread");
-
 template <int NC, int ROLE, int CT>
-__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(1, 1)))
+__global__ __launch_bounds__(kBlockK) __attribute__((amdgpu_waves_per_eu(kWavesPerSimd, kWavesPerSimd)))
 void lse_partial_kernel(PartialArgs a) {
     // Every scalar this launch needs (the loop's done flag, the eps scalars, both clouds' scales, the first
     // cloud's log2-copy tag) is requested at once, and the done flag tested after: one memory round trip before
@@ -670,7 +706,7 @@ void lse_partial_kernel(PartialArgs a) {
     if (skip != 0) return;
     constexpr bool kStream = NC <= kStreamMaxChunks;
     constexpr int kLdsY = kStream ? 1 : 2 * NC * Contract<CT>::pieces * 64;
-    constexpr int kLdsCol = kStream ? col_floats(CT == kF16x2) : 3 * 32;
+    constexpr int kLdsCol = kStream ? col_floats(CT == kF16x2) : 3 * 32 * (CT == kF16x2 ? 4 : 1);
     __shared__ typename Contract<CT>::T lds_y[kLdsY];
     __shared__ __attribute__((aligned(16))) float lds_col[kLdsCol];
     const int wv = __builtin_amdgcn_readfirstlane(tid_x() >> 6);   // one value per wave
@@ -711,11 +747,11 @@ template <int NC>
 hipError_t launch_nc(const PartialArgs& a, hipStream_t st) {
     if (a.contraction == kBF16x3) {
         if (a.rows_role != 0) return hipErrorInvalidValue;
-        hipLaunchKernelGGL((lse_partial_kernel<NC, 0, kBF16x3>), dim3(a.s.P), dim3(kBlock), 0, st, a);
+        hipLaunchKernelGGL((lse_partial_kernel<NC, 0, kBF16x3>), dim3(a.s.P), dim3(kBlockK), 0, st, a);
     } else if (a.rows_role == 0) {
-        hipLaunchKernelGGL((lse_partial_kernel<NC, 0, kF16x2>), dim3(a.s.P), dim3(kBlock), 0, st, a);
+        hipLaunchKernelGGL((lse_partial_kernel<NC, 0, kF16x2>), dim3(a.s.P), dim3(kBlockK), 0, st, a);
     } else {
-        hipLaunchKernelGGL((lse_partial_kernel<NC, 1, kF16x2>), dim3(a.s.P), dim3(kBlock), 0, st, a);
+        hipLaunchKernelGGL((lse_partial_kernel<NC, 1, kF16x2>), dim3(a.s.P), dim3(kBlockK), 0, st, a);
     }
     return hipGetLastError();
 }

@@ -7,8 +7,8 @@ directory); nothing is compiled at import time. Two translation units:
 
 * sk_lse_partial.hip -- the MFMA partial (max, sum) kernel, built with -fno-honor-nans -mno-amdgpu-ieee
   (no NaN ever reaches it; this drops the IEEE canonicalisation of every MFMA result before a max), twice:
-  the streamed instantiations (kp <= 64) with MFMA results in VGPRs (-amdgpu-mfma-vgpr-form), and the staged
-  ones (kp > 64) with the compiler's default register classes;
+  the streamed instantiations (kp <= 64) and the staged ones (kp > 64), both with MFMA results in VGPRs
+  (-amdgpu-mfma-vgpr-form: the epilogue reads them without copies);
 * sk_kernels.hip -- packing, finalisation, the on-device loop and the C ABI, built with default NaN
   semantics (the loop state stores NaN for "not checked yet").
 
@@ -38,7 +38,8 @@ COMMON = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", f"-I{INCLUDE}"
 UNITS = [   # (source, object name, extra flags)
     ("sk_lse_partial.hip", "sk_lse_partial_small", ["-fno-honor-nans", "-mno-amdgpu-ieee", "-DSK_PARTIAL_LARGE=0",
                                                     "-mllvm", "-amdgpu-mfma-vgpr-form"]),
-    ("sk_lse_partial.hip", "sk_lse_partial_large", ["-fno-honor-nans", "-mno-amdgpu-ieee", "-DSK_PARTIAL_LARGE=1"]),
+    ("sk_lse_partial.hip", "sk_lse_partial_large", ["-fno-honor-nans", "-mno-amdgpu-ieee", "-DSK_PARTIAL_LARGE=1",
+                                                    "-mllvm", "-amdgpu-mfma-vgpr-form"]),
     ("sk_kernels.hip", "sk_kernels", []),
     ("sk_median.hip", "sk_median", []),
 ]

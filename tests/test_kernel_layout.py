@@ -1,7 +1,7 @@
 """CPU emulation of the HIP kernels' index arithmetic (trainium-sinkhorn_amd/csrc).
 
-Every load and store of pack_cloud_kernel, lse_partial_kernel (global loads, LDS staging and reads, partial
-slots) and the merge of the slots (merge_group, sk_epilogue.h) is replayed in numpy with the kernels' own
+Every load and store of pack_cloud_kernel, lse_partial_kernel (global loads, LDS staging and reads -- for the
+staged variant a replay of its LDS ring with barrier epochs --, partial slots) and the merge of the slots (merge_group, sk_epilogue.h) is replayed in numpy with the kernels' own
 formulas (workgroup renumbering,
 stream-K ranges, partial slots, the power-of-two scale and two-piece fp16 packing, the
 v_mfma_f32_32x32x16_f16 operand and accumulator lane mapping, the product order of both row roles, the
@@ -13,7 +13,8 @@ import numpy as np
 import pytest
 from scipy.special import logsumexp
 
-TILE, WAVES, XCDS, RB, BLOCK = 32, 4, 8, 2, 256
+TILE, WAVES, XCDS, RB, BLOCK = 32, 4, 8, 2, 256   # streamed variant: 4 waves of 2 row blocks
+WAVES_K, RB_K, BLOCK_K = 8, 1, 512                 # staged variant: 8 waves of 1 row block
 STREAM_MAX_CHUNKS, COL_TILES = 4, 256        # streamed variant: nc <= 4; column terms staged per 256 tiles
 FOLD_COL_TILES = 192                         # ... per 192 tiles with the f16x2 contraction (folded, 16 B each)
 SEG_COST_STREAMED, SEG_COST_STAGED = 6, 2    # cost of a row-group boundary in tiles (sk_kernels.hip make_plan)
@@ -201,6 +202,141 @@ def mfma_32x32x16(Aop, Bop):
     return D[m, (lane % 32)[:, None]]
 
 
+def ring_depth(nc, pieces):
+    """Register slots of the staged kernel's column-chunk ring (sk_lse_partial.hip ring_depth)."""
+    top = 4 if pieces > 2 else 2 * nc
+    for dd in range(4, top + 1):
+        if (2 * nc) % dd == 0:
+            return dd
+    return 2
+
+
+def staged_protocol(segments, nc, pieces, products, tps, ahead=2):
+    """Replay the LDS protocol of the staged kernel (sk_lse_partial.hip Staged::run) over the work segments of one
+    workgroup, in program order, with barrier epochs: a write becomes visible to the other waves at the next
+    barrier, and waves interleave arbitrarily between barriers. Asserts that every read (column chunks into the
+    register ring, the column MFMA's operand, the column terms of the previous tile without FOLD) sees data
+    staged for the tile it belongs to (min(t, last)), written in an earlier epoch and not rewritten in the same
+    epoch, and that every MFMA takes its chunk from the ring slot holding it. `ahead` is the stage distance in
+    steps (two in the kernel; other values are planted mistakes). Returns the number of barriers."""
+    fold = pieces == 2
+    D = ring_depth(nc, pieces)
+    LA = D - 1
+    NS = products * nc * RB_K
+    nsets = 2 if tps == 1 else 1
+    stage_slot = NS // 3
+    visible = {}                  # ("y", lds tile) / ("c", column buffer, tile of step) -> tile id
+    pending = {}                  # writes of the current epoch
+    reads = set()                 # regions read in the current epoch
+    barriers = [0]
+
+    def write(key, tile):
+        assert key not in reads, f"write after read in one epoch: {key}"
+        pending[key] = tile
+
+    def read(key, tile):
+        assert key not in pending, f"read of {key} rewritten in the same epoch"
+        assert visible.get(key) == tile, f"{key} holds {visible.get(key)}, expected tile {tile}"
+        reads.add(key)
+
+    def barrier():
+        visible.update(pending)
+        pending.clear()
+        reads.clear()
+        barriers[0] += 1
+
+    for tb, te in segments:
+        last = te - 1
+        clamp = lambda t: t if t < te else last                           # noqa: E731
+        sets = [None] * nsets                      # tile ids held by each register set (per tile of the step)
+
+        def prefetch(sset, t0):
+            sets[sset] = [clamp(t0 + tt) for tt in range(tps)]
+
+        def stage_tile(sset, tt, ybuf):
+            write(("y", ybuf * tps + tt), sets[sset][tt])
+
+        def stage_cols(sset, cbuf):
+            for tt in range(tps):
+                write(("c", cbuf, tt), sets[sset][tt])
+
+        def stage(sset, ybuf, cbuf):
+            for tt in range(tps):
+                stage_tile(sset, tt, ybuf)
+            stage_cols(sset, cbuf)
+
+        ring = {}
+        yq, cq = 0, 0
+
+        def read_chunk(g, ytile, tile):
+            read(("y", ytile), tile)
+            ring[g % D] = (tile, g % nc)
+
+        if nsets == 2:
+            prefetch(0, tb)
+            prefetch(1, tb + tps)
+            stage(0, 0, 0)
+            stage(1, 1, 1)
+            prefetch(0, tb + 2 * tps)
+            prefetch(1, tb + 3 * tps)
+        else:
+            prefetch(0, tb)
+            stage(0, 0, 0)
+            prefetch(0, tb + tps)
+            stage(0, 1, 1)
+            prefetch(0, tb + 2 * tps)
+        barrier()
+        for g in range(LA):
+            read_chunk(g, 0, clamp(tb))
+
+        def tile(ph, t, prev):
+            nonlocal yq, cq
+            tt = ph % tps
+            ycur = yq * tps + tt
+            ynext = ycur + 1 if tt + 1 < tps else ((yq + 1) % 3) * tps
+            if fold:
+                read(("c", cq, tt), clamp(t))
+            for i in range(NS):
+                cc, p = i // products, i % products
+                g = ph * nc + cc
+                if p == 0:
+                    if cc + LA < nc:
+                        read_chunk((g + LA) % (2 * nc), ycur, clamp(t))
+                    else:
+                        read_chunk((g + LA) % (2 * nc), ynext, clamp(t + 1))
+                assert ring[g % D] == (clamp(t), cc), (t, cc, ring[g % D])
+                if i == 0 and prev is not None and not fold:
+                    read(("c",) + prev[0], prev[1])                       # the previous tile's column terms
+                if tt == 0:
+                    sset = 0 if nsets == 1 else ph
+                    if i == stage_slot - 2:
+                        stage_cols(sset, (cq + ahead) % 4)
+                    for u in range(tps):
+                        if i == stage_slot + 2 * u:
+                            stage_tile(sset, u, (yq + ahead) % 3)
+                        if i == stage_slot + 2 * u + 1:
+                            sets[sset][u] = clamp(t + (2 + nsets) * tps + u)
+                    if i == stage_slot + 2 * tps:
+                        pass                                              # the column inputs: same tile ids
+            if ph % tps == tps - 1:
+                yq, cq = (yq + 1) % 3, (cq + 1) % 4
+                barrier()
+            return ((cq if ph % tps != tps - 1 else (cq + 3) % 4, tt), clamp(t))
+
+        prev = tile(0, tb, None)
+        t = tb + 1
+        while te - t >= 2:
+            prev = tile(1, t, prev)
+            prev = tile(0, t + 1, prev)
+            t += 2
+        if t < te:
+            prev = tile(1, t, prev)
+        if not fold:
+            read(("c",) + prev[0], prev[1])                               # the last update's column terms
+        barrier()
+    return barriers[0]
+
+
 def emulate_lse(xa, ya, role=0, ncu=256, per_cu=1, c=np.log2(np.e), contraction="bf16x3", col=None,
                 fold_rule=(fold_split, fold_b_operand)):
     """Row LSE (plain mode: alpha = 1 on a 0 / -1e30 mask, beta = 0) through the kernels' index math, the
@@ -215,7 +351,9 @@ def emulate_lse(xa, ya, role=0, ncu=256, per_cu=1, c=np.log2(np.e), contraction=
     kp, rp, mp = pad_dim(K), pad_points(rows), pad_points(m)
     nc = kp // 16
     tile16 = nc * PIECES * 64
-    per_thread = -(-tile16 // BLOCK)
+    staged_variant = nc > STREAM_MAX_CHUNKS
+    waves, rbk, block = (WAVES_K, RB_K, BLOCK_K) if staged_variant else (WAVES, RB, BLOCK)
+    per_thread = -(-tile16 // block)
     sx, xr = pack(xa, rows, K, contraction)
     sy, yc = pack(ya, m, K, contraction)
     sigma, inv_sigma = np.float32(sx * sy), np.float32((1 / sx) * (1 / sy))
@@ -227,12 +365,11 @@ def emulate_lse(xa, ya, role=0, ncu=256, per_cu=1, c=np.log2(np.e), contraction=
     with np.errstate(over="ignore"):
         u = np.maximum((u_raw * sigma).astype(np.float32), PAD_SCORE)     # scaled column term, floored
     nrb, nt, ngroups, s, slots = plan(rp, mp, ncu, per_cu, nc=nc)
-    fold = contraction == "f16x2" and nc <= STREAM_MAX_CHUNKS
+    fold = contraction == "f16x2"
     part = np.full((slots, rp, 2), np.nan)
     lane = np.arange(64)
     h = lane >> 5
-    tid = np.arange(BLOCK)
-    cj = tid & 31
+    tid = np.arange(block)
     seen = np.zeros((ngroups, nt), dtype=int)
     cf = np.float32(np.float32(c) * inv_sigma)
     ra, ca = (FIRST_, SECOND_) if role == 0 else (SECOND_, FIRST_)
@@ -270,23 +407,24 @@ def emulate_lse(xa, ya, role=0, ncu=256, per_cu=1, c=np.log2(np.e), contraction=
                         staged[t] = (yc[gi].copy(), lds_col[rd].copy())
                 loads = [min(t + 1, te - 1) for t in range(tb, te)]      # the one-ahead operand loads
                 assert max(loads) * tile16 + tile16 - 1 < yc.shape[0]
-            lds_y = np.full((2 * tile16, 8), np.nan, dtype=np.float32)
-            lds_col = np.full(64, np.nan, dtype=np.float32)
-            for t in (list(range(tb, te)) + [te - 1]) if nc > STREAM_MAX_CHUNKS else []:
-                buf = (t - tb) & 1
+            if staged_variant:
+                # staged: the LDS protocol of the ring (asserted), then each tile's operands and column terms
+                staged_protocol([(tb, te)], nc, PIECES, len(FIRST_), 2 if contraction == "f16x2" else 1)
                 for k in range(per_thread):
-                    idx = np.where(tid + k * BLOCK < tile16, tid + k * BLOCK, tile16 - 1)
-                    gsrc = t * tile16 + idx
-                    assert gsrc.max() < yc.shape[0]
-                    dst = buf * tile16 + idx
-                    assert dst.max() < lds_y.shape[0]
-                    lds_y[dst] = yc[gsrc]
-                assert (t * 32 + cj).max() < mp
-                lds_col[buf * 32 + cj] = u[t * 32 + cj]
-                staged[t] = (lds_y[buf * tile16:(buf + 1) * tile16].copy(), lds_col[buf * 32:buf * 32 + 32].copy())
-            for wv in range(WAVES):
-                rb0 = (g * WAVES + wv) * RB
-                for bb in range(RB):
+                    idx = np.where(tid + k * block < tile16, tid + k * block, tile16 - 1)
+                    assert idx.max() < tile16 and (te - 1) * tile16 + idx.max() < yc.shape[0]
+                for t in range(tb, te):
+                    assert t * 32 + 31 < mp
+                    gi = t * tile16 + np.arange(tile16)
+                    if fold:
+                        q = np.zeros((64, 8), dtype=np.float32)
+                        q[:, 0], q[:, 1], q[:, 2] = fold_rule[0](u[t * 32 + (lane & 31)])
+                        staged[t] = (yc[gi].copy(), q)
+                    else:
+                        staged[t] = (yc[gi].copy(), u[t * 32 + np.arange(32)].copy())
+            for wv in range(waves):
+                rb0 = (g * waves + wv) * rbk
+                for bb in range(rbk):
                     blk = rb0 + bb if rb0 + bb < nrb else nrb - 1
                     xi = blk * tile16 + (np.arange(nc)[:, None, None] * PIECES + np.arange(PIECES)[None, :, None]) * 64 \
                         + lane[None, None, :]
@@ -628,3 +766,32 @@ def test_folded_column_terms_cover_small_and_mixed_scale_clouds(case):
     assert np.abs(got - want).max() <= tol, (np.abs(got - want).max(), tol)
     bad, _ = emulate_lse(x, y, col=col32, c=c, contraction="f16x2", fold_rule=(fp16_fold_split, fp16_fold_b_operand))
     assert np.abs(bad - want).max() > 1e3 * tol
+
+
+
+@pytest.mark.parametrize("nc", [5, 6, 7, 8])
+@pytest.mark.parametrize("ct", ["f16x2", "bf16x3"])
+def test_staged_ring_protocol(nc, ct):
+    """The staged kernel's LDS ring (three step buffers, four column buffers, steps of two tiles with f16x2 and
+    one with bf16x3, the column chunks read ahead into a register ring) over segments of every length from 1 to
+    13 tiles, one after another in one workgroup as the work split hands them out: every read sees its own
+    tile's data, staged in an earlier barrier epoch and not rewritten in its own; one barrier per step plus two
+    per segment."""
+    pieces, first, _ = CONTRACTIONS[ct]
+    tps = 2 if ct == "f16x2" else 1
+    lengths = range(1, 14)
+    segs, t0 = [], 0
+    for n in lengths:
+        segs.append((t0, t0 + n))
+        t0 += n + 3
+    nb = staged_protocol(segs, nc, pieces, len(first), tps)
+    assert nb == sum(2 + (n if tps == 1 else n // 2) for n in lengths)
+
+
+@pytest.mark.parametrize("ahead", [1, 3])
+def test_staged_ring_protocol_catches_a_wrong_stage_distance(ahead):
+    """Planted mistakes: staging the step `ahead` steps ahead instead of two. One ahead writes the buffer of the
+    step whose first chunks the current step's last tile reads; three ahead (into buffer q % 3, the current
+    step's own) rewrites operands still being read."""
+    with pytest.raises(AssertionError):
+        staged_protocol([(0, 9)], 8, 2, 3, 2, ahead=ahead)

@@ -45,8 +45,10 @@
 //     same time and share them through L1. The column terms of the whole segment are computed once into LDS
 //     (as MFMA operands with the fp16 contraction). No per-tile barrier.
 //   - staged (kp > 64, where a register double buffer no longer fits; 8 waves, two per SIMD, 1 row block
-//     each): the workgroup stages each tile and its 32 column terms (as bf16 MFMA operands with the fp16
-//     contraction) once in LDS, double buffered, one barrier per tile.
+//     each): the workgroup stages the tiles and their column terms (as bf16 MFMA operands with the fp16
+//     contraction) once in LDS, in steps of two tiles (one with the bf16 contraction) through a ring of three
+//     step buffers, two steps ahead, one barrier per step; each wave reads its column operands chunk by chunk
+//     a few chunks ahead of their MFMAs.
 // MFMA orientation: A = 32 columns, B = 32 rows, so lane l's 16 accumulators all belong to row l % 32
 // (columns 8 (r / 4) + 4 (l / 32) + r % 4); row reductions stay inside a lane and lanes l, l + 32 are merged
 // once per segment.
@@ -72,9 +74,10 @@ namespace {
 //   streamed (kp <= 64): 4 waves, one per SIMD, 2 row blocks each (64 rows of operands and two accumulator chains
 //     per wave, the epilogue interleaved with the MFMAs at compile time);
 //   staged (kp > 64): 8 waves, two per SIMD, one row block each. A wave then holds its row operands (kp / 2
-//     registers), one column tile (kp / 2) and two accumulator sets (32) within 256 registers with the MFMA results
-//     in VGPRs, where two row blocks per wave needed ~370 and moved every result out of AGPRs (about 90 VALU
-//     instructions per tile); and the two waves of a SIMD overlap one's exponentials with the other's MFMAs.
+//     registers), a ring of a few column chunks (32 registers at kp 128), two accumulator sets (32) and the
+//     registers of the step in flight within 256 registers with the MFMA results in VGPRs, where two row blocks
+//     per wave needed ~370 and moved every result out of AGPRs (about 90 VALU instructions per tile); and the two
+//     waves of a SIMD overlap one's exponentials with the other's MFMAs.
 #if SK_PARTIAL_LARGE
 constexpr int kWavesK = 8, kRowBlocksK = 1, kWavesPerSimd = 2;
 #else
@@ -247,6 +250,19 @@ __device__ __forceinline__ void store_rows(const PartialArgs& a, const float (&M
     }
 }
 
+// Register ring of the staged kernel's column operands: chunk g of a pair of tiles (g = 0 .. 2 nc - 1) sits in
+// slot g % D, read D - 1 chunks ahead of its MFMAs; D divides 2 nc so that the slots repeat every two tiles.
+constexpr int ring_depth(int nc, int pieces) {
+    const int top = pieces > 2 ? 4 : 2 * nc;          // three-piece chunks: at most 4 slots (48 registers)
+    for (int dd = 4; dd <= top; ++dd)
+        if ((2 * nc) % dd == 0) return dd;
+    return 2;
+}
+
+// Tiles per step of the staged kernel: two with the fp16 contraction (96 KB of column operands in flight at
+// kp 128), one with the bf16 one (whose tiles are 1.5 times larger).
+constexpr int staged_step_tiles(int ct) { return ct == kF16x2 ? 2 : 1; }
+
 template <int NC, int ROLE, int CT, bool L2>
 struct Staged {
     using C = Contract<CT>;
@@ -258,8 +274,24 @@ struct Staged {
     static constexpr int PER_THREAD = (TILE16 + kBlockK - 1) / kBlockK;
     static constexpr int NS = kProducts * NC * RB;     // MFMA slots per tile
     static constexpr bool FOLD = CT == kF16x2;         // column terms added by the matrix pipe
+    static constexpr int D = ring_depth(NC, kPieces);  // register slots of column chunks
+    static constexpr int LA = D - 1;                   // chunks read ahead
+    static constexpr int TPS = staged_step_tiles(CT);  // tiles per step (one barrier per step)
+    static constexpr int NSETS = TPS == 1 ? 2 : 1;     // register sets of staged steps in flight
+    static constexpr int kStageSlot = NS / 3;          // the MFMA slots from which the step two ahead is staged
 
     // Rows rb0 .. rb0 + RB - 1 against column tiles [tb, te); writes one (M, S) per row into `slot`.
+    //
+    // Pipeline, in steps of TPS tiles (step q: tiles tb + TPS q ..; its operands in LDS buffer q % 3, its column
+    // terms in column buffer q % 4):
+    //   - from a third of the way through each step's first tile, spread over a few MFMA slots, step q + 2 is
+    //     written to LDS from registers (its buffer held step q - 1, which every wave finished before the barrier
+    //     that ended it) and the same registers are loaded with step q + 2 + NSETS: about two tiles of latency
+    //     cover for the global loads;
+    //   - the column operands of a tile are read chunk by chunk, LA chunks ahead of their MFMAs, the last ones
+    //     of a tile already reading the first chunks of the next (staged at least a step earlier, visible since
+    //     the barrier that ended that step), so that the matrix pipe does not wait on LDS after a barrier;
+    //   - one barrier per step.
     __device__ __forceinline__ static void run(const PartialArgs& a, int rb0, int tb, int te, int slot, const float* cu,
                                                float alpha, float beta, float cs, float c, float inv_sigma,
                                                T* lds_y, float* lds_col) {
@@ -288,46 +320,72 @@ struct Staged {
             S[b] = 0.0f;
         }
 
-        // Staging of one column tile: every thread loads PER_THREAD 16-byte units and thread j % 32 the column
-        // term of column j. Branch-free (clamped indices; threads mapped to the same element write the same
-        // value), so that a whole tile is one basic block and the epilogue stays between the MFMAs. The
-        // operands are double buffered (read into registers before the tile's MFMAs); the column terms are
-        // triple buffered, since (without FOLD) the update of tile t - 1 reads them while tile t + 1 is staged.
-        // With FOLD each column term is staged as the A operand of the column MFMA, three exact bf16 pieces
-        // (q = q0 + q1 + q2), 16 bytes per column.
-        const int cj = tid & 31;
-        T pf[PER_THREAD];
-        float pc = 0.0f;
-        auto prefetch = [&](int t) {
+        // Staging of one step: for each of its tiles every thread loads PER_THREAD 16-byte units and thread j % 32
+        // the inputs of the column term of column j. Branch-free (clamped indices; threads mapped to the same
+        // element write the same value), so that a whole tile is one basic block and the epilogue stays between
+        // the MFMAs. The loads land in registers that nothing reads until the stage (the column term itself is
+        // formed there), so that no instruction in between waits for them. With FOLD each column term is staged
+        // as the A operand of the column MFMA, three exact bf16 pieces (q = q0 + q1 + q2), 16 bytes per column.
+        // Staging of one step. Thread `tid` copies the 16-byte units tid, tid + kBlockK, ... of each tile (clamped:
+        // threads mapped to the same unit write the same value), and lane l of every wave the inputs of the column
+        // term of column l % 32 of tile (l / 32) % TPS (the waves write the same values). Branch-free, so that a
+        // whole tile is one basic block and the epilogue stays between the MFMAs. The loads land in registers that
+        // nothing reads until the stage (the column term itself is formed there), so that no instruction in
+        // between waits for them. With FOLD each column term is staged as the A operand of the column MFMA, three
+        // exact bf16 pieces (q = q0 + q1 + q2), 16 bytes per column.
+        const int last = te - 1;
+        const int cl = lane & (32 * TPS - 1);             // column (cl % 32) of tile cl / 32 of the step
+        unsigned offb[PER_THREAD];                          // byte offsets of this thread's units in a tile
 #pragma unroll
-            for (int k = 0; k < PER_THREAD; ++k) {
-                const int idx = tid + k * kBlockK < TILE16 ? tid + k * kBlockK : TILE16 - 1;
-                pf[k] = yt[(size_t)t * TILE16 + idx];
-            }
-            pc = fmaxf(cs * fmaf(beta, a.v[t * 32 + cj], alpha * cu[t * 32 + cj]), kPadScore);
+        for (int k = 0; k < PER_THREAD; ++k)
+            offb[k] = (unsigned)(tid + k * kBlockK < TILE16 ? tid + k * kBlockK : TILE16 - 1) * 16u;
+        T pf[NSETS][TPS][PER_THREAD];
+        float pv[NSETS], pu[NSETS];
+        auto tile_ptr = [&](int t) { return reinterpret_cast<const char*>(yt + (size_t)(t < te ? t : last) * TILE16); };
+        auto prefetch_tile = [&](int s, int tt, int t0) {
+            const char* src = tile_ptr(t0 + tt);
+#pragma unroll
+            for (int k = 0; k < PER_THREAD; ++k) pf[s][tt][k] = *reinterpret_cast<const T*>(src + offb[k]);
         };
-        auto stage = [&](int buf, int cbuf) {
+        auto prefetch_cols = [&](int s, int t0) {
+            const int t = t0 + cl / 32 < te ? t0 + cl / 32 : last;
+            pv[s] = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(a.v + t * 32) + (cl % 32) * 4);
+            pu[s] = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(cu + t * 32) + (cl % 32) * 4);
+        };
+        auto stage_tile = [&](int s, int tt, int ybuf) {
+            char* dst = reinterpret_cast<char*>(lds_y + (ybuf * TPS + tt) * TILE16);
 #pragma unroll
-            for (int k = 0; k < PER_THREAD; ++k) {
-                const int idx = tid + k * kBlockK < TILE16 ? tid + k * kBlockK : TILE16 - 1;
-                lds_y[buf * TILE16 + idx] = pf[k];
-            }
+            for (int k = 0; k < PER_THREAD; ++k) *reinterpret_cast<T*>(dst + offb[k]) = pf[s][tt][k];
+        };
+        auto stage_cols = [&](int s, int cbuf) {
+            const float pc = fmaxf(cs * fmaf(beta, pv[s], alpha * pu[s]), kPadScore);
             if constexpr (FOLD) {
                 const __bf16 q0 = (__bf16)pc;
                 const float r1 = pc - (float)q0;                  // exact
                 const __bf16 q1 = (__bf16)r1;
-                const __bf16 q2 = (__bf16)(r1 - (float)q1);       // exact: at most 8 bits remain
-                reinterpret_cast<bf16x8*>(lds_col)[cbuf * 32 + cj] = bf16x8{q0, q1, q2, 0, 0, 0, 0, 0};
+                const __bf16 q2 = (__bf16)(r1 - (float)q1);       // exact: at most 8 significant bits remain
+                reinterpret_cast<bf16x8*>(lds_col)[cbuf * TPS * 32 + cl] = bf16x8{q0, q1, q2, 0, 0, 0, 0, 0};
             } else {
-                lds_col[cbuf * 32 + cj] = pc;
+                lds_col[cbuf * TPS * 32 + cl] = pc;
             }
         };
-        T yv[NC][kPieces];
-        auto read_tile = [&](int buf) {
+        auto prefetch = [&](int s, int t0) {
 #pragma unroll
-            for (int cc = 0; cc < NC; ++cc)
+            for (int tt = 0; tt < TPS; ++tt) prefetch_tile(s, tt, t0);
+            prefetch_cols(s, t0);
+        };
+        auto stage = [&](int s, int ybuf, int cbuf) {
 #pragma unroll
-                for (int p = 0; p < kPieces; ++p) yv[cc][p] = lds_y[buf * TILE16 + (cc * kPieces + p) * 64 + lane];
+            for (int tt = 0; tt < TPS; ++tt) stage_tile(s, tt, ybuf);
+            stage_cols(s, cbuf);
+        };
+        // The ring of column chunks: slot g % D holds chunk g of the current pair of tiles.
+        T yr[D][kPieces];
+        auto read_chunk = [&](auto G, int ytile) {
+            constexpr int g = decltype(G)::value;
+            constexpr int cc = g % NC;
+#pragma unroll
+            for (int p = 0; p < kPieces; ++p) yr[g % D][p] = lds_y[ytile * TILE16 + (cc * kPieces + p) * 64 + lane];
         };
         // With FOLD, the B operand of the column MFMA: 1 in k = 0, 1, 2 of every row (lanes 0-31), zeros elsewhere.
         const __bf16 one = h == 0 ? (__bf16)1.0f : (__bf16)0.0f;
@@ -335,11 +393,22 @@ struct Staged {
 
         f32x16 accA[RB], accB[RB];
         Online<RB, L2, FOLD> on;
-        // One tile: MFMAs into accN from zero, then (FOLD) the column MFMA with the tile's column terms from column
-        // buffer cbn; with `epi`, the update of the previous tile (accP, its column terms at colp) is spread between
-        // them, one slot per MFMA, fenced so the compiler keeps the interleave.
-        auto tile = [&](f32x16 (&accN)[RB], f32x16 (&accP)[RB], const float* colp, int cbn, bool epi) {
+        // Ring positions of the current step: LDS buffers yq = q % 3 and cq = q % 4.
+        int yq = 0, cq = 0;
+        auto nxt3 = [](int v) { return v == 2 ? 0 : v + 1; };
+        auto nxt4 = [](int v) { return (v + 1) & 3; };
+        // Tile t of phase PH (t - tb even: 0, odd: 1), tile TT = PH % TPS of its step: MFMAs into accN from zero,
+        // the column MFMA, and (epi) the update of the previous tile (accP, its column terms at colp) spread
+        // between them, one slot per MFMA, fenced so that the compiler keeps the interleave. The step's first
+        // tile stages step q + 2 and loads step q + 2 + NSETS.
+        auto tile = [&](auto PH, int t, f32x16 (&accN)[RB], f32x16 (&accP)[RB], const float* colp, bool epi) {
+            constexpr int ph = decltype(PH)::value;
+            constexpr int tt = ph % TPS;
             auto col4 = [&](int q) { return *reinterpret_cast<const f32x4*>(colp + 8 * q); };
+            const int ycur = yq * TPS + tt;                                   // LDS tile of this tile
+            const int ynext = tt + 1 < TPS ? ycur + 1 : nxt3(yq) * TPS;      // and of the next
+            bf16x8 colA;
+            if constexpr (FOLD) colA = reinterpret_cast<const bf16x8*>(lds_col)[(cq * TPS + tt) * 32 + (lane & 31)];
 #pragma unroll
             for (int b = 0; b < RB; ++b) accN[b] = f32x16{};
             static_for<0, NS>([&](auto I) {
@@ -347,16 +416,35 @@ struct Staged {
                 constexpr int cc = i / (kProducts * RB), p = (i / RB) % kProducts, b = i % RB;
                 constexpr int rp = ROLE == 0 ? C::first[p] : C::second[p];
                 constexpr int cp = ROLE == 0 ? C::second[p] : C::first[p];
-                accN[b] = C::mfma(yv[cc][cp], xv[b][cc][rp], accN[b]);
+                constexpr int g = ph * NC + cc;           // this chunk's place in the pair of tiles
+                if constexpr (p == 0 && b == 0) {
+                    // the chunk LA ahead: of this tile, or the first ones of the next
+                    if constexpr (cc + LA < NC)
+                        read_chunk(std::integral_constant<int, (g + LA) % (2 * NC)>{}, ycur);
+                    else
+                        read_chunk(std::integral_constant<int, (g + LA) % (2 * NC)>{}, ynext);
+                }
+                accN[b] = C::mfma(yr[g % D][cp], xv[b][cc][rp], accN[b]);
                 if (epi) {
                     constexpr int k0 = op_begin<RB, FOLD>(i, NS), k1 = op_begin<RB, FOLD>(i + 1, NS);
                     static_for<k0, k1>([&](auto K) { on.template step<decltype(K)::value>(accP, col4, M, S, c); });
+                }
+                // The step's staging, spread over a few slots: each tile's units (and the column terms) are written
+                // out before the same registers are loaded again.
+                if constexpr (tt == 0) {
+                    constexpr int s = NSETS == 1 ? 0 : ph;
+                    if constexpr (i == kStageSlot - 2) stage_cols(s, nxt4(nxt4(cq)));
+                    static_for<0, TPS>([&](auto U) {
+                        constexpr int u = decltype(U)::value;
+                        if constexpr (i == kStageSlot + 2 * u) stage_tile(s, u, nxt3(nxt3(yq)));
+                        if constexpr (i == kStageSlot + 2 * u + 1) prefetch_tile(s, u, t + (2 + NSETS) * TPS);
+                    });
+                    if constexpr (i == kStageSlot + 2 * TPS) prefetch_cols(s, t + (2 + NSETS) * TPS);
                 }
                 __builtin_amdgcn_sched_barrier(0);
             });
             // The column terms last, after the whole dot product: x.y is formed identically in both directions.
             if constexpr (FOLD) {
-                const bf16x8 colA = reinterpret_cast<const bf16x8*>(lds_col)[cbn * 32 + (lane & 31)];
 #pragma unroll
                 for (int b = 0; b < RB; ++b)
                     accN[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(colA, colB, accN[b], 0, 0, 0);
@@ -366,49 +454,58 @@ struct Staged {
             auto col4 = [&](int q) { return *reinterpret_cast<const f32x4*>(colp + 8 * q); };
             static_for<0, RB * kOps>([&](auto K) { on.template step<decltype(K)::value>(accP, col4, M, S, c); });
         };
-        auto colp_of = [&](int cbuf) { return lds_col + cbuf * 32 + 4 * h; };
-
-        // Tiles in pairs so the accumulator roles alternate without copies. Tile t sits in operand buffer
-        // (t - tb) & 1 and column buffer (t - tb) % 3; every prefetch / stage is unconditional (after the last
-        // tile the last one is staged again).
-        const int last = te - 1;
-        prefetch(tb);
-        stage(0, 0);
-        __syncthreads();
-        int t = tb;
-        int cb = 0;                            // column buffer of tile t
-        read_tile(0);
-        prefetch(t + 1 < te ? t + 1 : last);
-        tile(accA, accB, nullptr, 0, false);
-        stage(1, 1);
-        __syncthreads();
-        ++t;
-        while (t < te) {
-            int cn = cb == 2 ? 0 : cb + 1;     // tile t
-            int cn2 = cn == 2 ? 0 : cn + 1;    // tile t + 1
-            read_tile((t - tb) & 1);
-            prefetch(t + 1 < te ? t + 1 : last);
-            tile(accB, accA, colp_of(cb), cn, true);
-            stage((t + 1 - tb) & 1, cn2);
-            __syncthreads();
-            ++t;
-            cb = cn;
-            if (t >= te) {
-                update(accB, colp_of(cb));
-                goto done;
+        // Column terms (without FOLD) of tile tt of the step in column buffer cbuf.
+        auto colp_of = [&](int cbuf, int tt) { return lds_col + (cbuf * TPS + tt) * 32 + 4 * h; };
+        // After a tile: to the next step (every TPS tiles) and a barrier there.
+        auto advance = [&](auto PH) {
+            constexpr int ph = decltype(PH)::value;
+            if constexpr (ph % TPS == TPS - 1) {
+                yq = nxt3(yq);
+                cq = nxt4(cq);
+                __syncthreads();
             }
-            cn = cb == 2 ? 0 : cb + 1;
-            cn2 = cn == 2 ? 0 : cn + 1;
-            read_tile((t - tb) & 1);
-            prefetch(t + 1 < te ? t + 1 : last);
-            tile(accA, accB, colp_of(cb), cn, true);
-            stage((t + 1 - tb) & 1, cn2);
-            __syncthreads();
-            ++t;
-            cb = cn;
+        };
+
+        // Prologue: steps 0 and 1 staged, steps 2 .. 1 + NSETS in the register sets, the first chunks of tile tb
+        // read. Every prefetch / stage is unconditional (tiles past the last one are the last one again).
+        if constexpr (NSETS == 2) {
+            prefetch(0, tb);
+            prefetch(1, tb + TPS);
+            stage(0, 0, 0);
+            stage(1, 1, 1);
+            prefetch(0, tb + 2 * TPS);
+            prefetch(1, tb + 3 * TPS);
+        } else {
+            prefetch(0, tb);
+            stage(0, 0, 0);
+            prefetch(0, tb + TPS);
+            stage(0, 1, 1);
+            prefetch(0, tb + 2 * TPS);
         }
-        update(accA, colp_of(cb));
-    done:
+        __syncthreads();
+        static_for<0, LA>([&](auto G) { read_chunk(G, 0); });
+        int t = tb;
+        tile(std::integral_constant<int, 0>{}, t, accA, accB, nullptr, false);
+        advance(std::integral_constant<int, 0>{});
+        ++t;
+        // Tiles in pairs (phase 1 then phase 0), so that the accumulators keep their registers; the column terms
+        // of the tile before (without FOLD) are in column buffer cq - 1 after a step boundary, else cq.
+        while (te - t >= 2) {
+            tile(std::integral_constant<int, 1>{}, t, accB, accA, colp_of(TPS == 1 ? (cq + 3) & 3 : cq, 0), true);
+            advance(std::integral_constant<int, 1>{});
+            tile(std::integral_constant<int, 0>{}, t + 1, accA, accB, colp_of((cq + 3) & 3, TPS - 1), true);
+            advance(std::integral_constant<int, 0>{});
+            t += 2;
+        }
+        if (t < te) {
+            tile(std::integral_constant<int, 1>{}, t, accB, accA, colp_of(TPS == 1 ? (cq + 3) & 3 : cq, 0), true);
+            advance(std::integral_constant<int, 1>{});
+            update(accB, colp_of((cq + 3) & 3, TPS - 1));
+        } else {
+            update(accA, colp_of(TPS == 1 ? (cq + 3) & 3 : cq, 0));
+        }
+        // The next segment's prologue rewrites the first buffers: every wave is done with them first.
+        __syncthreads();
         store_rows<RB, L2>(a, M, S, rb0, slot, c, inv_sigma, lane);
     }
 };
@@ -705,8 +802,8 @@ void lse_partial_kernel(PartialArgs a) {
     asm volatile("" ::"s"(sc0), "s"(sc2), "s"(sx), "s"(sy), "s"(cb), "s"(cb_s2), "v"(skip));
     if (skip != 0) return;
     constexpr bool kStream = NC <= kStreamMaxChunks;
-    constexpr int kLdsY = kStream ? 1 : 2 * NC * Contract<CT>::pieces * 64;
-    constexpr int kLdsCol = kStream ? col_floats(CT == kF16x2) : 3 * 32 * (CT == kF16x2 ? 4 : 1);
+    constexpr int kLdsY = kStream ? 1 : 3 * staged_step_tiles(CT) * NC * Contract<CT>::pieces * 64;
+    constexpr int kLdsCol = kStream ? col_floats(CT == kF16x2) : 4 * staged_step_tiles(CT) * 32 * (CT == kF16x2 ? 4 : 1);
     __shared__ typename Contract<CT>::T lds_y[kLdsY];
     __shared__ __attribute__((aligned(16))) float lds_col[kLdsCol];
     const int wv = __builtin_amdgcn_readfirstlane(tid_x() >> 6);   // one value per wave

@@ -604,15 +604,20 @@ def test_three_products_are_fp32_accurate_and_symmetric():
 
 
 def bake_log2(xs, sx, sy, mx, c):
-    """sk_epilogue.h bake_params / bake_unit: the first cloud's log2-unit copy, pieces of fl(c x) / s_y where
-    x = (x0 + x1) / s_x; None where the copy would leave fp16's full-precision range."""
+    """sk_epilogue.h bake_params / bake_unit: the first cloud's log2-unit copy, pieces of t fl(c x) / s_y where
+    x = (x0 + x1) / s_x, and its unit t (1 while max |fl(c x)| / s_y lies in [2^-1, 2^15), else the power of two
+    that brings it into [2^4, 2^5), within [2^-40, 2^40]); None where no unit fits."""
     c = np.float32(c)
     wmax = np.float32(np.float32(c * np.float32(mx)) * np.float32(1.0 / sy))
-    if not (c > 0 and 0.5 <= wmax < 32768.0):
+    t = np.float32(1.0)
+    if wmax > 0 and not (0.5 <= wmax < 32768.0):
+        e = np.frexp(wmax)[1]
+        t = np.float32(np.ldexp(1.0, int(np.clip(5 - e, -40, 40))))
+    if not (c > 0 and 0.5 <= wmax * t < 32768.0):
         return None
     x = ((xs[0] + xs[1]).astype(np.float32) * np.float32(1.0 / sx)).astype(np.float32)
-    w = ((c * x).astype(np.float32) * np.float32(1.0 / sy)).astype(np.float32)
-    return split2(w)
+    w = (((c * x).astype(np.float32) * np.float32(1.0 / sy)).astype(np.float32) * t).astype(np.float32)
+    return split2(w), t
 
 
 @pytest.mark.parametrize("eps,shift", [(0.1, 0.5), (0.01, 0.0), (1.0, 0.0), (0.05, 3.0)])
@@ -627,8 +632,8 @@ def test_log2_copy_gives_c_x_dot_y_to_fp32_accuracy(eps, shift):
     sx, sy = pack_scale(np.abs(x).max()), pack_scale(np.abs(y).max())
     xs, ys = split2(x * sx), split2(y * sy)
     c = np.float32(np.float32(2.0 / eps) * np.float32(np.log2(np.e)))
-    ws = bake_log2(xs, sx, sy, np.abs(x).max(), c)
-    assert ws is not None
+    ws, t = bake_log2(xs, sx, sy, np.abs(x).max(), c)
+    assert t == 1.0
     for p in range(2):
         np.testing.assert_array_equal(ws[p], ws[p].astype(np.float16).astype(np.float32))
     exact = float(c) * (x.astype(np.float64) @ y.astype(np.float64).T)
@@ -647,17 +652,34 @@ def test_log2_copy_gives_c_x_dot_y_to_fp32_accuracy(eps, shift):
     np.testing.assert_array_equal(accumulate(ws, ys, FIRST, SECOND), accumulate(ys, ws, SECOND, FIRST).T)
 
 
-def test_log2_copy_validity_window():
-    """The copy is made only while max |fl(c x)| / s_y stays in [2^-1, 2^15); outside it the pair scales on
-    the VALU (header tag 0)."""
+def test_log2_copy_unit_and_window():
+    """The copy's unit: t = 1 while max |fl(c x)| / s_y stays in [2^-1, 2^15) (the pieces then hold the
+    copy as before), a power of two bringing it into [2^4, 2^5) outside that window (tiny or huge score
+    scales), and no copy only for c = 0 or past the unit's range. With any unit the three piece products
+    divided by t give c x.y to fp32 accuracy; without the rescaling (a planted mistake) they are off by t."""
     rng = np.random.default_rng(4)
     y = rng.normal(size=(20, 8)).astype(np.float32)
     sy = pack_scale(np.abs(y).max())
-    for mag, c, ok in [(1.0, 28.85, True), (1e-6, 28.85, False), (1e6, 288.5, False), (30.0, 2.885, True),
-                       (1.0, 0.0, False)]:
+    ys = split2(y * sy)
+    for mag, c, unit in [(1.0, 28.85, "one"), (1e-6, 28.85, "up"), (1e6, 288.5, "down"), (30.0, 2.885, "one"),
+                         (3e-3, 2.885, "up"), (1.0, 0.0, None), (1e-30, 1e-8, None)]:
         x = (rng.normal(size=(20, 8)) * mag).astype(np.float32)
         sx = pack_scale(np.abs(x).max())
-        assert (bake_log2(split2(x * sx), sx, sy, np.abs(x).max(), c) is not None) == ok, (mag, c)
+        got = bake_log2(split2(x * sx), sx, sy, np.abs(x).max(), c)
+        if unit is None:
+            assert got is None, (mag, c)
+            continue
+        ws, t = got
+        wmax = np.float32(np.float32(np.float32(c) * np.abs(x).max()) / sy)
+        assert {"one": t == 1.0, "up": t > 1.0, "down": t < 1.0}[unit], (mag, c, t)
+        if unit != "one":
+            assert 16.0 <= wmax * t < 32.0
+        exact = float(np.float32(c)) * (x.astype(np.float64) @ y.astype(np.float64).T)
+        bound = float(np.float32(c)) * (np.abs(x.astype(np.float64)) @ np.abs(y.astype(np.float64)).T)
+        approx = sum(ws[FIRST[p]].astype(np.float64) @ ys[SECOND[p]].astype(np.float64).T for p in range(3))
+        assert np.max(np.abs(approx / t - exact) / bound) < 2.0 ** -21, (mag, c)
+        if t != 1.0:
+            assert np.max(np.abs(approx - exact) / bound) > 0.4
 
 
 @pytest.mark.parametrize("ct", ["f16x2", "bf16x3"])

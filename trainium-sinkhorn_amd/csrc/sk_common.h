@@ -81,10 +81,11 @@ __host__ __device__ inline int last_wg(int g, const Split& s) { return owner_of(
 // A packed cloud: a 256-byte header of 32-bit words
 //     [0] max |coordinate| (float bits), [1] s, the power-of-two scale of the cloud's own pieces (1 for kBF16x3),
 //     [2] c_b, the score scale its log2-unit copy was made for (0: no valid copy),
-//     [3] the scale of the second cloud that copy was made against,
+//     [3] the scale of the second cloud that copy was made against, [4] the copy's unit t (a power of two),
 // then the tiles of the cloud's own pieces (s x), then (kF16x2 only) the tiles of its log2-unit copy: two fp16
-// pieces of fl(c_b x) / s_2 per coordinate, which the first cloud of a pair carries so that its piece products
-// with the second cloud's own pieces sum to c_b x.y, the half-step's score in log2 units (see bake_log2).
+// pieces of t fl(c_b x) / s_2 per coordinate, which the first cloud of a pair carries so that its piece products
+// with the second cloud's own pieces sum to t c_b x.y, the half-step's score in log2 units times t (see
+// bake_params in sk_epilogue.h).
 template <class T>
 __host__ __device__ inline const T* packed_tiles(const void* pk) {
     return reinterpret_cast<const T*>(reinterpret_cast<const char*>(pk) + kHeaderBytes);

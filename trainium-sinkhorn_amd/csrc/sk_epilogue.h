@@ -80,13 +80,17 @@ __device__ __forceinline__ void st(T* p, T v) {
 
 // The first cloud's log2-unit copy for score scale c = (2 / eps) log2(e) = sc[0] log2(e), against the second
 // cloud's scale s2: every coordinate x, as the cloud's own pieces hold it (x = (v0 + v1) / s1, exact), becomes
-// w = fl(c x) / s2 in two fp16 pieces (w0 = fp16(w), w1 = fp16(w - w0)). Products with the second cloud's own
-// pieces (s2 y) then sum to c x.y in fp32, the score in log2 units, so the exponentials need no scaling; the
-// f and g updates both use this copy, in the same product order, and stay bit-identical. The copy is valid
-// (header c_b = c, [3] = s2) when max |w| = fl(c max |x|) / s2 lies in [2^-1, 2^15): within fp16's range
-// and with w1 normal for the largest coordinates; otherwise c_b = 0 and the half-steps scale on the VALU.
+// w = t fl(c x) / s2 in two fp16 pieces (w0 = fp16(w), w1 = fp16(w - w0)), with t a power of two, the copy's
+// unit. Products with the second cloud's own pieces (s2 y) then sum to t c x.y in fp32: the score in log2 units
+// times t, so that the exponentials need no more than an exact power-of-two rescaling, fused with the max
+// subtraction (exp2(t^-1 a - t^-1 m), one fma); the f and g updates both use this copy, in the same product
+// order, and stay bit-identical. t = 1 while max |fl(c x)| / s2 lies in [2^-1, 2^15) (within fp16's range and
+// with w1 normal for the largest coordinates); outside that window t brings max |w| into [2^4, 2^5), as the
+// packing scale does for the clouds' own pieces. The copy is valid (header c_b = c, [3] = s2, [4] = t) for
+// every c > 0 and every cloud whose max |w| reaches that range with t in [2^-40, 2^40]; otherwise c_b = 0 and
+// the half-steps scale on the VALU.
 struct BakeParams {
-    float c, inv_s1, inv_s2;
+    float c, inv_s1, inv_s2, t;
     bool valid;
 };
 
@@ -98,7 +102,15 @@ __device__ inline BakeParams bake_params(const void* first, const void* second, 
     b.inv_s1 = 1.0f / s1;                                   // powers of two: exact
     b.inv_s2 = 1.0f / s2;
     const float wmax = (b.c * __uint_as_float(reinterpret_cast<const unsigned*>(first)[0])) * b.inv_s2;
-    b.valid = b.c > 0.0f && wmax >= 0.5f && wmax < 32768.0f;
+    b.t = 1.0f;
+    if (wmax > 0.0f && (wmax < 0.5f || wmax >= 32768.0f)) {
+        int e;
+        frexpf(wmax, &e);                                   // wmax in [2^(e-1), 2^e)
+        const int k = 5 - e;
+        b.t = ldexpf(1.0f, k < -40 ? -40 : (k > 40 ? 40 : k));
+    }
+    const float tw = wmax * b.t;                            // exact
+    b.valid = b.c > 0.0f && tw >= 0.5f && tw < 32768.0f;
     return b;
 }
 
@@ -113,7 +125,7 @@ __device__ inline void bake_unit(char* first, long long idx, int npad, int nc, c
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
         const float x = ((float)p0[e] + (float)p1[e]) * b.inv_s1;
-        const float w = (b.c * x) * b.inv_s2;
+        const float w = ((b.c * x) * b.inv_s2) * b.t;     // one rounding (c x), then exact scalings
         const _Float16 a0 = (_Float16)w;
         q0[e] = a0;
         q1[e] = (_Float16)(w - (float)a0);
@@ -126,6 +138,7 @@ __device__ inline void bake_header(char* first, const void* second, const BakePa
     float* h = reinterpret_cast<float*>(first);
     h[2] = b.valid ? b.c : 0.0f;
     h[3] = packed_scale(second);
+    h[4] = b.valid ? b.t : 1.0f;
 }
 
 // eps of the iteration that starts with `it` iterations done (sinkhorn.py:347-350).

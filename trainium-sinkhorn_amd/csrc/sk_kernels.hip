@@ -103,6 +103,7 @@ __global__ void pack_header_kernel(unsigned* __restrict__ header) {
         header[1] = __float_as_uint(1.0f);
         header[2] = 0u;                     // no log2-unit copy yet
         header[3] = 0u;
+        header[4] = __float_as_uint(1.0f);  // the copy's unit
     }
 }
 

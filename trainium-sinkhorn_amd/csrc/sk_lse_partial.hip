@@ -15,9 +15,10 @@
 // an fp32 dot product (error ~1e-7 of sum |x_k y_k| on N(0, 1) data; a float32 dot product gives ~2.3e-7,
 // the fp32 MFMA chain 3.2e-7). With sigma = s_x s_y, the kernel works in scaled accumulator units
 // sigma a = D + sigma (column term) and c / sigma, all exact power-of-two rescalings, and stores M / sigma.
-// When the first cloud carries its log2-unit copy (pieces of fl(c x) / s_y) for this launch's c, the same
-// three products of the copy and the second cloud's own pieces give c x.y: the scores are in log2 units and
-// the exponentials take them without a multiply (L2 below); M is stored in log2 units.
+// When the first cloud carries its log2-unit copy (pieces of t fl(c x) / s_y, t a power of two) for this
+// launch's c, the same three products of the copy and the second cloud's own pieces give t c x.y: the scores
+// are in log2 units times t and the exponentials take them with one fma that subtracts the max and rescales
+// by 1 / t exactly (L2 below); M is stored in log2 units.
 // On gfx950 the fp16 matrix pipe runs at ~15x the fp32 MFMA rate and, unlike the fp32 MFMA, issues alongside
 // VALU work of the same SIMD, so the exp / max / sum epilogue of one tile hides under the MFMAs of the next.
 // The general row log-sum-exp of arbitrary fp32 matrices (whose columns may mix magnitudes 1e9 apart, as the
@@ -129,7 +130,8 @@ __device__ __forceinline__ void static_for(F&& f) {
 // term is exactly 1 and S is relative to 2^(c M) exactly, which is what the merge of the slots assumes.
 // (Folding the offset into one fma, exp2(c a - fl(c m)), would leave S relative to the rounded fl(c M): an
 // error of up to half an ulp of c M in the log-sum-exp, which moves with M from one iteration to the next
-// and holds float32 Sinkhorn several ulps away from its fixed point.)
+// and holds float32 Sinkhorn several ulps away from its fixed point. With L2, c is a power of two, c m is
+// exact, and the fma is exactly c (a - m).)
 // Steps are spread over the MFMA slots of the next tile in proportion to their cost.
 constexpr int kOps = 57;
 template <bool FOLD>
@@ -155,10 +157,13 @@ constexpr int op_begin(int i, int NS) {
 }
 
 // col4(q) returns the column terms of accumulators 4q .. 4q + 3 of the tile being updated (unused with FOLD).
-// With L2 the scores are already in log2 units (the first cloud's log2-unit copy) and c is not applied.
+// With L2 the scores are in log2 units times the copy's unit t (the first cloud's log2-unit copy) and c = 1 / t,
+// a power of two: the max is subtracted and the rescaling applied by one fma, exp2(fma(a, c, -c m)), exact in
+// c m and equal to exp2(c (a - m)) bit for bit (for t = 1, exp2(a - m)).
 template <int RB, bool L2, bool FOLD = false>
 struct Online {
     float m[RB];
+    float mc[RB];      // L2: c m
     f32x4 cv[4];
     template <int k, class ColFn>
     __device__ __forceinline__ void step(f32x16 (&acc)[RB], ColFn&& col4, float (&M)[RB], float (&S)[RB], float c) {
@@ -183,7 +188,12 @@ struct Online {
                 m[b] = max3(m[b], acc[b][2 * p], acc[b][2 * p + 1]);
         } else if constexpr (j < 41) {
             constexpr int r = j - 25;
-            acc[b][r] = L2 ? ex2(acc[b][r] - m[b]) : ex2(c * (acc[b][r] - m[b]));
+            if constexpr (L2) {
+                if constexpr (r == 0) mc[b] = m[b] * c;
+                acc[b][r] = ex2(fmaf(acc[b][r], c, -mc[b]));
+            } else {
+                acc[b][r] = ex2(c * (acc[b][r] - m[b]));
+            }
         } else if constexpr (j < 56) {
             // tree level l (stride 2^l) pairs acc[2^(l+1) q] += acc[2^(l+1) q + 2^l]
             constexpr int t = j - 41;
@@ -192,7 +202,7 @@ struct Online {
             constexpr int lo = q << (l + 1), hi = lo + (1 << l);
             acc[b][lo] = acc[b][lo] + acc[b][hi];
         } else {
-            S[b] = fmaf(S[b], ex2(L2 ? M[b] - m[b] : c * (M[b] - m[b])), acc[b][0]);
+            S[b] = fmaf(S[b], ex2(L2 ? fmaf(M[b], c, -mc[b]) : c * (M[b] - m[b])), acc[b][0]);
             M[b] = m[b];
         }
     }
@@ -226,7 +236,7 @@ struct Contract<kBF16x3> {
 };
 
 // End of a work segment: lanes l and l + 32 hold the same row over different columns; merge them and store
-// (M / sigma, S) of each row, or with L2 (M, S) in log2 units.
+// (M / sigma, S) of each row (with L2, sigma is the copy's unit t and M / t is in log2 units).
 template <int RB, bool L2>
 __device__ __forceinline__ void store_rows(const PartialArgs& a, const float (&M)[RB], const float (&S)[RB], int rb0,
                                            int slot, float c, float inv_sigma, int lane) {
@@ -235,13 +245,12 @@ __device__ __forceinline__ void store_rows(const PartialArgs& a, const float (&M
         const float Mo = __shfl_xor(M[b], 32);
         const float So = __shfl_xor(S[b], 32);
         const float Mn = fmaxf(M[b], Mo);
-        const float Sn = L2 ? S[b] * ex2(M[b] - Mn) + So * ex2(Mo - Mn)
-                            : S[b] * ex2(c * (M[b] - Mn)) + So * ex2(c * (Mo - Mn));
+        const float Sn = S[b] * ex2(c * (M[b] - Mn)) + So * ex2(c * (Mo - Mn));
         if (lane < 32 && rb0 + b < a.nrb) {
             float2* dst = a.part + (size_t)slot * a.rows_pad + (size_t)(rb0 + b) * 32 + lane;
             // (a segment whose columns all have zero weight has M near the -1e30 floor; kept finite when
             // rescaled, as an empty slot)
-            const float2 v = make_float2(L2 ? Mn : fmaxf(Mn * inv_sigma, kEmpty), Sn);
+            const float2 v = make_float2(fmaxf(Mn * inv_sigma, kEmpty), Sn);
             if (a.group_counters != nullptr)
                 coh_store(dst, v);           // read back in this launch by the group's last workgroup
             else
@@ -757,7 +766,7 @@ __device__ inline void arrive(const PartialArgs& a, int g) {
 }
 
 // The work segments of workgroup p: a_ij = x_i . y_j + cs (alpha cu_j + beta v_j) in the kernel's units, scores
-// exp2(c (a - M)) (with L2: exp2(a - M), a already in log2 units).
+// exp2(c (a - M)) (with L2: exp2(fma(a, c, -c M)), a in log2 units times the copy's unit t = 1 / c).
 template <int NC, int ROLE, int CT, bool L2>
 __device__ __forceinline__ void segments(const PartialArgs& a, int p, int wv, const float* cu, float alpha, float beta,
                                          float cs, float c, float inv_sigma, typename Contract<CT>::T* lds_y,
@@ -793,13 +802,13 @@ void lse_partial_kernel(PartialArgs a) {
     const float* h1 = reinterpret_cast<const float*>(ROLE == 0 ? a.xr : a.yc);   // the first cloud's header
     const float sc0 = a.sc[0], sc2 = a.sc[2];                         // a.sc is valid in both modes
     const float sx = packed_scale(a.xr), sy = packed_scale(a.yc);   // 1 for kBF16x3
-    const float cb = h1[2], cb_s2 = h1[3];
+    const float cb = h1[2], cb_s2 = h1[3], cb_t = h1[4];
     const int skip = *skip_p;
     // The argument fields the segments need, requested with the first batch of argument loads rather than
     // after the scalars have arrived.
     asm volatile("" ::"s"(a.nrb), "s"(a.rows_pad), "s"(a.mode), "s"(a.s.nt), "s"(a.s.P), "s"(a.s.alpha),
                  "s"(a.s.ftot), "s"(a.s.q), "s"(a.s.r), "s"(a.group_counters));
-    asm volatile("" ::"s"(sc0), "s"(sc2), "s"(sx), "s"(sy), "s"(cb), "s"(cb_s2), "v"(skip));
+    asm volatile("" ::"s"(sc0), "s"(sc2), "s"(sx), "s"(sy), "s"(cb), "s"(cb_s2), "s"(cb_t), "v"(skip));
     if (skip != 0) return;
     constexpr bool kStream = NC <= kStreamMaxChunks;
     constexpr int kLdsY = kStream ? 1 : 3 * staged_step_tiles(CT) * NC * Contract<CT>::pieces * 64;
@@ -822,17 +831,20 @@ void lse_partial_kernel(PartialArgs a) {
         beta = 0.0f;
         c = kLog2e;
     }
-    // With a valid log2-unit copy of the first cloud for this c (log2_ready), the matrix cores produce c x.y and
-    // the exponentials take the scores as they are. The column term c (gh / 2 + eps log b / 2) then comes from
-    // the column cloud's potential in log2 units R = (c / 2) gh when the caller keeps one (u2, the on-device
-    // loop: R + log2(e) log b, one rounding), else from gh, scaled by c. Otherwise the kernel works in units
-    // scaled by sigma = s_rows s_cols (a power of two): column terms times sigma, c divided by it.
+    // With a valid log2-unit copy of the first cloud for this c (log2_ready), the matrix cores produce t c x.y
+    // (t, the copy's unit, a power of two; 1 for the usual score scales) and the exponentials take the scores
+    // with the exact rescaling by 1 / t fused into the max subtraction. The column term
+    // t c (gh / 2 + eps log b / 2) then comes from the column cloud's potential in log2 units R = (c / 2) gh
+    // when the caller keeps one (u2, the on-device loop: t (R + log2(e) log b), one rounding), else from gh,
+    // scaled by t c. Otherwise the kernel works in units scaled by sigma = s_rows s_cols (a power of two):
+    // column terms times sigma, c divided by it.
     if constexpr (CT == kF16x2) {
         if (a.mode == kHalfStep && cb != 0.0f && cb == c && cb_s2 == (ROLE == 0 ? sy : sx)) {
+            const float it = 1.0f / cb_t;                  // exact
             if (a.u2 != nullptr)
-                segments<NC, ROLE, CT, true>(a, p, wv, a.u2, 1.0f, kLog2e, 1.0f, 1.0f, 1.0f, lds_y, lds_col);
+                segments<NC, ROLE, CT, true>(a, p, wv, a.u2, 1.0f, kLog2e, cb_t, it, it, lds_y, lds_col);
             else
-                segments<NC, ROLE, CT, true>(a, p, wv, a.u, alpha, beta, c, 1.0f, 1.0f, lds_y, lds_col);
+                segments<NC, ROLE, CT, true>(a, p, wv, a.u, alpha, beta, c * cb_t, it, it, lds_y, lds_col);
             return;
         }
     }

@@ -2,6 +2,7 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
     python bench.py --profile [--reps R]     # for rocprofv3: R loop iterations, then a 256 MiB copy
+    python bench.py --profile --workload stress-65k [--reps R]   # the same on the 65k d 128 stress clouds
     python bench.py --workload {single-cell, single-cell-pipeline, stress-65k} [--no-cpu]
 
 Workload: synthetic balanced 10,000 x 10,000, d = 64, fp32, x ~ N(0, 1) (seed 0), y ~ N(0, 1) + 0.5
@@ -130,6 +131,36 @@ def profile_run(reps):
     dst.copy_(src)
     torch.cuda.synchronize()
     print(f"profile: {reps} loop iterations of {N} x {M} d {D}, then a 256 MiB copy", flush=True)
+
+
+def profile_stress(reps, eps=0.01):
+    """The stress counterpart of profile_run: `reps` iterations of the on-device loop on the 65,536 x 65,536 d 128
+    mixture clouds (median-normalised, uniform weights) at one eps (the staged partial kernel, kp 128), then the
+    same 256 MiB copy."""
+    import numpy as np
+    import torch
+    from trnopt import hip_sinkhorn as hk
+    from trnopt.sinkhorn import normalization
+
+    hk.lib()
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    x, y = stress_inputs()
+    center, scale = normalization(x, y, how="median")
+    xs, ys = (x - center) / np.sqrt(scale), (y - center) / np.sqrt(scale)
+    n = len(xs)
+    X = hk.HipCloud(xs, np.full(n, -np.log(n)), dev, role=0)
+    Y = hk.HipCloud(ys, np.full(n, -np.log(n)), dev, role=1)
+    loop = hk.DeviceLoop(X, Y, eps=eps, rho_x=None, rho_y=None, sched=[], stages=[], tol=1e-4, stage_tol=1e-5,
+                         max_iters=reps + 1, check_every=10, stage_max_iters=1000, fixed_iters=True, balanced=True)
+    loop.init()
+    loop.enqueue(reps)
+    src = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"profile: {reps} loop iterations of {n} x {n} d 128 at eps {eps}, then a 256 MiB copy", flush=True)
 
 
 def _cpu_model():
@@ -339,7 +370,12 @@ def main():
               "only); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
     if a.profile:
-        profile_run(a.reps)
+        if a.workload == "stress-65k":
+            profile_stress(a.reps)
+        elif a.workload is None:
+            profile_run(a.reps)
+        else:
+            sys.exit("--profile takes the headline or --workload stress-65k")
         return
     if a.workload is not None:
         print(json.dumps(WORKLOADS[a.workload](not a.no_cpu)), flush=True)

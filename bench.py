@@ -251,6 +251,12 @@ def workload_single_cell(cpu):
             "iterations": r.iterations, "converged": r.converged,
             "ms_per_iteration": round(r.seconds * 1e3 / max(r.iterations, 1), 4), "gpu_median_s": round(med, 4),
             "config": {"workload": "unbalanced 7355 x 8962, d 30, eps 0.05, rho (1, 50), median cost, tol 1e-6"}}
+    # the exponentials, which bound this shape's roofline: 2 I J per iteration
+    t_it = r.seconds / max(r.iterations, 1)
+    exps_it = 2.0 * I * J
+    line["roofline"] = {"bound": "exp", "achieved": round(exps_it / t_it / 1e12, 3), "peak": EXP_PEAK / 1e12,
+                        "unit": "Texp/s", "frac": round(exps_it / t_it / EXP_PEAK, 4),
+                        "basis": "exponentials of both half-steps per iteration over the iteration time"}
     if cpu:
         hm = _host_median_seconds(x, y)
         per = _cpu_per_iteration(x, y, a, b, center, scale, eps=0.05, rho=(1.0, 50.0), a_target=w, b_target=b)
@@ -340,6 +346,12 @@ def workload_stress(cpu):
             "data": "synthetic", "iterations": r.iterations,
             "ms_per_iteration": round(r.seconds * 1e3 / max(r.iterations, 1), 3),
             "config": {"workload": "balanced 65536 x 65536, d 128, eps 1.0 -> 0.01 (0.7 per stage), 280 its"}}
+    # the fp16 pipe the staged kernel runs on, over whole iterations (both half-steps, merges and control included)
+    t_it = r.seconds / max(r.iterations, 1)
+    flop_it = 2 * PRODUCTS * 2.0 * len(x) * len(y) * 128
+    line["roofline"] = {"bound": "mfma", "achieved": round(flop_it / t_it / 1e12, 1), "peak": MFMA_F16_PEAK / 1e12,
+                        "unit": "TFLOP/s", "frac": round(flop_it / t_it / MFMA_F16_PEAK, 4),
+                        "basis": "three-product fp16 MFMA FLOP of both half-steps per iteration over the iteration time"}
     if cpu:
         per = _cpu_per_iteration(x, y, None, None, r.center, r.cost_scale, iters=2, eps=0.01)
         line["cpu_baseline"] = {"value": round(per * 280, 1), "unit": "s", "cores": len(os.sched_getaffinity(0)),

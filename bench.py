@@ -273,32 +273,46 @@ def pipeline_sizes(n_points=39, total=175_000):
     return np.maximum(np.round(s * total / s.sum()).astype(int), 2)
 
 
+PIPELINE_STREAMS = 4      # pairs in flight at once (wot_transport_maps); 2 to 8 measured, 4 the fastest
+
+
 def workload_pipeline(cpu):
     """38 consecutive wot transport maps (39 time points, log-uniform sizes in [1,500, 9,000] summing to
-    ~175,000, d 30), each with median normalisation, wot's eps stages and 3 growth iterations, end to end."""
+    ~175,000, d 30), each with median normalisation, wot's eps stages and 3 growth iterations, end to end:
+    the pairs PIPELINE_STREAMS at a time (wot_transport_maps, one HIP stream per pair in flight), and for scale
+    the same maps one pair after the other (bit-identical results, checked here)."""
     import numpy as np
     import torch
     from trnopt import Backend, SinkhornOptions
-    from trnopt.singlecell import wot_transport_map
+    from trnopt.singlecell import wot_transport_map, wot_transport_maps
     sizes = pipeline_sizes()
     o = SinkhornOptions(check_every=5, max_iters=50_000, kernel="hip", backend=Backend.preset("rocm"))
     clouds = [single_cell_inputs(n=int(sizes[t]), m=int(sizes[t + 1]), t0=t, t1=t + 1)[:2]
               for t in range(len(sizes) - 1)]
     wot_transport_map(*clouds[0], growth_iters=1, opts=o)          # warm-up
+    kw = dict(growth_iters=3, tol=1e-6, stage_tol=1e-6, opts=o)
     torch.cuda.synchronize()
     t = time.perf_counter()
+    maps = wot_transport_maps(clouds, streams=PIPELINE_STREAMS, **kw)
+    total = time.perf_counter() - t
     work = iters = 0
-    for k, (x0, x1) in enumerate(clouds):
-        tm = wot_transport_map(x0, x1, growth_iters=3, tol=1e-6, stage_tol=1e-6, opts=o)
+    for k, ((x0, x1), tm) in enumerate(zip(clouds, maps)):
         iters += tm.iterations
         work += tm.iterations * len(x0) * len(x1)
-        print(f"pair {k}: {len(x0)} x {len(x1)}, {tm.iterations} iterations, {tm.seconds:.3f} s", file=sys.stderr,
-              flush=True)
-    total = time.perf_counter() - t
+        print(f"pair {k}: {len(x0)} x {len(x1)}, {tm.iterations} iterations, {tm.seconds:.3f} s (overlapped)",
+              file=sys.stderr, flush=True)
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    seq = wot_transport_maps(clouds, streams=1, **kw)
+    seq_s = time.perf_counter() - t
+    same = all(np.array_equal(a.result.f, b.result.f) and np.array_equal(a.result.g, b.result.g) and
+               a.iterations == b.iterations for a, b in zip(maps, seq))
     line = {"metric": "total seconds, 38-pair wot pipeline (3 growth iterations each)", "value": round(total, 3),
             "unit": "s", "higher_is_better": False, "n_gpus": 1, "dtype": "f32", "data": "synthetic",
             "pairs": len(clouds), "iterations": iters, "points": int(sizes.sum()),
-            "config": {"workload": "39 time points, d 30, eps 0.05, rho (1, 50), wot stages, tol 1e-6, growth 3"}}
+            "sequential_s": round(seq_s, 3), "sequential_bit_identical": same,
+            "config": {"workload": "39 time points, d 30, eps 0.05, rho (1, 50), wot stages, tol 1e-6, growth 3",
+                       "pairs_in_flight": PIPELINE_STREAMS}}
     if cpu:
         x0, x1 = clouds[0]
         I, J = len(x0), len(x1)

@@ -461,10 +461,35 @@ def test_wot_pipeline_three_pairs_matches_torch_path():
         assert np.abs(a.result.row_mass / b.result.row_mass - 1).max() < 1e-3
 
 
+def test_wot_transport_maps_in_flight_equal_one_at_a_time():
+    """Pairs in flight at once (wot_transport_maps, one HIP stream and host thread each, fewer streams than
+    pairs) give every map bit for bit as the pairs run one after the other: a pair's kernels, work split and
+    host steps do not depend on what runs beside it."""
+    from trnopt.singlecell import wot_transport_maps
+    sizes = [1500, 2400, 900, 3100, 2000, 700, 2600]
+    sig = 1.0 / np.sqrt(np.arange(30) + 1.0)
+    pts = [np.random.default_rng(40 + t).standard_normal((s, 30)) * sig + 0.3 * sig * t for t, s in enumerate(sizes)]
+    pairs = list(zip(pts[:-1], pts[1:]))
+    gpu = SinkhornOptions(kernel="hip", backend=ROCM, check_every=5, max_iters=50_000)
+    kw = dict(growth_iters=2, tol=1e-6, stage_tol=1e-6, opts=gpu)
+    print("pairs in flight", flush=True)
+    many = wot_transport_maps(pairs, streams=4, **kw)
+    print("pairs one at a time", flush=True)
+    one = wot_transport_maps(pairs, streams=1, **kw)
+    for k, (a, b) in enumerate(zip(many, one)):
+        assert a.result.converged and a.iterations == b.iterations, k
+        np.testing.assert_array_equal(a.result.f, b.result.f)
+        np.testing.assert_array_equal(a.result.g, b.result.g)
+        np.testing.assert_array_equal(a.result.row_mass, b.result.row_mass)
+        for Ga, Gb in zip(a.learned_growth, b.learned_growth):
+            np.testing.assert_array_equal(Ga, Gb)
+
+
 def test_wot_pipeline_38_pairs_at_full_size():
     """The pipeline workload at its full size: 39 time points (log-uniform cell counts in [1,500, 9,000], 175,000
     cells, d 30), 38 consecutive wot maps, each with its GPU median normalisation, wot's eps stages, tol 1e-6
-    and 3 growth iterations (src/trnopt/singlecell.py:61-86, README.md:19-24). Every pair converges and its
+    and 3 growth iterations (src/trnopt/singlecell.py:61-86, README.md:19-24), several pairs in flight as the
+    benchmark runs them. Every pair converges and its
     masses are the float64 plan's row and column sums of its potentials; the largest pair meets the float64
     fixed-point pins (last g update at sampled columns, next f update within tolerance), and the smallest pair
     matches the oracle's float32 run of the reference's op sequence (learned growth within 1e-3, potentials
@@ -472,18 +497,18 @@ def test_wot_pipeline_38_pairs_at_full_size():
     import sys
     from pathlib import Path
     sys.path.insert(0, str(Path(__file__).resolve().parent.parent))
-    from bench import pipeline_sizes, single_cell_inputs
-    from trnopt.singlecell import wot_transport_map
+    from bench import PIPELINE_STREAMS, pipeline_sizes, single_cell_inputs
+    from trnopt.singlecell import wot_transport_maps
     sizes = pipeline_sizes()
     assert len(sizes) == 39 and abs(int(sizes.sum()) - 175_000) < 50
     gpu = SinkhornOptions(kernel="hip", backend=ROCM, check_every=5, max_iters=50_000)
     clouds = [single_cell_inputs(n=int(sizes[t]), m=int(sizes[t + 1]), t0=t, t1=t + 1)[:2] for t in range(38)]
-    maps, iters = [], 0
-    for k, (x0, x1) in enumerate(clouds):
-        tm = wot_transport_map(x0, x1, growth_iters=3, tol=1e-6, stage_tol=1e-6, opts=gpu)
+    # as the benchmark runs them: several pairs in flight
+    maps = wot_transport_maps(clouds, streams=PIPELINE_STREAMS, growth_iters=3, tol=1e-6, stage_tol=1e-6, opts=gpu)
+    iters = 0
+    for k, tm in enumerate(maps):
         assert tm.result.converged and len(tm.learned_growth) == 3, k
         iters += tm.iterations
-        maps.append(tm)
     print("pipeline:", iters, "iterations over 38 pairs", flush=True)
     worst_mass = 0.0                                 # relative to each pair's float32 floor
     for k, ((x0, x1), tm) in enumerate(zip(clouds, maps)):

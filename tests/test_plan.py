@@ -178,3 +178,28 @@ def test_wot_eps_stages_closed_form():
     np.testing.assert_allclose(wot_eps_stages(0.01, eps0=2.0, scalings=4), [2.0 * 0.01 ** (e / 4) for e in range(4)],
                                rtol=1e-14)
     assert all(e > 0.05 for e in st)           # every stage lies above the final eps: the solver keeps them all
+
+
+def test_wot_transport_maps_equal_the_per_pair_maps():
+    """wot_transport_maps runs a pipeline's independent pairs (on the fused path several at once); on the torch
+    path it runs them in order, and every map equals wot_transport_map's for its pair, with per-pair growth and
+    time steps. Mismatched per-pair arguments are refused."""
+    from trnopt.singlecell import wot_transport_map, wot_transport_maps
+    opts = SinkhornOptions(kernel="torch", backend=Backend.preset("cpu"), max_iters=20000)
+    sig = 1.0 / np.sqrt(np.arange(4) + 1.0)
+    pts = [np.random.default_rng(s).standard_normal((n, 4)) * sig + 0.3 * s * sig for n, s in ((90, 1), (110, 2), (70, 3))]
+    pairs = [(pts[0], pts[1]), (pts[1], pts[2])]
+    growth = [np.linspace(0.5, 1.5, len(pts[0])), None]
+    maps = wot_transport_maps(pairs, growth=growth, delta_days=[1.0, 0.5], streams=4, growth_iters=2, tol=1e-7,
+                              opts=opts)
+    for (x0, x1), G, dd, tm in zip(pairs, growth, [1.0, 0.5], maps):
+        one = wot_transport_map(x0, x1, G, dd, growth_iters=2, tol=1e-7, opts=opts)
+        assert tm.iterations == one.iterations
+        np.testing.assert_array_equal(tm.result.f, one.result.f)
+        np.testing.assert_array_equal(tm.result.g, one.result.g)
+        for a, b in zip(tm.learned_growth, one.learned_growth):
+            np.testing.assert_array_equal(a, b)
+    with pytest.raises(ValueError, match="one entry per pair"):
+        wot_transport_maps(pairs, growth=[None], opts=opts)
+    with pytest.raises(ValueError, match="one entry per pair"):
+        wot_transport_maps(pairs, delta_days=[1.0, 2.0, 3.0], opts=opts)

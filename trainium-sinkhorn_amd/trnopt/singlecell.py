@@ -74,6 +74,59 @@ def wot_transport_map(x0: np.ndarray, x1: np.ndarray, growth: np.ndarray | None 
     return TransportMap(result=res, learned_growth=learned, seconds=seconds, iterations=iters)
 
 
+def wot_transport_maps(pairs, growth=None, delta_days=1.0, streams: int = 4, **kw) -> list:
+    """wot_transport_map for every (x0, x1) of `pairs` -- the consecutive time points of a pipeline, whose maps
+    are independent -- with up to `streams` pairs in flight at once on the GPU (the reference's example runs them
+    one after the other, examples/singlecell_wot.py:84-89).
+
+    growth: None or one growth array per pair; delta_days: a number or one per pair; kw: wot_transport_map's
+    other arguments (eps, lambda1, lambda2, growth_iters, tol, stage_tol, opts). On the fused path each pair runs
+    on its own HIP stream, driven by its own host thread: a small pair's kernels are mostly launch and load
+    latency, which the pairs beside it fill. A pair's kernels, work split and host steps do not depend on what
+    runs beside it, so every map equals wot_transport_map's for that pair bit for bit. With streams=1, or on the
+    torch path, the pairs run in order. Returns the TransportMaps in the order of `pairs`."""
+    import torch
+    pairs = list(pairs)
+    n = len(pairs)
+    growths = [None] * n if growth is None else list(growth)
+    days = list(delta_days) if np.ndim(delta_days) else [float(delta_days)] * n
+    if len(growths) != n or len(days) != n:
+        raise ValueError("growth and delta_days need one entry per pair")
+    opts = kw.get("opts") or SinkhornOptions()
+    streams = max(1, int(streams))
+
+    def one(k):
+        x0, x1 = pairs[k]
+        return wot_transport_map(x0, x1, growths[k], days[k], **kw)
+
+    if streams == 1 or n < 2 or not all(_use_hip(opts, np.shape(x0)[1]) for x0, _ in pairs):
+        return [one(k) for k in range(n)]
+    import threading
+    from concurrent.futures import ThreadPoolExecutor
+    from . import hip_sinkhorn as hk
+    hk.lib()                                     # loaded once, before the threads
+    dev = _gpu_device(opts)
+    with torch.cuda.device(dev):
+        caller = torch.cuda.current_stream()
+        pool = [torch.cuda.Stream() for _ in range(min(streams, n))]
+        for s in pool:
+            s.wait_stream(caller)
+    free, lock, local = list(pool), threading.Lock(), threading.local()
+
+    def run(k):
+        if not hasattr(local, "stream"):        # one stream per worker thread, for all its pairs
+            with lock:
+                local.stream = free.pop()
+        with torch.cuda.device(dev), torch.cuda.stream(local.stream):
+            return one(k)
+
+    with ThreadPoolExecutor(len(pool)) as ex:
+        maps = list(ex.map(run, range(n)))
+    for s in pool:
+        caller.wait_stream(s)
+    return maps
+
+
 def wot_tmap(x0, x1, tm: TransportMap) -> np.ndarray:
     """The dense map in wot's normalisation (I * P), small pairs only."""
     I, J = len(x0), len(x1)

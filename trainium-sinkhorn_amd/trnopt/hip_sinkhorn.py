@@ -442,8 +442,7 @@ class DeviceLoop:
             ev.synchronize()
             st = SkState.from_buffer_copy(buf.numpy().tobytes())
             if st.done:
-                torch.cuda.current_stream().synchronize()
-                return self.read_state()
+                return st                     # final: the launches still queued return at once, changing nothing
             if not inflight and queued >= self.max_iters:  # pragma: no cover - done must be set by then
                 return self.read_state()
 

@@ -203,16 +203,19 @@ def _solve_hip(p, opts: SinkhornOptions):
                              check_every=opts.check_every, stage_max_iters=opts.stage_max_iters,
                              fixed_iters=opts.fixed_iters, balanced=p.balanced)
         t0 = time.perf_counter()
+        c1 = None if p.balanced else hk.scalars(opts.eps, 1.0, dev)     # requested before the loop's launches
         st = loop.run()
-        # f = fh + |x|^2 in float32 on the device, then float64, as the reference reads it back (:379-380)
-        f = (loop.fh + X.sq)[:X.n].to("cpu", torch.float64).numpy()
-        g = (loop.gh + Y.sq)[:Y.n].to("cpu", torch.float64).numpy()
+        # f = fh + |x|^2 in float32 on the device, then float64, as the reference reads it back (:379-380); unbalanced,
+        # also one balanced half-step each way (kappa = 1, no offset) at the final eps (:381-389). One read-back.
+        parts = [(loop.fh + X.sq)[:X.n], (loop.gh + Y.sq)[:Y.n]]
+        if not p.balanced:
+            parts.append((hk.half_step(X, Y, loop.gh, c1, use_off=False) + X.sq)[:X.n])
+            parts.append((hk.half_step(Y, X, loop.fh, c1, use_off=False) + Y.sq)[:Y.n])
+        host = torch.cat(parts).to("cpu", torch.float64).numpy()
+        f, g = host[:X.n], host[X.n:X.n + Y.n]
         fb = gb = None
         if not p.balanced:
-            # one balanced half-step each way (kappa = 1, no offset) at the final eps (:381-389)
-            c1 = hk.scalars(opts.eps, 1.0, dev)
-            fb = (hk.half_step(X, Y, loop.gh, c1, use_off=False) + X.sq)[:X.n].to("cpu", torch.float64).numpy()
-            gb = (hk.half_step(Y, X, loop.fh, c1, use_off=False) + Y.sq)[:Y.n].to("cpu", torch.float64).numpy()
+            fb, gb = host[X.n + Y.n:2 * X.n + Y.n], host[2 * X.n + Y.n:]
     return f, g, fb, gb, int(st.it), float(st.err), bool(st.converged), t0
 
 

@@ -461,18 +461,22 @@ def test_wot_pipeline_three_pairs_matches_torch_path():
         assert np.abs(a.result.row_mass / b.result.row_mass - 1).max() < 1e-3
 
 
-def test_wot_transport_maps_in_flight_equal_one_at_a_time():
+@pytest.mark.parametrize("graphs", [False, True])
+def test_wot_transport_maps_in_flight_equal_one_at_a_time(monkeypatch, graphs):
     """Pairs in flight at once (wot_transport_maps, one HIP stream and host thread each, fewer streams than
     pairs) give every map bit for bit as the pairs run one after the other: a pair's kernels, work split and
-    host steps do not depend on what runs beside it."""
+    host steps do not depend on what runs beside it. With TRNOPT_HIP_GRAPH=1 the pairs one at a time replay
+    captured graphs in the main thread while the worker threads launch eagerly (a capture in one thread and a
+    graph released in another must not overlap), and the maps are still the same bit for bit."""
     from trnopt.singlecell import wot_transport_maps
+    monkeypatch.setenv("TRNOPT_HIP_GRAPH", "1" if graphs else "0")
     sizes = [1500, 2400, 900, 3100, 2000, 700, 2600]
     sig = 1.0 / np.sqrt(np.arange(30) + 1.0)
     pts = [np.random.default_rng(40 + t).standard_normal((s, 30)) * sig + 0.3 * sig * t for t, s in enumerate(sizes)]
     pairs = list(zip(pts[:-1], pts[1:]))
     gpu = SinkhornOptions(kernel="hip", backend=ROCM, check_every=5, max_iters=50_000)
     kw = dict(growth_iters=2, tol=1e-6, stage_tol=1e-6, opts=gpu)
-    print("pairs in flight", flush=True)
+    print("pairs in flight, graphs", graphs, flush=True)
     many = wot_transport_maps(pairs, streams=4, **kw)
     print("pairs one at a time", flush=True)
     one = wot_transport_maps(pairs, streams=1, **kw)

@@ -24,6 +24,7 @@ from __future__ import annotations
 
 import ctypes
 import os
+import threading
 from pathlib import Path
 
 import numpy as np
@@ -344,7 +345,9 @@ class DeviceLoop:
     With TRNOPT_HIP_GRAPH=1, whole batches of GRAPH_BATCH iterations are replayed from one captured HIP graph
     (20 to 40 kernels, no memset nodes): fewer host calls, for callers whose host enqueue is the bottleneck. Graph
     and eager launches run the same kernels with the same arguments, so the results are bit-identical. The
-    default is eager: the GPU-bound loop measured no faster from graphs, and each solve would pay a capture."""
+    default is eager: the GPU-bound loop measured no faster from graphs, and each solve would pay a capture
+    (host enqueue at 3,000 x 3,500 d 30: 10.6-12.7 us per iteration eager, 5.2-5.3 us replayed, after a first
+    capture of about 4.4 ms). Graphs are used in the main thread only (graphs_enabled)."""
 
     GRAPH_BATCH = 10
 
@@ -384,19 +387,31 @@ class DeviceLoop:
 
     @staticmethod
     def graphs_enabled() -> bool:
-        return os.environ.get("TRNOPT_HIP_GRAPH", "0") == "1"
+        """TRNOPT_HIP_GRAPH=1, and only in the main thread. A capture in one host thread and a graph released in
+        another (or a device synchronisation there) cannot overlap: the HIP runtime refuses the release while any
+        stream captures, and torch's graph destructor then terminates the process. Worker threads -- such as
+        wot_transport_maps' pairs in flight -- therefore launch eagerly, which is also the faster form there."""
+        return os.environ.get("TRNOPT_HIP_GRAPH", "0") == "1" and threading.current_thread() is threading.main_thread()
 
     def capture(self) -> None:
-        """Capture the graph of GRAPH_BATCH iterations now (enqueue would do it on first use). Capturing
-        synchronises the device and launches nothing."""
+        """Capture the graph of GRAPH_BATCH iterations now (enqueue would do it on first use). Capturing launches
+        nothing and does not synchronise the device: the capture is thread-local, so that other host threads
+        (wot_transport_maps drives one pair per thread) keep launching on their own streams meanwhile. (The
+        torch.cuda.graph context would synchronise the whole device first, which another thread's capture
+        forbids.)"""
         if self._graph is not None or not self.graphs_enabled():
             return
         cur = torch.cuda.current_stream()
         side = torch.cuda.Stream(device=self.X.device)
         side.wait_stream(cur)
         g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g, stream=side):
-            _check(lib().sk_loop_run_f32(ctypes.byref(self._L), self.GRAPH_BATCH, _stream()), "sk_loop_run_f32")
+        with torch.cuda.stream(side):
+            g.capture_begin(capture_error_mode="thread_local")
+            try:
+                st = lib().sk_loop_run_f32(ctypes.byref(self._L), self.GRAPH_BATCH, _stream())
+            finally:
+                g.capture_end()
+        _check(st, "sk_loop_run_f32")
         cur.wait_stream(side)
         self._graph = g
 

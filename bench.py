@@ -30,7 +30,7 @@ Also reported on the same JSON line:
 * cpu_baseline -- the reference's plain-PyTorch CPU path (the oracle's restatement, float32, block 2048,
   all host cores) on the same workload: best of 3 runs of 10 fixed iterations after 1 warm-up iteration;
 * end_to_end_s -- sinkhorn() wall time for 10 fixed iterations, host arrays in, float64 potentials out
-  (setup, H2D, packing, loop, read-back).
+  (setup, H2D, packing, loop, read-back): best of 3 after 2 warm-up calls.
 """
 
 from __future__ import annotations
@@ -111,11 +111,14 @@ def gpu_run(steps, warmup):
     from trnopt import Backend, SinkhornOptions, sinkhorn
     o = SinkhornOptions(eps=EPS, normalize=False, max_iters=10, fixed_iters=True, kernel="hip",
                         backend=Backend.preset("rocm"))
-    sinkhorn(x, y, opts=o)
+    for _ in range(2):                   # warm-up: the caching allocator and pinned buffers settle
+        sinkhorn(x, y, opts=o)
     torch.cuda.synchronize()
-    te = time.perf_counter()
-    sinkhorn(x, y, opts=o)
-    e2e = time.perf_counter() - te
+    e2e = float("inf")
+    for _ in range(3):                   # best of 3, each from host arrays to float64 potentials on the host
+        te = time.perf_counter()
+        sinkhorn(x, y, opts=o)
+        e2e = min(e2e, time.perf_counter() - te)
     return dict(ms_per_it=ms_per_it, kernel_ms=kernel_ms, e2e=e2e, kp=hk.pad_dim(D))
 
 

@@ -1,0 +1,72 @@
+"""A seeded random sweep of sinkhorn(kernel="hip") -- the on-device loop -- against the oracle's float64 run of
+the reference's driver (src/trnopt/sinkhorn.py:241-394) with the same options.
+
+Each case draws the cloud sizes (30 to 1,500, log-uniform), the dimension (1 to 128), the weights, balanced or
+unbalanced (one rho or a pair, with or without marginal targets), the normalisation (mean of sampled pairs,
+the exact median, none), eps, and the eps path: a fixed eps, an eps_start / eps_decay schedule, or wot-style
+stages. Every case runs a fixed number of iterations (fixed_iters), and stages advance by stage_max_iters at
+their first check, so that the iteration path does not depend on float32 rounding near a threshold; the
+potentials must then agree with float64 within the 1e-5 relative (inf-norm) bar.
+"""
+
+import numpy as np
+import pytest
+
+from oracle import reference as ref
+from conftest import inf_rel
+
+from trnopt import Backend
+from trnopt.sinkhorn import SinkhornOptions, sinkhorn
+
+pytestmark = pytest.mark.gpu
+N_CASES = 24
+TOL = 1e-5
+
+
+def _case(k):
+    rng = np.random.default_rng(9100 + k)
+    n = int(np.exp(rng.uniform(np.log(30.0), np.log(1500.0))))
+    m = int(np.exp(rng.uniform(np.log(30.0), np.log(1500.0))))
+    d = int(rng.integers(1, 129))
+    x = rng.normal(size=(n, d)) * np.exp(rng.uniform(-1.0, 1.0))
+    y = rng.normal(size=(m, d)) * np.exp(rng.uniform(-1.0, 1.0)) + rng.normal(scale=0.5, size=d)
+    a = rng.uniform(0.2, 1.8, n)
+    b = rng.uniform(0.2, 1.8, m)
+    a, b = a / a.sum(), b / b.sum()
+    opts = dict(fixed_iters=True, max_iters=int(rng.integers(5, 41)), check_every=int(rng.integers(2, 8)))
+    opts["normalize"] = [True, "median", False][int(rng.integers(0, 3))]
+    if opts["normalize"] is False:                         # keep eps on the scale of the raw costs
+        scale = float(np.mean(((x[:200, None, :] - y[None, :200, :]) ** 2).sum(-1)))
+    else:
+        scale = 1.0
+    opts["eps"] = float(scale * np.exp(rng.uniform(np.log(0.02), np.log(1.0))))
+    kw = {}
+    if rng.uniform() < 0.5:
+        rho = float(np.exp(rng.uniform(np.log(0.1), np.log(100.0))))
+        opts["rho"] = rho if rng.uniform() < 0.5 else (rho, float(np.exp(rng.uniform(np.log(0.1), np.log(100.0)))))
+        if rng.uniform() < 0.5:
+            kw["a_target"] = a * rng.uniform(0.5, 1.5, n)
+            kw["b_target"] = b * rng.uniform(0.5, 1.5, m)
+    path = int(rng.integers(0, 3))
+    if path == 1:
+        opts["eps_start"] = opts["eps"] * float(np.exp(rng.uniform(np.log(2.0), np.log(20.0))))
+        opts["eps_decay"] = float(rng.uniform(0.5, 0.95))
+    elif path == 2:
+        top = opts["eps"] * float(np.exp(rng.uniform(np.log(2.0), np.log(20.0))))
+        ns = int(rng.integers(2, 5))
+        opts["eps_stages"] = tuple(float(top * (opts["eps"] / top) ** (s / ns)) for s in range(ns))
+        opts["stage_max_iters"] = opts["check_every"]       # every stage ends at its first check
+        opts["max_iters"] = max(opts["max_iters"], ns * opts["check_every"] + 5)
+    return x, y, a, b, opts, kw
+
+
+@pytest.mark.parametrize("k", range(N_CASES))
+def test_solver_random_sweep(k):
+    x, y, a, b, opts, kw = _case(k)
+    print(f"solver sweep case {k}: n {len(x)} m {len(y)} d {x.shape[1]} {opts} targets {bool(kw)}", flush=True)
+    res = sinkhorn(x, y, a, b, opts=SinkhornOptions(kernel="hip", backend=Backend.preset("rocm"), **opts), **kw)
+    want = ref.sinkhorn_ref(x, y, a, b, **opts, **kw)
+    assert res.iterations == want.iterations == opts["max_iters"]
+    ef, eg = inf_rel(res.f, want.f), inf_rel(res.g, want.g)
+    print(f"  |f - f64| / |f64| {ef:.2e}, |g - g64| / |g64| {eg:.2e}", flush=True)
+    assert ef < TOL and eg < TOL, (ef, eg)

@@ -841,7 +841,11 @@ void lse_partial_kernel(PartialArgs a) {
     if constexpr (CT == kF16x2) {
         if (a.mode == kHalfStep && cb != 0.0f && cb == c && cb_s2 == (ROLE == 0 ? sy : sx)) {
             const float it = 1.0f / cb_t;                  // exact
-            if (a.u2 != nullptr)
+            // The usual unit t = 1 gets its own inlined copy: with c = 1 a constant, each exponential's argument is
+            // the two-operand a - m (v_sub_f32) instead of the three-operand fma.
+            if (a.u2 != nullptr && cb_t == 1.0f)
+                segments<NC, ROLE, CT, true>(a, p, wv, a.u2, 1.0f, kLog2e, 1.0f, 1.0f, 1.0f, lds_y, lds_col);
+            else if (a.u2 != nullptr)
                 segments<NC, ROLE, CT, true>(a, p, wv, a.u2, 1.0f, kLog2e, cb_t, it, it, lds_y, lds_col);
             else
                 segments<NC, ROLE, CT, true>(a, p, wv, a.u, alpha, beta, c * cb_t, it, it, lds_y, lds_col);

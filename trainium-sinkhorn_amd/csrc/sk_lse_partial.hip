@@ -665,19 +665,22 @@ struct Streamed {
         stage_cols(tb, cend);
         tile(accA, accB, nullptr, yA, t, false);
         ++t;
+        // The restaging of the column terms (once per kColTiles tiles) and the segment's end are the unlikely
+        // branches: laid out of line, so that consecutive tiles fall through with no taken branch between them
+        // (with one wave per SIMD a taken branch costs the wave about 25 cycles in which nothing issues).
         while (t < te) {
-            if (t >= cend) {
+            if (__builtin_expect(t >= cend, 0)) {
                 cend = t + kColTiles < te ? t + kColTiles : te;
                 stage_cols(t, cend);
             }
             load_y(t + 1 < te ? t + 1 : last, yA);
             tile(accB, accA, colp_of(t - 1), yB, t, true);
             ++t;
-            if (t >= te) {
+            if (__builtin_expect(t >= te, 0)) {
                 update(accB, colp_of(t - 1));
                 goto done;
             }
-            if (t >= cend) {
+            if (__builtin_expect(t >= cend, 0)) {
                 cend = t + kColTiles < te ? t + kColTiles : te;
                 stage_cols(t, cend);
             }

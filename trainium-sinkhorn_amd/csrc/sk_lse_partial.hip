@@ -608,16 +608,16 @@ struct Streamed {
         };
         T yA[NC][kPieces], yB[NC][kPieces];
         // A tile's pieces lie in 1 KB units (one per K chunk and piece). The loads address them from a scalar base
-        // plus the lane's offset; units from the fifth on are past the loads' 4 KB immediate-offset range and take a
-        // second scalar base (opaque to the compiler, which would otherwise form a 64-bit vector address for them:
-        // four more VALU instructions per tile).
+        // plus the lane's offset; each group of four units is one 4 KB immediate-offset range, and the groups
+        // after the first take scalar bases of their own, b0 + g ystep (ystep opaque to the compiler, which would
+        // otherwise form a 64-bit vector address for them: four more VALU instructions per tile).
         size_t ystep = 4 * 64;                          // opaque once, so that the pointer stays a global one
         if constexpr (NC * kPieces > 4) asm volatile("" : "+s"(ystep));
         auto load_y = [&](int t, T (&yv)[NC][kPieces]) {
             const T* b0 = yt + (size_t)t * TILE16;
-            const T* b1 = b0 + ystep;
 #pragma unroll
-            for (int k = 0; k < NC * kPieces; ++k) yv[k / kPieces][k % kPieces] = (k < 4 ? b0 : b1)[(k % 4) * 64 + lane];
+            for (int k = 0; k < NC * kPieces; ++k)
+                yv[k / kPieces][k % kPieces] = (b0 + (k / 4) * ystep)[(k % 4) * 64 + lane];
         };
         auto colp_of = [&](int t) { return lds_col + (t - cbase) * 32 + 4 * h; };
         // With FOLD, the A operand of tile t's column MFMA (lane l: column l % 32; lanes 32-63 meet zeros in B)

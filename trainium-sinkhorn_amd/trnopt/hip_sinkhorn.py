@@ -246,13 +246,13 @@ class HipCloud:
         if role not in (0, 1):
             raise ValueError("role must be 0 (first cloud) or 1 (second cloud)")
         pts = np.asarray(pts, dtype=np.float64)
-        _check_range("points", float(np.abs(pts).max()) if pts.size else 0.0)
+        _check_range("points", max(float(pts.max()), -float(pts.min())) if pts.size else 0.0)   # no |pts| copy
         npad = pad_points(n)
         self.n, self.npad, self.d, self.device, self.role = n, npad, d, device, role
         # |p|^2 (float64 sums), log w, w and the offset in one host array and one copy to the device; padding
         # points have |p|^2 = 0, log weight PAD_LOG_WEIGHT (weight exactly 0) and no offset
         vec = np.zeros((3 if off is None else 4, npad), dtype=np.float32)
-        vec[0, :n] = (pts * pts).sum(axis=1)           # as the reference sums them (float64), then cast
+        vec[0, :n] = np.einsum("ij,ij->i", pts, pts)   # float64 sums, as the reference's, then cast
         L = np.full(npad, PAD_LOG_WEIGHT)
         L[:n] = log_w
         vec[1] = L
@@ -262,8 +262,11 @@ class HipCloud:
         dv = torch.from_numpy(vec).to(device)
         self.sq, self.log_w, self.w = dv[0], dv[1], dv[2]
         self.off = dv[3] if off is not None else None
-        # the points unpadded: the packing pads them to npad x kp with zeros
-        pts32 = torch.from_numpy(np.ascontiguousarray(pts, dtype=np.float32)).to(device)
+        # the points unpadded (the packing pads them to npad x kp with zeros), cast into pinned host memory and
+        # copied asynchronously (the caching host allocator keeps the buffer until the copy has run)
+        host32 = torch.empty((n, d), dtype=torch.float32, pin_memory=True)
+        np.copyto(host32.numpy(), pts, casting="same_kind")
+        pts32 = host32.to(device, non_blocking=True)
         self.pk = pack_cloud(pts32)
 
     def c_struct(self) -> SkCloud:

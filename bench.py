@@ -167,6 +167,29 @@ def profile_stress(reps, eps=0.01):
     print(f"profile: {reps} loop iterations of {n} x {n} d 128 at eps {eps}, then a 256 MiB copy", flush=True)
 
 
+def profile_single_cell(reps):
+    """The single-cell counterpart of profile_run: one sinkhorn(kernel="hip") call of the single-cell workload
+    (7,355 x 8,962, d 30, eps 0.05, rho (1, 50), median-normalised cost, wot formulation) held to `reps` fixed
+    iterations (the streamed partial kernel at kp 32 and a merge kernel per half-step: both passes have fewer than
+    40 row groups), then the same 256 MiB copy."""
+    import numpy as np
+    import torch
+    from trnopt import Backend, SinkhornOptions, sinkhorn
+    x, y, w = single_cell_inputs()
+    I, J = len(x), len(y)
+    a, b = np.full(I, 1.0 / I), np.full(J, 1.0 / J)
+    o = SinkhornOptions(eps=0.05, rho=(1.0, 50.0), normalize="median", tol=1e-6, max_iters=reps, fixed_iters=True,
+                        kernel="hip", backend=Backend.preset("rocm"))
+    r = sinkhorn(x, y, a, b, o, a_target=w, b_target=b)
+    src = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"profile: {r.iterations} iterations of the {I} x {J} d 30 single-cell solve, then a 256 MiB copy",
+          flush=True)
+
+
 def _cpu_model():
     try:
         for line in Path("/proc/cpuinfo").read_text().splitlines():
@@ -407,10 +430,12 @@ def main():
     if a.profile:
         if a.workload == "stress-65k":
             profile_stress(a.reps)
+        elif a.workload == "single-cell":
+            profile_single_cell(a.reps)
         elif a.workload is None:
             profile_run(a.reps)
         else:
-            sys.exit("--profile takes the headline or --workload stress-65k")
+            sys.exit("--profile takes the headline, --workload single-cell or --workload stress-65k")
         return
     if a.workload is not None:
         print(json.dumps(WORKLOADS[a.workload](not a.no_cpu)), flush=True)

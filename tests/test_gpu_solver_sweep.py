@@ -70,3 +70,27 @@ def test_solver_random_sweep(k):
     ef, eg = inf_rel(res.f, want.f), inf_rel(res.g, want.g)
     print(f"  |f - f64| / |f64| {ef:.2e}, |g - g64| / |g64| {eg:.2e}", flush=True)
     assert ef < TOL and eg < TOL, (ef, eg)
+
+
+# A few points against a large cloud, and the reverse: one pass is a single row group whose columns are split
+# over every workgroup (merged by the merge kernel), the other hundreds of row groups against one column tile
+# (merged inside the partial kernel); balanced and unbalanced.
+EXTREME = [(6, 120_000, 16, None), (120_000, 6, 16, 1.0), (3, 50_000, 100, None), (50_000, 3, 100, (0.5, 5.0))]
+
+
+@pytest.mark.parametrize("i", range(len(EXTREME)))
+def test_solver_extreme_aspect_ratios(i):
+    n, m, d, rho = EXTREME[i]
+    rng = np.random.default_rng(9500 + i)
+    x = rng.normal(size=(n, d))
+    y = rng.normal(size=(m, d)) + 0.3
+    opts = dict(fixed_iters=True, max_iters=12, check_every=4, eps=0.1, normalize=True)
+    if rho is not None:
+        opts["rho"] = rho
+    print(f"solver extreme case {i}: n {n} m {m} d {d} rho {rho}", flush=True)
+    res = sinkhorn(x, y, opts=SinkhornOptions(kernel="hip", backend=Backend.preset("rocm"), **opts))
+    want = ref.sinkhorn_ref(x, y, **opts)
+    assert res.iterations == want.iterations == opts["max_iters"]
+    ef, eg = inf_rel(res.f, want.f), inf_rel(res.g, want.g)
+    print(f"  |f - f64| / |f64| {ef:.2e}, |g - g64| / |g64| {eg:.2e}", flush=True)
+    assert ef < TOL and eg < TOL, (ef, eg)

@@ -25,11 +25,13 @@ DEV = "cuda"
 N_CASES = 48
 
 
-def _case(k):
+def _case(k, shape=None):
     rng = np.random.default_rng(7000 + k)
     rows = int(np.exp(rng.uniform(0.0, np.log(3000.0))))
     m = int(np.exp(rng.uniform(0.0, np.log(3000.0))))
     d = int(rng.integers(1, 129))
+    if shape is not None:
+        rows, m, d = shape
     sx, sy = np.exp(rng.uniform(np.log(1e-3), np.log(1e3), 2))
     x = rng.normal(size=(rows, d)) * sx
     y = rng.normal(size=(m, d)) * sy + 0.3 * sy
@@ -62,9 +64,24 @@ def _budget(r32, c32, col_term, eps, kappa, want):
 
 @pytest.mark.parametrize("k", range(N_CASES))
 def test_half_step_random_sweep(hip, k):
-    c = _case(k)
+    _check_case(hip, _case(k), f"sweep case {k}")
+
+
+# A few points against a large cloud and the reverse: one row group whose columns are split over every
+# workgroup (256 partial slots per row for the merge), and hundreds of row groups against a single column
+# tile; the staged kernel (d 100) and d 1-2 as well.
+EXTREME = [(5, 150_000, 16), (150_000, 5, 16), (3, 60_000, 100), (60_000, 3, 100), (2, 200_000, 2),
+           (40_000, 1, 64)]
+
+
+@pytest.mark.parametrize("i", range(len(EXTREME)))
+def test_half_step_extreme_aspect_ratios(hip, i):
+    _check_case(hip, _case(500 + i, EXTREME[i]), f"extreme case {EXTREME[i]}")
+
+
+def _check_case(hip, c, label):
     rows, m, d, eps, kappa = c["rows"], c["m"], c["d"], c["eps"], c["kappa"]
-    print(f"sweep case {k}: rows {rows} m {m} d {d} scales {c['sx']:.3g} {c['sy']:.3g} eps {eps:.3g} "
+    print(f"{label}: rows {rows} m {m} d {d} scales {c['sx']:.3g} {c['sy']:.3g} eps {eps:.3g} "
           f"kappa {kappa:.3f}", flush=True)
     X = hip.HipCloud(c["x"], c["la"], DEV, off=c["offx"], role=0)
     Y = hip.HipCloud(c["y"], c["lb"], DEV, off=c["offy"], role=1)

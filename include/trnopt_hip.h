@@ -150,7 +150,8 @@ int sk_half_step_noalloc_f32(const void* x_pk, const float* xsq, const float* of
  * g update, stage advance, balanced / unbalanced checks every check_every iterations, fp32 floors).
  */
 typedef struct sk_cloud_f32 {
-    const void* pk;       /* packed points (sk_pack_cloud_f32 layout); the loop rewrites x's log2-unit copy */
+    const void* pk;       /* packed points (sk_pack_cloud_f32 layout); the loop rewrites x's log2-unit copy and
+                             writes the cloud's largest log weight into header word 5 at init */
     const float* sq;      /* |p|^2 (npad), float64 sums cast to fp32 (src/trnopt/sinkhorn.py:149) */
     const float* log_w;   /* log weights (npad), padding SK_PAD_LOG_WEIGHT */
     const float* w;       /* exp(log_w) (npad), padding 0 */

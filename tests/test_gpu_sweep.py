@@ -14,6 +14,8 @@ an fp32 dot product: a few 2^-24 of sum_k |x_k| |y_k| and of the scaled pieces' 
 own rounding, the exp2 / log2 of the log-sum-exp, and the final rounding of the result.
 """
 
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -22,7 +24,8 @@ from oracle import brute
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
-N_CASES = 48
+# The default sweep; SK_SWEEP_CASES=N runs the first N seeded cases instead (a longer one-off sweep).
+N_CASES = int(os.environ.get("SK_SWEEP_CASES", "160"))
 
 
 def _case(k, shape=None):

@@ -15,6 +15,9 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 constexpr float kLog2e = 1.44269504088896340736f;
+// log2(e) - kLog2e (1.93e-8): with it, fmaf(kLog2e, v, fmaf(kLog2eLo, v, r)) is r + log2(e) v rounded once
+// (kLog2e alone is 1.3e-8 low, a bias of 1.3e-8 |v| that does not average out).
+constexpr float kLog2eLo = (float)(1.44269504088896340736 - (double)kLog2e);
 constexpr float kLn2 = 0.69314718055994530942f;
 constexpr float kEmpty = -1.0e30f;     // running max of a row before its first column (finite on purpose)
 constexpr int kWaves = 4;              // waves per workgroup of the partial kernel (one per SIMD)

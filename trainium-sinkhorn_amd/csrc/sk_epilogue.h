@@ -141,6 +141,22 @@ __device__ inline void bake_header(char* first, const void* second, const BakePa
     h[4] = b.valid ? b.t : 1.0f;
 }
 
+// The column weights' offset of the on-device loop's half-steps (scores in log2 units from the first cloud's
+// log2-unit copy, column terms t (R + log2(e) log w)): t log2(e) max_j log w_j, rounded to an integer, with the
+// column cloud's largest log weight from word 5 of its packed header (written at loop init; 0 elsewhere). The
+// partial kernel subtracts it from every column term it stages and the merge adds it back (divided by t, as
+// the slots store M / t) to each row's maximum, in double. The column MFMA rounds its sum downward (a quarter
+// ulp of the result on average, never up: measured on the bf16 MFMA adding a column term to a nonzero
+// accumulator), so column terms at the magnitude of log w (about -log2 m, the larger part of them at large eps)
+// would give every score a bias of a quarter ulp of that magnitude. The bias differs between the f and g updates
+// when the two clouds' sizes put their terms in different binades, and the balanced iteration keeps the
+// difference, along the neutral mode of the potentials, every iteration (at eps 9 times the typical cost, 2e-5
+// of g after 23 iterations; the reference's float32 path: 4e-8). The offset is uniform over the launch, so the
+// merge restores it exactly; weights that span many binades keep the offset at their maximum.
+__device__ __forceinline__ float column_weight_offset(float t, float wmax) {
+    return __builtin_rintf((t * kLog2e) * wmax);
+}
+
 // eps of the iteration that starts with `it` iterations done (sinkhorn.py:347-350).
 __device__ inline double eps_for(const LoopCfg& c, int it, int stage) {
     if (c.n_stages > 0) return stage < c.n_stages ? c.stages[stage] : c.eps;
@@ -184,7 +200,8 @@ __device__ inline bool merge_group(const PartialArgs& a, int g) {
     const float sc0 = a.sc[0], sc1 = a.sc[1], sc2 = a.sc[2], sc3 = a.sc[3];   // valid in both modes
     const float* h1 = reinterpret_cast<const float*>(a.rows_role == 0 ? a.xr : a.yc);   // the first cloud
     const float* h2 = reinterpret_cast<const float*>(a.rows_role == 0 ? a.yc : a.xr);
-    const float cb = h1[2], cb_s2 = h1[3], s2 = h2[1];
+    const float cb = h1[2], cb_s2 = h1[3], s2 = h2[1], cb_t = h1[4];
+    const float wmax = reinterpret_cast<const float*>(a.yc)[5];   // the column cloud's largest log weight
     const int ic = i < a.rows_pad ? i : a.rows_pad - 1;
     const float x2 = a.mode == kHalfStep ? a.xsq[ic] : 0.0f;
     const float o = a.off != nullptr ? a.off[ic] : 0.0f;
@@ -198,8 +215,8 @@ __device__ inline bool merge_group(const PartialArgs& a, int g) {
 #pragma unroll
     for (int k = 0; k < kMergeBatch; ++k) v0[k] = p0 + k <= p1 ? ld<COH>(pp + (size_t)k * a.rows_pad) : make_float2(kEmpty, 0.0f);
     const int skip = *skip_p;
-    asm volatile("" ::"s"(sc0), "s"(sc1), "s"(sc2), "s"(sc3), "s"(cb), "s"(cb_s2), "s"(s2), "v"(x2), "v"(o),
-                 "v"(old), "v"(wi), "v"(skip));
+    asm volatile("" ::"s"(sc0), "s"(sc1), "s"(sc2), "s"(sc3), "s"(cb), "s"(cb_s2), "s"(s2), "s"(cb_t), "s"(wmax),
+                 "v"(x2), "v"(o), "v"(old), "v"(wi), "v"(skip));
     if (skip != 0) return false;
     const float c_hs = sc0 * kLog2e;
     // log2_ready, on the header words loaded above
@@ -226,6 +243,10 @@ __device__ inline bool merge_group(const PartialArgs& a, int g) {
             M = Mn;
             S = Sn;
         }
+        // the row maximum in the stored units, with the loop's column weights' offset (column_weight_offset)
+        // back on: the slots store M / t with t = cb_t
+        const double Md = (double)M + (l2 && a.u2 != nullptr ? (double)column_weight_offset(cb_t, wmax) / (double)cb_t
+                                                               : 0.0);
         // The row's log-sum-exp and the epilogue in double, rounded once: f may be far smaller than the max score
         // and the log of the sum it is the difference of (clouds far from unit scale under normalize=False), so
         // each float rounding of those would cost f relative precision.
@@ -248,13 +269,13 @@ __device__ inline bool merge_group(const PartialArgs& a, int g) {
                 // mathematics, so R = kappa (O - (M + log2 S)) + (kappa - 1) X2 with X2 = (c / 2) |x|^2 and
                 // O = log2(e) off, and fh = R / (c / 2), each rounded once from the double.
                 const double k2 = 0.5 * (double)c_hs;
-                const double R = kappa * (od * (double)kLog2eD - ((double)M + l2s)) + (kappa - 1.0) * (x2d * k2);
+                const double R = kappa * (od * (double)kLog2eD - (Md + l2s)) + (kappa - 1.0) * (x2d * k2);
                 val = (float)(R / k2);
                 if (i < a.n_store) st<COH>(a.out2 + i, (float)R);
             } else {
                 // eps lse = 2 M + eps ln(S) in accumulator units (log2-unit slots: M / c), with the caller's eps
                 // (float) as the reference's epilogue multiplies by it (src/trnopt/sinkhorn.py:119)
-                const double eps_lse = 2.0 * (l2 ? (double)M / (double)c_hs : (double)M) + (double)sc2 * kLn2D * l2s;
+                const double eps_lse = 2.0 * (l2 ? Md / (double)c_hs : Md) + (double)sc2 * kLn2D * l2s;
                 val = (float)(kappa * ((double)sc2 * od - eps_lse) + (kappa - 1.0) * x2d);
             }
             if (a.meas != nullptr) {
@@ -264,7 +285,7 @@ __device__ inline bool merge_group(const PartialArgs& a, int g) {
             }
             if (i < a.n_store) st<COH>(a.out + i, val);
         } else if (i < a.n_store) {
-            st<COH>(a.out + i, (float)((double)M + l2s / (double)kLog2e));   // natural log: l2s / c, c = log2(e)
+            st<COH>(a.out + i, (float)(Md + l2s / (double)kLog2e));   // natural log: l2s / c, c = log2(e)
         }
     }
     if (a.meas != nullptr) {

@@ -104,7 +104,21 @@ __global__ void pack_header_kernel(unsigned* __restrict__ header) {
         header[2] = 0u;                     // no log2-unit copy yet
         header[3] = 0u;
         header[4] = __float_as_uint(1.0f);  // the copy's unit
+        header[5] = 0u;                     // the largest log weight (the on-device loop writes it)
     }
+}
+
+// Word 5 of a packed cloud's header: its largest log weight over the real points (the on-device loop's column
+// offset, column_weight_offset in sk_epilogue.h). One workgroup.
+__global__ __launch_bounds__(256) void weight_max_kernel(const float* __restrict__ log_w, int n,
+                                                         unsigned* __restrict__ header) {
+    __shared__ float s_mx[4];
+    float mx = -3.0e38f;
+    for (int i = threadIdx.x; i < n; i += 256) mx = fmaxf(mx, log_w[i]);
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    if ((threadIdx.x & 63) == 0) s_mx[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    if (threadIdx.x == 0) header[5] = __float_as_uint(fmaxf(fmaxf(s_mx[0], s_mx[1]), fmaxf(s_mx[2], s_mx[3])));
 }
 
 __global__ __launch_bounds__(256) void absmax_kernel(const float* __restrict__ src, int n, int d, int ld,
@@ -755,6 +769,11 @@ int sk_loop_init_f32(const sk_loop_f32* L, void* stream) {
     const LoopLayout lo = loop_layout(L);
     hipLaunchKernelGGL(loop_init_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, L->state, loop_cfg(L),
                        lo.counters, lo.ncounters);
+    // both clouds' largest log weights into their headers (each is the column cloud of one half-step)
+    hipLaunchKernelGGL(weight_max_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, L->x.log_w, L->x.n,
+                       (unsigned*)const_cast<void*>(L->x.pk));
+    hipLaunchKernelGGL(weight_max_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, L->y.log_w, L->y.n,
+                       (unsigned*)const_cast<void*>(L->y.pk));
     // x's log2-unit copy for the first iteration's eps and both log2-unit potentials (from fh and the caller's
     // gh); the loop control remakes them when eps changes
     launch_bake(const_cast<void*>(L->x.pk), L->y.pk, L->x.npad, sk_pad_dim(L->d) / 16, L->state->sc_x,

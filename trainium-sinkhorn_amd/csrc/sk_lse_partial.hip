@@ -302,8 +302,8 @@ struct Staged {
     //     the barrier that ended that step), so that the matrix pipe does not wait on LDS after a barrier;
     //   - one barrier per step.
     __device__ __forceinline__ static void run(const PartialArgs& a, int rb0, int tb, int te, int slot, const float* cu,
-                                               float alpha, float beta, float cs, float c, float inv_sigma,
-                                               T* lds_y, float* lds_col) {
+                                               float alpha, float beta, float beta_lo, float cs, float K, float c,
+                                               float inv_sigma, T* lds_y, float* lds_col) {
         const int tid = tid_x();
         const int lane = tid & 63;
         const int h = lane >> 5;
@@ -367,7 +367,7 @@ struct Staged {
             for (int k = 0; k < PER_THREAD; ++k) *reinterpret_cast<T*>(dst + offb[k]) = pf[s][tt][k];
         };
         auto stage_cols = [&](int s, int cbuf) {
-            const float pc = fmaxf(cs * fmaf(beta, pv[s], alpha * pu[s]), kPadScore);
+            const float pc = fmaxf(cs * fmaf(beta, pv[s], fmaf(beta_lo, pv[s], alpha * pu[s])), kPadScore) - K;
             if constexpr (FOLD) {
                 const __bf16 q0 = (__bf16)pc;
                 const float r1 = pc - (float)q0;                  // exact
@@ -539,8 +539,8 @@ struct Streamed {
     static constexpr int kColTiles = col_tiles(FOLD);
 
     __device__ __forceinline__ static void run(const PartialArgs& a, int rb0, int tb, int te, int slot, const float* cu,
-                                               float alpha, float beta, float cs, float c, float inv_sigma,
-                                               float* lds_col) {
+                                               float alpha, float beta, float beta_lo, float cs, float K, float c,
+                                               float inv_sigma, float* lds_col) {
         const int tid = tid_x();
         const int lane = tid & 63;
         const int h = lane >> 5;
@@ -590,7 +590,7 @@ struct Streamed {
                 for (int q = 0; q < kColBatch; ++q) {
                     const int k = k0 + q * kBlockK + tid, j = base + k;
                     if (k < n && j >= 0) {
-                        const float v = fmaxf(cs * fmaf(beta, vv[q], alpha * uu[q]), kPadScore);
+                        const float v = fmaxf(cs * fmaf(beta, vv[q], fmaf(beta_lo, vv[q], alpha * uu[q])), kPadScore) - K;
                         if constexpr (FOLD) {
                             const __bf16 q0 = (__bf16)v;
                             const float r1 = v - (float)q0;                 // exact
@@ -774,12 +774,13 @@ __device__ inline void arrive(const PartialArgs& a, int g) {
     __syncthreads();   // the next segment's column staging reuses LDS the merge does not touch; keep waves together
 }
 
-// The work segments of workgroup p: a_ij = x_i . y_j + cs (alpha cu_j + beta v_j) in the kernel's units, scores
+// The work segments of workgroup p: a_ij = x_i . y_j + cs (alpha cu_j + (beta + beta_lo) v_j) - K in the kernel's
+// units (K: the column weights' offset of the on-device loop, below; 0 otherwise), scores
 // exp2(c (a - M)) (with L2: exp2(fma(a, c, -c M)), a in log2 units times the copy's unit t = 1 / c).
 template <int NC, int ROLE, int CT, bool L2>
 __device__ __forceinline__ void segments(const PartialArgs& a, int p, int wv, const float* cu, float alpha, float beta,
-                                         float cs, float c, float inv_sigma, typename Contract<CT>::T* lds_y,
-                                         float* lds_col) {
+                                         float beta_lo, float cs, float K, float c, float inv_sigma,
+                                         typename Contract<CT>::T* lds_y, float* lds_col) {
     // The segment bounds are 32-bit integer arithmetic (the divisions expand to vector code); their results are
     // the same in every lane, and readfirstlane hands them to the scalar unit, so the tile loop's counters and
     // operand addresses stay in scalar registers.
@@ -793,9 +794,10 @@ __device__ __forceinline__ void segments(const PartialArgs& a, int p, int wv, co
         // in the workgroup's barriers.
         const int rb0 = (g * kWavesK + wv) * kRowBlocksK;
         if constexpr (NC <= kStreamMaxChunks)
-            Streamed<NC, ROLE, CT, L2>::run(a, rb0, tb, te, slot, cu, alpha, beta, cs, c, inv_sigma, lds_col);
+            Streamed<NC, ROLE, CT, L2>::run(a, rb0, tb, te, slot, cu, alpha, beta, beta_lo, cs, K, c, inv_sigma, lds_col);
         else
-            Staged<NC, ROLE, CT, L2>::run(a, rb0, tb, te, slot, cu, alpha, beta, cs, c, inv_sigma, lds_y, lds_col);
+            Staged<NC, ROLE, CT, L2>::run(a, rb0, tb, te, slot, cu, alpha, beta, beta_lo, cs, K, c, inv_sigma, lds_y,
+                                            lds_col);
         if (a.group_counters != nullptr) arrive(a, g);
         u += te - tb;
     }
@@ -812,12 +814,13 @@ void lse_partial_kernel(PartialArgs a) {
     const float sc0 = a.sc[0], sc2 = a.sc[2];                         // a.sc is valid in both modes
     const float sx = packed_scale(a.xr), sy = packed_scale(a.yc);   // 1 for kBF16x3
     const float cb = h1[2], cb_s2 = h1[3], cb_t = h1[4];
+    const float wmax = reinterpret_cast<const float*>(a.yc)[5];   // the column cloud's largest log weight (loop)
     const int skip = *skip_p;
     // The argument fields the segments need, requested with the first batch of argument loads rather than
     // after the scalars have arrived.
     asm volatile("" ::"s"(a.nrb), "s"(a.rows_pad), "s"(a.mode), "s"(a.s.nt), "s"(a.s.P), "s"(a.s.alpha),
                  "s"(a.s.ftot), "s"(a.s.q), "s"(a.s.r), "s"(a.group_counters));
-    asm volatile("" ::"s"(sc0), "s"(sc2), "s"(sx), "s"(sy), "s"(cb), "s"(cb_s2), "s"(cb_t), "v"(skip));
+    asm volatile("" ::"s"(sc0), "s"(sc2), "s"(sx), "s"(sy), "s"(cb), "s"(cb_s2), "s"(cb_t), "s"(wmax), "v"(skip));
     if (skip != 0) return;
     constexpr bool kStream = NC <= kStreamMaxChunks;
     constexpr int kLdsY = kStream ? 1 : 3 * staged_step_tiles(CT) * NC * Contract<CT>::pieces * 64;
@@ -852,17 +855,20 @@ void lse_partial_kernel(PartialArgs a) {
             const float it = 1.0f / cb_t;                  // exact
             // The usual unit t = 1 gets its own inlined copy: with c = 1 a constant, each exponential's argument is
             // the two-operand a - m (v_sub_f32) instead of the three-operand fma.
+            const float K = column_weight_offset(cb_t, wmax);
             if (a.u2 != nullptr && cb_t == 1.0f)
-                segments<NC, ROLE, CT, true>(a, p, wv, a.u2, 1.0f, kLog2e, 1.0f, 1.0f, 1.0f, lds_y, lds_col);
+                segments<NC, ROLE, CT, true>(a, p, wv, a.u2, 1.0f, kLog2e, kLog2eLo, 1.0f, K, 1.0f, 1.0f, lds_y,
+                                             lds_col);
             else if (a.u2 != nullptr)
-                segments<NC, ROLE, CT, true>(a, p, wv, a.u2, 1.0f, kLog2e, cb_t, it, it, lds_y, lds_col);
+                segments<NC, ROLE, CT, true>(a, p, wv, a.u2, 1.0f, kLog2e, kLog2eLo, cb_t, K, it, it, lds_y, lds_col);
             else
-                segments<NC, ROLE, CT, true>(a, p, wv, a.u, alpha, beta, c * cb_t, it, it, lds_y, lds_col);
+                segments<NC, ROLE, CT, true>(a, p, wv, a.u, alpha, beta, 0.0f, c * cb_t, 0.0f, it, it, lds_y, lds_col);
             return;
         }
     }
     const float sigma = sx * sy, inv_sigma = (1.0f / sx) * (1.0f / sy);
-    segments<NC, ROLE, CT, false>(a, p, wv, a.u, alpha, beta, sigma, c * inv_sigma, inv_sigma, lds_y, lds_col);
+    segments<NC, ROLE, CT, false>(a, p, wv, a.u, alpha, beta, 0.0f, sigma, 0.0f, c * inv_sigma, inv_sigma, lds_y,
+                                  lds_col);
 }
 
 template <int NC>

@@ -150,9 +150,10 @@ __device__ inline void bake_header(char* first, const void* second, const BakePa
 // accumulator), so column terms at the magnitude of log w (about -log2 m, the larger part of them at large eps)
 // would give every score a bias of a quarter ulp of that magnitude. The bias differs between the f and g updates
 // when the two clouds' sizes put their terms in different binades, and the balanced iteration keeps the
-// difference, along the neutral mode of the potentials, every iteration (at eps 9 times the typical cost, 2e-5
-// of g after 23 iterations; the reference's float32 path: 4e-8). The offset is uniform over the launch, so the
-// merge restores it exactly; weights that span many binades keep the offset at their maximum.
+// difference, along the neutral mode of the potentials, every iteration (at eps 9 times the typical cost, an
+// offset of 1.4e-5 after 23 iterations where the reference's float32 op sequence drifts 4e-8). The offset is
+// uniform over the launch, so the merge restores it exactly; weights that span many binades keep it at their
+// maximum (columns of weight ~0 then stay far below it, as they should).
 __device__ __forceinline__ float column_weight_offset(float t, float wmax) {
     return __builtin_rintf((t * kLog2e) * wmax);
 }

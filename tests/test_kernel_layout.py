@@ -818,3 +818,39 @@ def test_staged_ring_protocol_catches_a_wrong_stage_distance(ahead):
     step's own) rewrites operands still being read."""
     with pytest.raises(AssertionError):
         staged_protocol([(0, 9)], 8, 2, 3, 2, ahead=ahead)
+
+
+def _round_down_f32(v):
+    """float64 -> float32 rounded toward -inf (a model of the column MFMA's downward rounding of its sum)."""
+    r = v.astype(np.float32)
+    below = r.astype(np.float64) > v
+    r[below] = np.nextafter(r[below], np.float32(-np.inf))
+    return r
+
+
+def test_column_weight_offset_removes_the_column_add_bias():
+    """The on-device loop's column terms q_j = R_j + log2(e) log w_j (log2 units) are added to the dot products by
+    an MFMA that rounds its sum down (measured on gfx950: a quarter ulp of the result on average, never up). With
+    log w ~ -ln m the scores sit at |log2 m| and every row's log-sum-exp is biased low by a fraction of that
+    magnitude's ulp; taking K = rint(log2(e) max log w) off the column terms (and adding it back to the row
+    maximum in double, as the merge does) leaves the bias at the scale of the scores' spread. Modelled here with
+    round-toward-minus-infinity, the worst case of that adder."""
+    rng = np.random.default_rng(5)
+    n, m = 64, 909
+    dots = rng.normal(scale=0.1, size=(n, m))                      # the dot-product part, small at large eps
+    log_w = np.log(rng.uniform(0.2, 1.8, m) / m)                   # about -ln m
+    R = rng.normal(scale=0.05, size=m)
+    q = (R + np.log2(np.e) * log_w).astype(np.float32)             # column terms, rounded once
+    exact = np.log2(np.exp2(dots + q.astype(np.float64)).sum(1))   # the row LSEs (log2) on the float32 terms
+
+    def lse_rd(offset):
+        K = np.float32(np.rint(np.log2(np.e) * log_w.max())) if offset else np.float32(0.0)
+        s = _round_down_f32(dots + (q - K).astype(np.float64))     # the MFMA's sum of the dot part and q - K
+        mx = s.max(1).astype(np.float64)
+        return mx + np.log2(np.exp2(s - mx[:, None]).sum(1)) + float(K)
+
+    bias_plain = float((lse_rd(False) - exact).mean())
+    bias_offset = float((lse_rd(True) - exact).mean())
+    ulp = np.spacing(np.float32(np.abs(q).max()))                   # about 1e-6 at |q| ~ 10
+    assert bias_plain < -0.2 * ulp                                 # the scores' downward rounding shows
+    assert abs(bias_offset) < 0.25 * abs(bias_plain), (bias_plain, bias_offset)

@@ -109,24 +109,49 @@ __global__ void pack_header_kernel(unsigned* __restrict__ header) {
 }
 
 // Word 5 of a packed cloud's header: its largest log weight over the real points (the on-device loop's column
-// offset, column_weight_offset in sk_epilogue.h). One workgroup.
-__global__ __launch_bounds__(256) void weight_max_kernel(const float* __restrict__ log_w, int n,
-                                                         unsigned* __restrict__ header) {
-    __shared__ float s_mx[4];
+// offset, column_weight_offset in sk_epilogue.h). One workgroup of kWeightMaxThreads, eight loads in flight per
+// thread (a cloud of 10,000 points in two rounds).
+constexpr int kWeightMaxThreads = 1024;
+__global__ __launch_bounds__(kWeightMaxThreads) void weight_max_kernel(const float* __restrict__ log_w, int n,
+                                                                       unsigned* __restrict__ header) {
+    __shared__ float s_mx[kWeightMaxThreads / 64];
     float mx = -3.0e38f;
-    for (int i = threadIdx.x; i < n; i += 256) mx = fmaxf(mx, log_w[i]);
+    for (int i0 = 0; i0 < n; i0 += 8 * kWeightMaxThreads) {
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int i = i0 + k * kWeightMaxThreads + (int)threadIdx.x;
+            v[k] = i < n ? log_w[i] : -3.0e38f;
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) mx = fmaxf(mx, v[k]);
+    }
     for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
     if ((threadIdx.x & 63) == 0) s_mx[threadIdx.x >> 6] = mx;
     __syncthreads();
-    if (threadIdx.x == 0) header[5] = __float_as_uint(fmaxf(fmaxf(s_mx[0], s_mx[1]), fmaxf(s_mx[2], s_mx[3])));
+    if (threadIdx.x == 0) {
+        float r = s_mx[0];
+        for (int w = 1; w < kWeightMaxThreads / 64; ++w) r = fmaxf(r, s_mx[w]);
+        header[5] = __float_as_uint(r);
+    }
 }
 
+// I: the element index type (32-bit whenever n d fits, so that the row / column split is a 32-bit division).
+// Four elements per thread per round, their loads in flight together.
+template <typename I>
 __global__ __launch_bounds__(256) void absmax_kernel(const float* __restrict__ src, int n, int d, int ld,
                                                      unsigned* __restrict__ header) {
     float mx = 0.0f;
-    const long long total = (long long)n * d;
-    for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (long long)gridDim.x * blockDim.x)
-        mx = fmaxf(mx, fabsf(src[(i / d) * ld + i % d]));
+    const I total = (I)n * d, stride = (I)gridDim.x * blockDim.x;
+    for (I i0 = (I)blockIdx.x * blockDim.x + threadIdx.x; i0 < total; i0 += 4 * stride) {
+        float v[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const I i = i0 + k * stride;
+            v[k] = i < total ? fabsf(src[(size_t)(i / d) * ld + (size_t)(i % d)]) : 0.0f;
+        }
+        mx = fmaxf(fmaxf(mx, fmaxf(v[0], v[1])), fmaxf(v[2], v[3]));
+    }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
     __shared__ float red[4];
@@ -512,9 +537,14 @@ int sk_pack_cloud_f32(const float* pts, int n, int d, int ld, void* out, void* s
     const long long blocks = (total + threads - 1) / threads;
     hipStream_t st = (hipStream_t)stream;
     const long long elems = (long long)n * d;
-    const long long mblocks = std::min<long long>((elems + threads - 1) / threads, 1024);
+    const long long mblocks = std::min<long long>((elems + threads - 1) / threads, 256);   // one atomic per block
     hipLaunchKernelGGL(pack_header_kernel, dim3(1), dim3(64), 0, st, (unsigned*)out);
-    hipLaunchKernelGGL(absmax_kernel, dim3((unsigned)mblocks), dim3(threads), 0, st, pts, n, d, ld, (unsigned*)out);
+    if (elems + 4LL * mblocks * threads < (1LL << 31))
+        hipLaunchKernelGGL(absmax_kernel<int>, dim3((unsigned)mblocks), dim3(threads), 0, st, pts, n, d, ld,
+                           (unsigned*)out);
+    else
+        hipLaunchKernelGGL(absmax_kernel<long long>, dim3((unsigned)mblocks), dim3(threads), 0, st, pts, n, d, ld,
+                           (unsigned*)out);
     hipLaunchKernelGGL(pack_cloud_kernel, dim3((unsigned)blocks), dim3(threads), 0, st, pts, n, d, ld, (char*)out,
                        npad, nc);
     hipError_t e = hipGetLastError();
@@ -770,10 +800,10 @@ int sk_loop_init_f32(const sk_loop_f32* L, void* stream) {
     hipLaunchKernelGGL(loop_init_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, L->state, loop_cfg(L),
                        lo.counters, lo.ncounters);
     // both clouds' largest log weights into their headers (each is the column cloud of one half-step)
-    hipLaunchKernelGGL(weight_max_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, L->x.log_w, L->x.n,
-                       (unsigned*)const_cast<void*>(L->x.pk));
-    hipLaunchKernelGGL(weight_max_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, L->y.log_w, L->y.n,
-                       (unsigned*)const_cast<void*>(L->y.pk));
+    hipLaunchKernelGGL(weight_max_kernel, dim3(1), dim3(kWeightMaxThreads), 0, (hipStream_t)stream, L->x.log_w,
+                       L->x.n, (unsigned*)const_cast<void*>(L->x.pk));
+    hipLaunchKernelGGL(weight_max_kernel, dim3(1), dim3(kWeightMaxThreads), 0, (hipStream_t)stream, L->y.log_w,
+                       L->y.n, (unsigned*)const_cast<void*>(L->y.pk));
     // x's log2-unit copy for the first iteration's eps and both log2-unit potentials (from fh and the caller's
     // gh); the loop control remakes them when eps changes
     launch_bake(const_cast<void*>(L->x.pk), L->y.pk, L->x.npad, sk_pad_dim(L->d) / 16, L->state->sc_x,

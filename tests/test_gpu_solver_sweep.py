@@ -107,3 +107,27 @@ def test_solver_extreme_aspect_ratios(i):
     ef, eg = inf_rel(res.f, want.f), inf_rel(res.g, want.g)
     print(f"  |f - f64| / |f64| {ef:.2e}, |g - g64| / |g64| {eg:.2e}", flush=True)
     assert ef < TOL and eg < TOL, (ef, eg)
+
+
+@pytest.mark.parametrize("path", ["fixed", "schedule"])
+def test_solver_weights_spanning_many_binades(path):
+    """Weights from 1e-20 to 1 within one cloud (a fifth of the points carry ~1e-20 of the mass): the loop's
+    column weights' offset sits at the largest log weight, so the light columns' terms lie ~66 log2 units below
+    it, and must still contribute exactly nothing more than their weight; balanced, against the float64 oracle."""
+    rng = np.random.default_rng(9700)
+    n, m, d = 300, 500, 8
+    x = rng.normal(size=(n, d))
+    y = rng.normal(size=(m, d)) + 0.2
+    a = rng.uniform(0.5, 1.5, n) * np.where(rng.uniform(size=n) < 0.2, 1e-20, 1.0)
+    b = rng.uniform(0.5, 1.5, m) * np.where(rng.uniform(size=m) < 0.2, 1e-20, 1.0)
+    a, b = a / a.sum(), b / b.sum()
+    opts = dict(fixed_iters=True, max_iters=30, check_every=5, eps=0.2, normalize=True)
+    if path == "schedule":
+        opts.update(eps_start=5.0, eps_decay=0.7)
+    print(f"weights spanning binades, {path}", flush=True)
+    res = sinkhorn(x, y, a, b, opts=SinkhornOptions(kernel="hip", backend=Backend.preset("rocm"), **opts))
+    want = ref.sinkhorn_ref(x, y, a, b, **opts)
+    assert res.iterations == want.iterations == opts["max_iters"]
+    ef, eg = inf_rel(res.f, want.f), inf_rel(res.g, want.g)
+    print(f"  |f - f64| / |f64| {ef:.2e}, |g - g64| / |g64| {eg:.2e}", flush=True)
+    assert ef < TOL and eg < TOL, (ef, eg)

@@ -70,11 +70,11 @@ def test_half_step_random_sweep(hip, k):
     _check_case(hip, _case(k), f"sweep case {k}")
 
 
-# A few points against a large cloud and the reverse: one row group whose columns are split over every
-# workgroup (256 partial slots per row for the merge), and hundreds of row groups against a single column
-# tile; the staged kernel (d 100) and d 1-2 as well.
+# A few points against a large cloud and the reverse, up to a million points: one row group whose columns are
+# split over every workgroup (256 partial slots per row for the merge), and hundreds to thousands of row groups
+# against a single column tile; the staged kernel (d 100) and d 1-2 as well.
 EXTREME = [(5, 150_000, 16), (150_000, 5, 16), (3, 60_000, 100), (60_000, 3, 100), (2, 200_000, 2),
-           (40_000, 1, 64)]
+           (40_000, 1, 64), (1_000_000, 7, 16), (9, 1_000_000, 4)]
 
 
 @pytest.mark.parametrize("i", range(len(EXTREME)))

@@ -494,7 +494,7 @@ def test_emulated_partial_and_finalize_match_logsumexp(rows, m, K, ncu, role, ct
 
 @pytest.mark.parametrize("n,m", [(10_000, 10_000), (7355, 8962), (8962, 7355), (65_536, 65_536), (32, 100_000),
                                  (100_000, 32), (2048, 2048), (1, 5), (5, 150_000), (150_000, 5), (2, 200_000),
-                                 (40_000, 1), (6, 120_000), (120_000, 6)])
+                                 (40_000, 1), (6, 120_000), (120_000, 6), (1_000_000, 7), (9, 1_000_000)])
 @pytest.mark.parametrize("ncu,per_cu", [(256, 1), (304, 1), (80, 1), (256, 2)])
 def test_split_covers_work_and_slot_bounds(n, m, ncu, per_cu):
     """The stream-K split at full sizes: units covered once and each owned by the workgroup whose range holds

@@ -88,7 +88,8 @@ def test_solver_random_sweep(k):
 # A few points against a large cloud, and the reverse: one pass is a single row group whose columns are split
 # over every workgroup (merged by the merge kernel), the other hundreds of row groups against one column tile
 # (merged inside the partial kernel); balanced and unbalanced.
-EXTREME = [(6, 120_000, 16, None), (120_000, 6, 16, 1.0), (3, 50_000, 100, None), (50_000, 3, 100, (0.5, 5.0))]
+EXTREME = [(6, 120_000, 16, None), (120_000, 6, 16, 1.0), (3, 50_000, 100, None), (50_000, 3, 100, (0.5, 5.0)),
+           (1_000_000, 6, 8, None)]
 
 
 @pytest.mark.parametrize("i", range(len(EXTREME)))

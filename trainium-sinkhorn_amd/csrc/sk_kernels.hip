@@ -501,7 +501,7 @@ void launch_bake(void* first, const void* second, int npad, int nc, const float*
 
 extern "C" {
 
-int sk_version(void) { return 300; }
+int sk_version(void) { return 400; }   // 0.4.0: header word 5 (the largest log weight, written by the loop)
 
 const char* sk_last_error(void) { return g_err; }
 

@@ -224,7 +224,7 @@ def staged_protocol(segments, nc, pieces, products, tps, ahead=2):
     LA = D - 1
     NS = products * nc * RB_K
     nsets = 2 if tps == 1 else 1
-    stage_slot = NS // 3
+    stage_slot = NS // 2
     visible = {}                  # ("y", lds tile) / ("c", column buffer, tile of step) -> tile id
     pending = {}                  # writes of the current epoch
     reads = set()                 # regions read in the current epoch

@@ -287,13 +287,13 @@ struct Staged {
     static constexpr int LA = D - 1;                   // chunks read ahead
     static constexpr int TPS = staged_step_tiles(CT);  // tiles per step (one barrier per step)
     static constexpr int NSETS = TPS == 1 ? 2 : 1;     // register sets of staged steps in flight
-    static constexpr int kStageSlot = NS / 3;          // the MFMA slots from which the step two ahead is staged
+    static constexpr int kStageSlot = NS / 2;          // the MFMA slots from which the step two ahead is staged
 
     // Rows rb0 .. rb0 + RB - 1 against column tiles [tb, te); writes one (M, S) per row into `slot`.
     //
     // Pipeline, in steps of TPS tiles (step q: tiles tb + TPS q ..; its operands in LDS buffer q % 3, its column
     // terms in column buffer q % 4):
-    //   - from a third of the way through each step's first tile, spread over a few MFMA slots, step q + 2 is
+    //   - from half-way through each step's first tile, spread over a few MFMA slots, step q + 2 is
     //     written to LDS from registers (its buffer held step q - 1, which every wave finished before the barrier
     //     that ended it) and the same registers are loaded with step q + 2 + NSETS: about two tiles of latency
     //     cover for the global loads;

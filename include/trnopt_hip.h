@@ -151,13 +151,19 @@ int sk_half_step_noalloc_f32(const void* x_pk, const float* xsq, const float* of
  */
 typedef struct sk_cloud_f32 {
     const void* pk;       /* packed points (sk_pack_cloud_f32 layout); the loop rewrites x's log2-unit copy and
-                             writes the cloud's largest log weight into header word 5 at init */
+                             writes the cloud's log2 weight offset rint(log2(e) max log_w) into header word 5 at
+                             init */
     const float* sq;      /* |p|^2 (npad), float64 sums cast to fp32 (src/trnopt/sinkhorn.py:149) */
     const float* log_w;   /* log weights (npad), padding SK_PAD_LOG_WEIGHT */
     const float* w;       /* exp(log_w) (npad), padding 0 */
     const float* off;     /* log(target / reference) (npad) or NULL */
     int n;                /* real points */
     int npad;             /* sk_pad_points(n) */
+    const float* log_w_lo; /* or NULL (zeros): the low part of the log weights, fp32(log w - log_w) from the
+                             caller's float64 log w (padding 0). The loop carries log_w + log_w_lo, so that the two
+                             marginals' total masses agree to float64 rounding: a balanced iteration at an eps far
+                             above the cost scale moves its potentials by eps times their log ratio every
+                             iteration, and log weights rounded to fp32 leave it at a few 1e-8. */
 } sk_cloud_f32;
 
 /* Loop state, device resident, written by the loop's own kernels (layout is part of the ABI). */
@@ -197,7 +203,8 @@ typedef struct sk_loop_f32 {
 
 size_t sk_loop_workspace_bytes(int nx_pad, int ny_pad, int d);
 /* Write the initial state (it = 0, first eps and its scalars); make x's log2-unit copy for that eps
- * (sk_bake_log2_f32) and the loop's log2-unit potentials (c / 2) fh, (c / 2) gh in ws from fh and gh. */
+ * (sk_bake_log2_f32), both clouds' log2 weights (log2(e) log w less an integer offset, as two floats) and the
+ * loop's log2-unit potentials (c / 2) fh, (c / 2) gh in ws from fh and gh. */
 int sk_loop_init_f32(const sk_loop_f32* L, void* stream);
 /* Enqueue `iters` iterations (f update, g update with the loop control in its merge: a partial-kernel launch
  * each, which merges its own row groups from 40 row groups (10k rows) up, and a merge-kernel launch after it

@@ -85,6 +85,8 @@ __host__ __device__ inline int last_wg(int g, const Split& s) { return owner_of(
 //     [0] max |coordinate| (float bits), [1] s, the power-of-two scale of the cloud's own pieces (1 for kBF16x3),
 //     [2] c_b, the score scale its log2-unit copy was made for (0: no valid copy),
 //     [3] the scale of the second cloud that copy was made against, [4] the copy's unit t (a power of two),
+//     [5] L0, the integer offset of the cloud's log2 weights in the on-device loop (a float; written at loop
+//         init, 0 elsewhere),
 // then the tiles of the cloud's own pieces (s x), then (kF16x2 only) the tiles of its log2-unit copy: two fp16
 // pieces of t fl(c_b x) / s_2 per coordinate, which the first cloud of a pair carries so that its piece products
 // with the second cloud's own pieces sum to t c_b x.y, the half-step's score in log2 units times t (see
@@ -125,7 +127,8 @@ struct PartialArgs {
     const void* yc;     // packed columns
     const float* u;     // column term = alpha * u + beta * v  (m_pad each)
     const float* v;
-    float* u2;          // or null: the column cloud's potential in log2 units, (c / 2) u (on-device loop)
+    float* u2;          // or null: the column cloud's potential in log2 units (on-device loop), (c / 2) u + Ll
+    const float* v2;    // with u2: the column cloud's log2 weights Lh (log2(e) log w - L0 = Lh + Ll, L0 in word 5)
     const float* sc;    // {2/eps, 1/eps, eps, kappa} (half-step mode)
     const int* skip;
     float2* part;       // [slot][rows_pad] partial (M, S): M = max_j a_ij, S = sum_j exp2(c (a_ij - M))
@@ -140,7 +143,9 @@ struct PartialArgs {
     const float* xsq;   // |x|^2 (half-step epilogue)
     const float* off;   // log(target / weight) or null
     float* out;         // merged result (fh, or the plain row-LSE)
-    float* out2;        // or null: with log2-unit scores, also the result in log2 units, (c / 2) fh
+    float* out2;        // or null: with log2-unit scores, also the result in log2 units, (c / 2) fh + Ll
+    const float* rows_l2lo;   // with out2: the rows' Ll (the low part of their log2 weights)
+    const float* cols_l2lo;   // with out2 and rebake: the columns' Ll
     int n_store;        // rows of out written
     float2* meas;       // per-group convergence partials (g update of the loop), or null
     const float* w;     // row weights, with meas

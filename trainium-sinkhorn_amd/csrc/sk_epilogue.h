@@ -14,9 +14,9 @@
 namespace sk {
 
 constexpr float kDeltaCap = 50.0f;     // cap of (g_old - g_new) / eps in the balanced check (sinkhorn.py:60)
-constexpr int kMergeBatch = 16;
+constexpr int kMergeBatch = 16;                      // partial slots a merging thread loads at once (their latencies overlap)
 constexpr double kLog2eD = 1.4426950408889634074;   // log2(e) in double
-constexpr double kLn2D = 0.69314718055994530942;     // ln(2) in double        // partial slots a merging thread loads at once (their latencies overlap)
+constexpr double kLn2D = 0.69314718055994530942;     // ln(2) in double
 
 __device__ __forceinline__ float ep_ex2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float ep_lg2(float x) { return __builtin_amdgcn_logf(x); }
@@ -141,22 +141,23 @@ __device__ inline void bake_header(char* first, const void* second, const BakePa
     h[4] = b.valid ? b.t : 1.0f;
 }
 
-// The column weights' offset of the on-device loop's half-steps (scores in log2 units from the first cloud's
-// log2-unit copy, column terms t (R + log2(e) log w)): t log2(e) max_j log w_j, rounded to an integer, with the
-// column cloud's largest log weight from word 5 of its packed header (written at loop init; 0 elsewhere). The
-// partial kernel subtracts it from every column term it stages and the merge adds it back (divided by t, as
-// the slots store M / t) to each row's maximum, in double. The column MFMA rounds its sum downward (a quarter
-// ulp of the result on average, never up: measured on the bf16 MFMA adding a column term to a nonzero
-// accumulator), so column terms at the magnitude of log w (about -log2 m, the larger part of them at large eps)
-// would give every score a bias of a quarter ulp of that magnitude. The bias differs between the f and g updates
-// when the two clouds' sizes put their terms in different binades, and the balanced iteration keeps the
-// difference, along the neutral mode of the potentials, every iteration (at eps 9 times the typical cost, an
-// offset of 1.4e-5 after 23 iterations where the reference's float32 op sequence drifts 4e-8). The offset is
-// uniform over the launch, so the merge restores it exactly; weights that span many binades keep it at their
-// maximum (columns of weight ~0 then stay far below it, as they should).
-__device__ __forceinline__ float column_weight_offset(float t, float wmax) {
-    return __builtin_rintf((t * kLog2e) * wmax);
-}
+// The on-device loop's log2 weights. In log2 units a column term is R_j + log2(e) log w_j (R_j = (c / 2) gh_j,
+// the column cloud's potential). The loop carries each cloud's log2 weights as a double-float relative to an
+// integer offset, log2(e) log w_j - L0 = Lh_j + Ll_j (made at loop init from the caller's log weights and their
+// low parts, log_w + log_w_lo = log w to double precision; L0 = rint(log2(e) max log w) in header word 5), keeps
+// Ll inside the stored potential (u2 = fl(R + Ll)) and stages the column term as t fl(Lh + u2): one rounding at
+// the magnitude of the term relative to the largest weight. The merge adds L0 back to each row's maximum in
+// double. Why the precision: at an eps far above the cost scale every half-step's log-sum-exp is nearly the
+// weights' own log-sum-exp, and a balanced iteration moves its potentials along the neutral mode (f + s, g - s)
+// by eps times the log of the two marginals' effective total masses' ratio each iteration. Log weights rounded
+// to float32 change those masses by a few 1e-8 (relative), so at eps ten times the typical cost the potentials
+// drifted by 1e-6 of their size per iteration (3.6e-4 per iteration at eps 9,746 on a 144 x 435 d 126 raw
+// cloud pair, against none for the float64 run). The reference's float32 op sequence has the same mismatch but
+// no drift: its float32 log of each row's sum, nearly the same number for every row at such an eps, rounds the
+// same way in every row, which makes its iteration flat along the neutral mode. With the log weights carried to
+// double precision the masses match, and the term's one rounding, relative to the largest weight, is at most
+// half an ulp of a few log2 units.
+__device__ __forceinline__ float loop_weight_offset(const void* pk) { return reinterpret_cast<const float*>(pk)[5]; }
 
 // eps of the iteration that starts with `it` iterations done (sinkhorn.py:347-350).
 __device__ inline double eps_for(const LoopCfg& c, int it, int stage) {
@@ -202,12 +203,13 @@ __device__ inline bool merge_group(const PartialArgs& a, int g) {
     const float* h1 = reinterpret_cast<const float*>(a.rows_role == 0 ? a.xr : a.yc);   // the first cloud
     const float* h2 = reinterpret_cast<const float*>(a.rows_role == 0 ? a.yc : a.xr);
     const float cb = h1[2], cb_s2 = h1[3], s2 = h2[1], cb_t = h1[4];
-    const float wmax = reinterpret_cast<const float*>(a.yc)[5];   // the column cloud's largest log weight
+    const float L0 = loop_weight_offset(a.yc);                     // the column cloud's log2 weight offset (loop)
     const int ic = i < a.rows_pad ? i : a.rows_pad - 1;
     const float x2 = a.mode == kHalfStep ? a.xsq[ic] : 0.0f;
     const float o = a.off != nullptr ? a.off[ic] : 0.0f;
     const float old = a.meas != nullptr ? a.out[ic] : 0.0f;
     const float wi = a.meas != nullptr ? a.w[ic] : 0.0f;
+    const float ll = a.rows_l2lo != nullptr ? a.rows_l2lo[ic] : 0.0f;   // the row's Ll (kept in its log2 potential)
     // The first kMergeBatch slots of the row (all there are up to that many workgroups per row group) come with
     // the scalars.
     const int p0 = first_wg(g, a.s), p1 = last_wg(g, a.s);
@@ -216,8 +218,8 @@ __device__ inline bool merge_group(const PartialArgs& a, int g) {
 #pragma unroll
     for (int k = 0; k < kMergeBatch; ++k) v0[k] = p0 + k <= p1 ? ld<COH>(pp + (size_t)k * a.rows_pad) : make_float2(kEmpty, 0.0f);
     const int skip = *skip_p;
-    asm volatile("" ::"s"(sc0), "s"(sc1), "s"(sc2), "s"(sc3), "s"(cb), "s"(cb_s2), "s"(s2), "s"(cb_t), "s"(wmax),
-                 "v"(x2), "v"(o), "v"(old), "v"(wi), "v"(skip));
+    asm volatile("" ::"s"(sc0), "s"(sc1), "s"(sc2), "s"(sc3), "s"(cb), "s"(cb_s2), "s"(s2), "s"(cb_t), "s"(L0),
+                 "v"(x2), "v"(o), "v"(old), "v"(wi), "v"(ll), "v"(skip));
     if (skip != 0) return false;
     const float c_hs = sc0 * kLog2e;
     // log2_ready, on the header words loaded above
@@ -244,10 +246,9 @@ __device__ inline bool merge_group(const PartialArgs& a, int g) {
             M = Mn;
             S = Sn;
         }
-        // the row maximum in the stored units, with the loop's column weights' offset (column_weight_offset)
-        // back on: the slots store M / t with t = cb_t
-        const double Md = (double)M + (l2 && a.u2 != nullptr ? (double)column_weight_offset(cb_t, wmax) / (double)cb_t
-                                                               : 0.0);
+        // the row maximum in the stored units (the slots store M / t with t = cb_t), with the loop's log2 weight
+        // offset of the columns back on (loop_weight_offset)
+        const double Md = (double)M + (l2 && a.u2 != nullptr ? (double)L0 : 0.0);
         // The row's log-sum-exp and the epilogue in double, rounded once: f may be far smaller than the max score
         // and the log of the sum it is the difference of (clouds far from unit scale under normalize=False), so
         // each float rounding of those would cost f relative precision.
@@ -268,11 +269,12 @@ __device__ inline bool merge_group(const PartialArgs& a, int g) {
             if (l2 && a.out2 != nullptr) {
                 // In log2 units, R = (c / 2) fh (the loop's state): (c / 2) eps lse = M + log2 S exactly in the
                 // mathematics, so R = kappa (O - (M + log2 S)) + (kappa - 1) X2 with X2 = (c / 2) |x|^2 and
-                // O = log2(e) off, and fh = R / (c / 2), each rounded once from the double.
+                // O = log2(e) off, and fh = R / (c / 2), each rounded once from the double; the state stored for
+                // the other half-step's column terms is R + Ll (loop_weight_offset).
                 const double k2 = 0.5 * (double)c_hs;
                 const double R = kappa * (od * (double)kLog2eD - (Md + l2s)) + (kappa - 1.0) * (x2d * k2);
                 val = (float)(R / k2);
-                if (i < a.n_store) st<COH>(a.out2 + i, (float)R);
+                if (i < a.n_store) st<COH>(a.out2 + i, (float)(R + (double)ll));
             } else {
                 // eps lse = 2 M + eps ln(S) in accumulator units (log2-unit slots: M / c), with the caller's eps
                 // (float) as the reference's epilogue multiplies by it (src/trnopt/sinkhorn.py:119)
@@ -286,7 +288,10 @@ __device__ inline bool merge_group(const PartialArgs& a, int g) {
             }
             if (i < a.n_store) st<COH>(a.out + i, val);
         } else if (i < a.n_store) {
-            st<COH>(a.out + i, (float)(Md + l2s / (double)kLog2e));   // natural log: l2s / c, c = log2(e)
+            // natural log: ln S = ln(2) log2 S. (The exponentials used c = kLog2e, log2(e) rounded to float32,
+            // 1 - 9e-9 of it, so S sums e^((1 - 9e-9)(a - M)) and ln(2) log2 S errs by 9e-9 |E_p[a - M]|; dividing
+            // log2 S by kLog2e instead would add 9e-9 ln S, one-sided.)
+            st<COH>(a.out + i, (float)(Md + kLn2D * l2s));
         }
     }
     if (a.meas != nullptr) {
@@ -431,12 +436,13 @@ __device__ inline void loop_step(const PartialArgs& a, int g, const LoopCounters
     __syncthreads();
     if (s_done != 0 || s_sc[0] == s_sc0_ran) return;     // same eps next: the copy and the log2 states stand
     // A new eps (a schedule or a stage): the log2-unit potentials R = (c / 2) fh of both clouds again from the
-    // accumulator-unit ones, and the first cloud's log2-unit copy for the new score scale, so that the next f
-    // update already finds them. (This is the g update: rows y, columns x.)
-    const float k2 = 0.5f * (s_sc[0] * kLog2e);
+    // accumulator-unit ones (stored as R + Ll, loop_weight_offset), and the first cloud's log2-unit copy for the
+    // new score scale, so that the next f update already finds them. (This is the g update: rows y, columns x.)
+    const double k2 = 0.5 * (double)(s_sc[0] * kLog2e);
     const int nx = a.s.nt * SK_TILE;
-    for (int i = tid_x(); i < a.rows_pad; i += NT) a.out2[i] = ld<COH>(a.out + i) * k2;
-    for (int i = tid_x(); i < nx; i += NT) a.u2[i] = a.u[i] * k2;
+    for (int i = tid_x(); i < a.rows_pad; i += NT)
+        a.out2[i] = (float)((double)ld<COH>(a.out + i) * k2 + (double)a.rows_l2lo[i]);
+    for (int i = tid_x(); i < nx; i += NT) a.u2[i] = (float)((double)a.u[i] * k2 + (double)a.cols_l2lo[i]);
     const void* second = a.xr;
     const BakeParams b = bake_params(a.rebake, second, s_sc);
     const float* h = reinterpret_cast<const float*>(a.rebake);

@@ -11,8 +11,8 @@
 //
 // the score is c a_ij in log2 units. x_i . y_j is accumulated by fp16 MFMAs from a two-piece fp16 split of
 // the power-of-two scaled fp32 coordinates (sk_lse_partial.hip), bit-identical in the f and g updates; the
-// column term is added after it (for kp <= 64 by one more MFMA, as three exact bf16 pieces; on the VALU above). The running (max, sum) of a
-// row is kept as
+// column term is added after it by one more MFMA, as exact bf16 pieces (column_operand in sk_lse_partial.hip;
+// on the VALU for the bf16 row-LSE). The running (max, sum) of a row is kept as
 //
 //     eps * lse_i = 2 M_i + eps ln(2) log2 S_i,   S_i = sum_j exp2(c (a_ij - M_i)),  M_i = max_j a_ij,
 //
@@ -104,16 +104,16 @@ __global__ void pack_header_kernel(unsigned* __restrict__ header) {
         header[2] = 0u;                     // no log2-unit copy yet
         header[3] = 0u;
         header[4] = __float_as_uint(1.0f);  // the copy's unit
-        header[5] = 0u;                     // the largest log weight (the on-device loop writes it)
+        header[5] = 0u;                     // L0, the loop's log2 weight offset (the on-device loop writes it)
     }
 }
 
-// Word 5 of a packed cloud's header: its largest log weight over the real points (the on-device loop's column
-// offset, column_weight_offset in sk_epilogue.h). One workgroup of kWeightMaxThreads, eight loads in flight per
-// thread (a cloud of 10,000 points in two rounds).
+// Word 5 of a packed cloud's header: the on-device loop's log2 weight offset L0 = rint(log2(e) max log w) over the
+// real points, a float (loop_weight_offset in sk_epilogue.h). One workgroup of kWeightMaxThreads, eight loads in
+// flight per thread (a cloud of 10,000 points in two rounds).
 constexpr int kWeightMaxThreads = 1024;
-__global__ __launch_bounds__(kWeightMaxThreads) void weight_max_kernel(const float* __restrict__ log_w, int n,
-                                                                       unsigned* __restrict__ header) {
+__global__ __launch_bounds__(kWeightMaxThreads) void weight_offset_kernel(const float* __restrict__ log_w, int n,
+                                                                          unsigned* __restrict__ header) {
     __shared__ float s_mx[kWeightMaxThreads / 64];
     float mx = -3.0e38f;
     for (int i0 = 0; i0 < n; i0 += 8 * kWeightMaxThreads) {
@@ -132,7 +132,7 @@ __global__ __launch_bounds__(kWeightMaxThreads) void weight_max_kernel(const flo
     if (threadIdx.x == 0) {
         float r = s_mx[0];
         for (int w = 1; w < kWeightMaxThreads / 64; ++w) r = fmaxf(r, s_mx[w]);
-        header[5] = __float_as_uint(r);
+        header[5] = __float_as_uint((float)rint(kLog2eD * (double)r));
     }
 }
 
@@ -262,14 +262,35 @@ __global__ __launch_bounds__(kRowsPerGroup) void merge_kernel(PartialArgs a) {
     loop_step<false, kRowsPerGroup>(a, (int)blockIdx.x, lc, a.counters);
 }
 
-// The on-device loop's log2-unit potentials from the accumulator-unit ones, R = (c / 2) fh, c = sc[0] log2(e).
-__global__ __launch_bounds__(256) void derive_log2_kernel(const float* __restrict__ fh, float* __restrict__ rf, int nx,
-                                                          const float* __restrict__ gh, float* __restrict__ rg, int ny,
-                                                          const float* __restrict__ sc) {
-    const float k2 = 0.5f * (sc[0] * kLog2e);
+// One cloud's part of the on-device loop's log2 state (loop_weight_offset in sk_epilogue.h): its log2 weights
+// relative to its offset L0 (header word 5, weight_offset_kernel) as a double-float,
+//     log2(e) (log_w + log_w_lo) - L0 = Lh + Ll      (log_w_lo null: zeros; Ll = 0 on padding points),
+// and its log2-unit potential R = (c / 2) fh, c = sc[0] log2(e), stored as R + Ll.
+struct Log2Side {
+    const float* fh;
+    const float* log_w;
+    const float* log_w_lo;
+    const void* pk;
+    float* r;
+    float* lh;
+    float* ll;
+    int n, npad;
+};
+__device__ inline void log2_side(const Log2Side& c, int i, double k2) {
+    if (i >= c.npad) return;
+    const double L0 = (double)loop_weight_offset(c.pk);
+    const double L = kLog2eD * ((double)c.log_w[i] + (c.log_w_lo != nullptr ? (double)c.log_w_lo[i] : 0.0)) - L0;
+    const float lh = (float)L;
+    const float ll = i < c.n ? (float)(L - (double)lh) : 0.0f;
+    c.lh[i] = lh;
+    c.ll[i] = ll;
+    c.r[i] = (float)((double)c.fh[i] * k2 + (double)ll);
+}
+__global__ __launch_bounds__(256) void loop_log2_kernel(Log2Side x, Log2Side y, const float* __restrict__ sc) {
+    const double k2 = 0.5 * (double)(sc[0] * kLog2e);
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < nx) rf[i] = fh[i] * k2;
-    if (i < ny) rg[i] = gh[i] * k2;
+    log2_side(x, i, k2);
+    log2_side(y, i, k2);
 }
 
 // ---------------------------------------------------------------------------------------------------
@@ -372,7 +393,8 @@ struct Pass {
     int kp;
     const float* u;
     const float* v;
-    float* u2;      // the column cloud's log2-unit potential (on-device loop), or null
+    float* u2;      // the column cloud's log2-unit potential + Ll (on-device loop), or null
+    const float* v2;  // with u2: the column cloud's Lh
     const float* sc;
     const int* skip;
     int mode;
@@ -381,7 +403,9 @@ struct Pass {
     const float* xsq;
     const float* off;
     float* out;
-    float* out2;    // the rows' log2-unit potential (on-device loop), or null
+    float* out2;    // the rows' log2-unit potential + Ll (on-device loop), or null
+    const float* rows_l2lo;   // with out2: the rows' Ll
+    const float* cols_l2lo;   // with out2: the columns' Ll
     int n_store;
     float2* meas;
     const float* w;
@@ -402,6 +426,7 @@ hipError_t run_pass(const Pass& ps, const Plan& pl, hipStream_t st) {
     a.u = ps.u;
     a.v = ps.v;
     a.u2 = ps.u2;
+    a.v2 = ps.v2;
     a.sc = ps.sc;
     a.skip = ps.skip;
     a.part = ps.part;
@@ -416,6 +441,8 @@ hipError_t run_pass(const Pass& ps, const Plan& pl, hipStream_t st) {
     a.off = ps.off;
     a.out = ps.out;
     a.out2 = ps.out2;
+    a.rows_l2lo = ps.rows_l2lo;
+    a.cols_l2lo = ps.cols_l2lo;
     a.n_store = ps.n_store;
     a.meas = ps.meas;
     a.w = ps.w;
@@ -501,7 +528,7 @@ void launch_bake(void* first, const void* second, int npad, int nc, const float*
 
 extern "C" {
 
-int sk_version(void) { return 400; }   // 0.4.0: header word 5 (the largest log weight, written by the loop)
+int sk_version(void) { return 500; }   // 0.5.0: sk_cloud_f32.log_w_lo; header word 5 is the loop's log2 weight offset
 
 const char* sk_last_error(void) { return g_err; }
 
@@ -749,14 +776,15 @@ size_t sk_loop_workspace_bytes(int nx_pad, int ny_pad, int d) {
     return std::max(partial_bytes(pf, nx_pad), partial_bytes(pg, ny_pad)) +
            align_up((size_t)meas_count(ny_pad) * sizeof(float2)) +
            align_up((size_t)(1 + std::max(pf.ngroups, pg.ngroups)) * sizeof(int)) +
-           align_up((size_t)nx_pad * sizeof(float)) + align_up((size_t)ny_pad * sizeof(float));
+           3 * (align_up((size_t)nx_pad * sizeof(float)) + align_up((size_t)ny_pad * sizeof(float)));
 }
 
 namespace {
 // The loop's workspace: partial slots (shared by the f and g updates), the g update's per-group convergence
 // partials, the arrival counters (zeroed at init, left zero by every launch: [0] the loop control's, then one
-// per row group for the merge inside the partial kernel), and the two potentials in log2 units, R = (c / 2) fh,
-// that the iteration carries when the scores come in log2 units.
+// per row group for the merge inside the partial kernel), the two potentials in log2 units that the iteration
+// carries when the scores come in log2 units, R = (c / 2) fh stored as R + Ll, and both clouds' log2 weights
+// Lh, Ll (loop_weight_offset in sk_epilogue.h).
 struct LoopLayout {
     Plan pf, pg;
     float2* part;
@@ -765,6 +793,7 @@ struct LoopLayout {
     int ncounters;
     float* rf;
     float* rg;
+    float *lxh, *lxl, *lyh, *lyl;
 };
 
 LoopLayout loop_layout(const sk_loop_f32* L) {
@@ -777,8 +806,13 @@ LoopLayout loop_layout(const sk_loop_f32* L) {
     o.meas = (float2*)((char*)L->ws + part_sz);
     o.counters = (int*)((char*)o.meas + align_up((size_t)meas_count(L->y.npad) * sizeof(float2)));
     o.ncounters = 1 + std::max(o.pf.ngroups, o.pg.ngroups);
+    const size_t bx = align_up((size_t)L->x.npad * sizeof(float)), by = align_up((size_t)L->y.npad * sizeof(float));
     o.rf = (float*)((char*)o.counters + align_up((size_t)o.ncounters * sizeof(int)));
-    o.rg = (float*)((char*)o.rf + align_up((size_t)L->x.npad * sizeof(float)));
+    o.rg = (float*)((char*)o.rf + bx);
+    o.lxh = (float*)((char*)o.rg + by);
+    o.lxl = (float*)((char*)o.lxh + bx);
+    o.lyh = (float*)((char*)o.lxl + bx);
+    o.lyl = (float*)((char*)o.lyh + by);
     return o;
 }
 }  // namespace
@@ -799,18 +833,20 @@ int sk_loop_init_f32(const sk_loop_f32* L, void* stream) {
     const LoopLayout lo = loop_layout(L);
     hipLaunchKernelGGL(loop_init_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, L->state, loop_cfg(L),
                        lo.counters, lo.ncounters);
-    // both clouds' largest log weights into their headers (each is the column cloud of one half-step)
-    hipLaunchKernelGGL(weight_max_kernel, dim3(1), dim3(kWeightMaxThreads), 0, (hipStream_t)stream, L->x.log_w,
+    // both clouds' log2 weight offsets into their headers (each is the column cloud of one half-step)
+    hipLaunchKernelGGL(weight_offset_kernel, dim3(1), dim3(kWeightMaxThreads), 0, (hipStream_t)stream, L->x.log_w,
                        L->x.n, (unsigned*)const_cast<void*>(L->x.pk));
-    hipLaunchKernelGGL(weight_max_kernel, dim3(1), dim3(kWeightMaxThreads), 0, (hipStream_t)stream, L->y.log_w,
+    hipLaunchKernelGGL(weight_offset_kernel, dim3(1), dim3(kWeightMaxThreads), 0, (hipStream_t)stream, L->y.log_w,
                        L->y.n, (unsigned*)const_cast<void*>(L->y.pk));
-    // x's log2-unit copy for the first iteration's eps and both log2-unit potentials (from fh and the caller's
-    // gh); the loop control remakes them when eps changes
+    // x's log2-unit copy for the first iteration's eps, both clouds' log2 weights and both log2-unit potentials
+    // (from fh and the caller's gh); the loop control remakes the copy and the potentials when eps changes
     launch_bake(const_cast<void*>(L->x.pk), L->y.pk, L->x.npad, sk_pad_dim(L->d) / 16, L->state->sc_x,
                 (hipStream_t)stream);
     const int nmax = std::max(L->x.npad, L->y.npad);
-    hipLaunchKernelGGL(derive_log2_kernel, dim3((nmax + 255) / 256), dim3(256), 0, (hipStream_t)stream, L->fh, lo.rf,
-                       L->x.npad, L->gh, lo.rg, L->y.npad, L->state->sc_x);
+    const Log2Side sx = {L->fh, L->x.log_w, L->x.log_w_lo, L->x.pk, lo.rf, lo.lxh, lo.lxl, L->x.n, L->x.npad};
+    const Log2Side sy = {L->gh, L->y.log_w, L->y.log_w_lo, L->y.pk, lo.rg, lo.lyh, lo.lyl, L->y.n, L->y.npad};
+    hipLaunchKernelGGL(loop_log2_kernel, dim3((nmax + 255) / 256), dim3(256), 0, (hipStream_t)stream, sx, sy,
+                       L->state->sc_x);
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? SK_OK : hip_fail(e, "sk_loop_init_f32");
 }
@@ -846,6 +882,7 @@ int sk_loop_run_f32(const sk_loop_f32* L, int iters, void* stream) {
     f.u = L->gh;
     f.v = L->y.log_w;
     f.u2 = lo.rg;
+    f.v2 = lo.lyh;
     f.sc = st->sc_x;
     f.skip = skip;
     f.mode = kHalfStep;
@@ -855,6 +892,8 @@ int sk_loop_run_f32(const sk_loop_f32* L, int iters, void* stream) {
     f.off = L->x.off;
     f.out = L->fh;
     f.out2 = lo.rf;
+    f.rows_l2lo = lo.lxl;
+    f.cols_l2lo = lo.lyl;
     f.n_store = L->x.npad;
     f.tick = st;
     f.part = part;
@@ -869,6 +908,7 @@ int sk_loop_run_f32(const sk_loop_f32* L, int iters, void* stream) {
     g.u = L->fh;
     g.v = L->x.log_w;
     g.u2 = lo.rf;
+    g.v2 = lo.lxh;
     g.sc = st->sc_y;
     g.skip = skip;
     g.mode = kHalfStep;
@@ -878,6 +918,8 @@ int sk_loop_run_f32(const sk_loop_f32* L, int iters, void* stream) {
     g.off = L->y.off;
     g.out = L->gh;
     g.out2 = lo.rg;
+    g.rows_l2lo = lo.lyl;
+    g.cols_l2lo = lo.lxl;
     g.n_store = L->y.npad;
     g.meas = meas;
     g.w = L->y.w;

@@ -33,9 +33,10 @@
 // product of the two scales in both directions): `rows_role` says
 // whether the rows are the first or the second cloud, and the pair list is transposed accordingly. The
 // contraction starts from zero and the column term is added afterwards: by one more MFMA per row block and
-// tile with the fp16 contraction (the fp32 term split exactly into three bf16 pieces, summed against
-// B = (1, 1, 1): exact for every fp32 value, since bf16 has fp32's exponent range; 32 VALU adds per tile
-// fewer), on the VALU otherwise. The max is subtracted before scaling, exp2(c (a - M)), so the dominant term
+// tile with the fp16 contraction (the fp32 term split exactly into bf16 pieces, summed against B = 1:
+// exact for every fp32 value, since bf16 has fp32's exponent range, with q's largest piece in quarters so that
+// the MFMA's rounding of the sum is nearly unbiased, column_operand; 32 VALU adds per tile fewer), on the VALU
+// otherwise. The max is subtracted before scaling, exp2(c (a - M)), so the dominant term
 // is exactly 1.
 //
 // Layout of one workgroup (one row group of 256 rows): wave w owns kRowBlocksK blocks of 32 rows of the
@@ -235,6 +236,35 @@ struct Contract<kBF16x3> {
     }
 };
 
+// The A operand of the column MFMA (v_mfma_f32_32x32x16_bf16 against B = 1 in k < kColPieces of every row): the
+// column term q as bf16 pieces that sum to it exactly, (q0 / 4, q0 / 4, q0 / 4, q0 / 4, q1, q2, 0, 0) with
+// q0 = bf16(q), q1 = bf16(q - q0), q2 = q - q0 - q1 (each piece the nearest bf16 to what the earlier ones leave:
+// 8 + 8 + 8 significand bits, all of fp32's; q0 / 4 is exact for |q| >= 2^-124, and bf16 has fp32's exponent
+// range, so no term is out of range).
+// Why q0 comes in quarters: this MFMA floors its accumulator input onto the grid of half an ulp of its largest
+// product, 2^(e - 24) for a largest product in [2^e, 2^(e+1)), and then rounds the sum to nearest; products
+// below that grid are dropped. (Measured on gfx950 over 4.2 million (accumulator, term) pairs of either sign and
+// magnitude ratios 2^-14 to 2^3: that rule reproduces every result bit for bit.) With q0 whole, an accumulator
+// (the dot product) much smaller than the column term therefore comes out a quarter ulp low on average, a bias
+// toward -inf that does not average out over a row's scores and, at eps far above the scores' spread, moved
+// balanced potentials along their neutral mode. With the largest product q0 / 4 the grid is four times finer and
+// the bias a sixteenth of an ulp (measured: -0.060 against -0.249 ulp of the result); a compensating piece
+// below the grid would be dropped, so none is added.
+constexpr int kColPieces = 6;
+__device__ __forceinline__ bf16x8 column_operand(float v) {
+    const __bf16 q0 = (__bf16)v;
+    const float r1 = v - (float)q0;                       // exact
+    const __bf16 q1 = (__bf16)r1;
+    const __bf16 q2 = (__bf16)(r1 - (float)q1);           // exact: at most 8 significant bits remain
+    const __bf16 qq = (__bf16)((float)q0 * 0.25f);        // exact
+    return bf16x8{qq, qq, qq, qq, q1, q2, 0, 0};
+}
+// The B operand of the column MFMA: 1 in k < kColPieces of every row (lanes 0-31), zeros elsewhere.
+__device__ __forceinline__ bf16x8 column_ones(int h) {
+    const __bf16 one = h == 0 ? (__bf16)1.0f : (__bf16)0.0f;
+    return bf16x8{one, one, one, one, one, one, 0, 0};
+}
+
 // End of a work segment: lanes l and l + 32 hold the same row over different columns; merge them and store
 // (M / sigma, S) of each row (with L2, sigma is the copy's unit t and M / t is in log2 units).
 template <int RB, bool L2>
@@ -302,8 +332,8 @@ struct Staged {
     //     the barrier that ended that step), so that the matrix pipe does not wait on LDS after a barrier;
     //   - one barrier per step.
     __device__ __forceinline__ static void run(const PartialArgs& a, int rb0, int tb, int te, int slot, const float* cu,
-                                               float alpha, float beta, float beta_lo, float cs, float K, float c,
-                                               float inv_sigma, T* lds_y, float* lds_col) {
+                                               const float* cv, float alpha, float beta, float beta_lo, float cs,
+                                               float c, float inv_sigma, T* lds_y, float* lds_col) {
         const int tid = tid_x();
         const int lane = tid & 63;
         const int h = lane >> 5;
@@ -329,19 +359,13 @@ struct Staged {
             S[b] = 0.0f;
         }
 
-        // Staging of one step: for each of its tiles every thread loads PER_THREAD 16-byte units and thread j % 32
-        // the inputs of the column term of column j. Branch-free (clamped indices; threads mapped to the same
-        // element write the same value), so that a whole tile is one basic block and the epilogue stays between
-        // the MFMAs. The loads land in registers that nothing reads until the stage (the column term itself is
-        // formed there), so that no instruction in between waits for them. With FOLD each column term is staged
-        // as the A operand of the column MFMA, three exact bf16 pieces (q = q0 + q1 + q2), 16 bytes per column.
         // Staging of one step. Thread `tid` copies the 16-byte units tid, tid + kBlockK, ... of each tile (clamped:
         // threads mapped to the same unit write the same value), and lane l of every wave the inputs of the column
         // term of column l % 32 of tile (l / 32) % TPS (the waves write the same values). Branch-free, so that a
         // whole tile is one basic block and the epilogue stays between the MFMAs. The loads land in registers that
         // nothing reads until the stage (the column term itself is formed there), so that no instruction in
-        // between waits for them. With FOLD each column term is staged as the A operand of the column MFMA, three
-        // exact bf16 pieces (q = q0 + q1 + q2), 16 bytes per column.
+        // between waits for them. With FOLD each column term is staged as the A operand of the column MFMA, exact bf16
+        // pieces (column_operand), 16 bytes per column.
         const int last = te - 1;
         const int cl = lane & (32 * TPS - 1);             // column (cl % 32) of tile cl / 32 of the step
         unsigned offb[PER_THREAD];                          // byte offsets of this thread's units in a tile
@@ -358,7 +382,7 @@ struct Staged {
         };
         auto prefetch_cols = [&](int s, int t0) {
             const int t = t0 + cl / 32 < te ? t0 + cl / 32 : last;
-            pv[s] = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(a.v + t * 32) + (cl % 32) * 4);
+            pv[s] = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(cv + t * 32) + (cl % 32) * 4);
             pu[s] = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(cu + t * 32) + (cl % 32) * 4);
         };
         auto stage_tile = [&](int s, int tt, int ybuf) {
@@ -367,13 +391,9 @@ struct Staged {
             for (int k = 0; k < PER_THREAD; ++k) *reinterpret_cast<T*>(dst + offb[k]) = pf[s][tt][k];
         };
         auto stage_cols = [&](int s, int cbuf) {
-            const float pc = fmaxf(cs * fmaf(beta, pv[s], fmaf(beta_lo, pv[s], alpha * pu[s])), kPadScore) - K;
+            const float pc = fmaxf(cs * fmaf(beta, pv[s], fmaf(beta_lo, pv[s], alpha * pu[s])), kPadScore);
             if constexpr (FOLD) {
-                const __bf16 q0 = (__bf16)pc;
-                const float r1 = pc - (float)q0;                  // exact
-                const __bf16 q1 = (__bf16)r1;
-                const __bf16 q2 = (__bf16)(r1 - (float)q1);       // exact: at most 8 significant bits remain
-                reinterpret_cast<bf16x8*>(lds_col)[cbuf * TPS * 32 + cl] = bf16x8{q0, q1, q2, 0, 0, 0, 0, 0};
+                reinterpret_cast<bf16x8*>(lds_col)[cbuf * TPS * 32 + cl] = column_operand(pc);
             } else {
                 lds_col[cbuf * TPS * 32 + cl] = pc;
             }
@@ -396,9 +416,8 @@ struct Staged {
 #pragma unroll
             for (int p = 0; p < kPieces; ++p) yr[g % D][p] = lds_y[ytile * TILE16 + (cc * kPieces + p) * 64 + lane];
         };
-        // With FOLD, the B operand of the column MFMA: 1 in k = 0, 1, 2 of every row (lanes 0-31), zeros elsewhere.
-        const __bf16 one = h == 0 ? (__bf16)1.0f : (__bf16)0.0f;
-        const bf16x8 colB = {one, one, one, 0, 0, 0, 0, 0};
+        // With FOLD, the B operand of the column MFMA (column_ones).
+        const bf16x8 colB = column_ones(h);
 
         f32x16 accA[RB], accB[RB];
         Online<RB, L2, FOLD> on;
@@ -539,8 +558,8 @@ struct Streamed {
     static constexpr int kColTiles = col_tiles(FOLD);
 
     __device__ __forceinline__ static void run(const PartialArgs& a, int rb0, int tb, int te, int slot, const float* cu,
-                                               float alpha, float beta, float beta_lo, float cs, float K, float c,
-                                               float inv_sigma, float* lds_col) {
+                                               const float* cv, float alpha, float beta, float beta_lo, float cs,
+                                               float c, float inv_sigma, float* lds_col) {
         const int tid = tid_x();
         const int lane = tid & 63;
         const int h = lane >> 5;
@@ -568,9 +587,8 @@ struct Streamed {
 
         // Column terms into LDS, tile t at (t - cbase) * 32. Without FOLD: tiles [t0 - 1, t1), one float per
         // column (the update of tile t0 - 1 still runs while tile t0's MFMAs do). With FOLD: tiles [t0, t1), each
-        // column term q stored as the A operand of one bf16 MFMA, eight bf16 values (q0, q1, q2, 0, ...) with
-        // q = q0 + q1 + q2 exactly (each piece the nearest bf16 to what the previous ones leave: 8 + 8 + 8
-        // significand bits, all of fp32's; bf16 has fp32's exponent range, so no term is out of range).
+        // column term q stored as the A operand of one bf16 MFMA, eight bf16 values whose sum is q exactly
+        // (column_operand).
         int cbase = tb - 1;
         auto stage_cols = [&](int t0, int t1) {
             __syncthreads();
@@ -584,19 +602,15 @@ struct Streamed {
                     const int k = k0 + q * kBlockK + tid, j = base + k;
                     const int jc = (k < n && j >= 0) ? j : 0;     // clamped in bounds; not stored
                     uu[q] = cu[jc];
-                    vv[q] = a.v[jc];
+                    vv[q] = cv[jc];
                 }
 #pragma unroll
                 for (int q = 0; q < kColBatch; ++q) {
                     const int k = k0 + q * kBlockK + tid, j = base + k;
                     if (k < n && j >= 0) {
-                        const float v = fmaxf(cs * fmaf(beta, vv[q], fmaf(beta_lo, vv[q], alpha * uu[q])), kPadScore) - K;
+                        const float v = fmaxf(cs * fmaf(beta, vv[q], fmaf(beta_lo, vv[q], alpha * uu[q])), kPadScore);
                         if constexpr (FOLD) {
-                            const __bf16 q0 = (__bf16)v;
-                            const float r1 = v - (float)q0;                 // exact
-                            const __bf16 q1 = (__bf16)r1;
-                            const __bf16 q2 = (__bf16)(r1 - (float)q1);     // exact: at most 8 bits remain
-                            reinterpret_cast<bf16x8*>(lds_col)[k] = bf16x8{q0, q1, q2, 0, 0, 0, 0, 0};
+                            reinterpret_cast<bf16x8*>(lds_col)[k] = column_operand(v);
                         } else {
                             lds_col[k] = v;
                         }
@@ -621,10 +635,9 @@ struct Streamed {
         };
         auto colp_of = [&](int t) { return lds_col + (t - cbase) * 32 + 4 * h; };
         // With FOLD, the A operand of tile t's column MFMA (lane l: column l % 32; lanes 32-63 meet zeros in B)
-        // and the B operand (1 in k = 0, 1, 2 of every row, zeros elsewhere): the MFMA adds q0 + q1 + q2 = q.
+        // and the B operand (column_ones): the MFMA adds the pieces of column_operand, whose sum is q.
         auto colA_of = [&](int t) { return reinterpret_cast<const bf16x8*>(lds_col)[(t - cbase) * 32 + (lane & 31)]; };
-        const __bf16 one = h == 0 ? (__bf16)1.0f : (__bf16)0.0f;
-        const bf16x8 colB = {one, one, one, 0, 0, 0, 0, 0};
+        const bf16x8 colB = column_ones(h);
 
         f32x16 accA[RB], accB[RB];
         Online<RB, L2, FOLD> on;
@@ -774,12 +787,12 @@ __device__ inline void arrive(const PartialArgs& a, int g) {
     __syncthreads();   // the next segment's column staging reuses LDS the merge does not touch; keep waves together
 }
 
-// The work segments of workgroup p: a_ij = x_i . y_j + cs (alpha cu_j + (beta + beta_lo) v_j) - K in the kernel's
-// units (K: the column weights' offset of the on-device loop, below; 0 otherwise), scores
-// exp2(c (a - M)) (with L2: exp2(fma(a, c, -c M)), a in log2 units times the copy's unit t = 1 / c).
+// The work segments of workgroup p: a_ij = x_i . y_j + cs (alpha cu_j + (beta + beta_lo) cv_j) in the kernel's
+// units (the column term rounded once, then scaled by a power of two), scores exp2(c (a - M)) (with L2:
+// exp2(fma(a, c, -c M)), a in log2 units times the copy's unit t = 1 / c).
 template <int NC, int ROLE, int CT, bool L2>
-__device__ __forceinline__ void segments(const PartialArgs& a, int p, int wv, const float* cu, float alpha, float beta,
-                                         float beta_lo, float cs, float K, float c, float inv_sigma,
+__device__ __forceinline__ void segments(const PartialArgs& a, int p, int wv, const float* cu, const float* cv,
+                                         float alpha, float beta, float beta_lo, float cs, float c, float inv_sigma,
                                          typename Contract<CT>::T* lds_y, float* lds_col) {
     // The segment bounds are 32-bit integer arithmetic (the divisions expand to vector code); their results are
     // the same in every lane, and readfirstlane hands them to the scalar unit, so the tile loop's counters and
@@ -794,10 +807,11 @@ __device__ __forceinline__ void segments(const PartialArgs& a, int p, int wv, co
         // in the workgroup's barriers.
         const int rb0 = (g * kWavesK + wv) * kRowBlocksK;
         if constexpr (NC <= kStreamMaxChunks)
-            Streamed<NC, ROLE, CT, L2>::run(a, rb0, tb, te, slot, cu, alpha, beta, beta_lo, cs, K, c, inv_sigma, lds_col);
-        else
-            Staged<NC, ROLE, CT, L2>::run(a, rb0, tb, te, slot, cu, alpha, beta, beta_lo, cs, K, c, inv_sigma, lds_y,
+            Streamed<NC, ROLE, CT, L2>::run(a, rb0, tb, te, slot, cu, cv, alpha, beta, beta_lo, cs, c, inv_sigma,
                                             lds_col);
+        else
+            Staged<NC, ROLE, CT, L2>::run(a, rb0, tb, te, slot, cu, cv, alpha, beta, beta_lo, cs, c, inv_sigma, lds_y,
+                                          lds_col);
         if (a.group_counters != nullptr) arrive(a, g);
         u += te - tb;
     }
@@ -814,13 +828,12 @@ void lse_partial_kernel(PartialArgs a) {
     const float sc0 = a.sc[0], sc2 = a.sc[2];                         // a.sc is valid in both modes
     const float sx = packed_scale(a.xr), sy = packed_scale(a.yc);   // 1 for kBF16x3
     const float cb = h1[2], cb_s2 = h1[3], cb_t = h1[4];
-    const float wmax = reinterpret_cast<const float*>(a.yc)[5];   // the column cloud's largest log weight (loop)
     const int skip = *skip_p;
     // The argument fields the segments need, requested with the first batch of argument loads rather than
     // after the scalars have arrived.
     asm volatile("" ::"s"(a.nrb), "s"(a.rows_pad), "s"(a.mode), "s"(a.s.nt), "s"(a.s.P), "s"(a.s.alpha),
                  "s"(a.s.ftot), "s"(a.s.q), "s"(a.s.r), "s"(a.group_counters));
-    asm volatile("" ::"s"(sc0), "s"(sc2), "s"(sx), "s"(sy), "s"(cb), "s"(cb_s2), "s"(cb_t), "s"(wmax), "v"(skip));
+    asm volatile("" ::"s"(sc0), "s"(sc2), "s"(sx), "s"(sy), "s"(cb), "s"(cb_s2), "s"(cb_t), "v"(skip));
     if (skip != 0) return;
     constexpr bool kStream = NC <= kStreamMaxChunks;
     constexpr int kLdsY = kStream ? 1 : 3 * staged_step_tiles(CT) * NC * Contract<CT>::pieces * 64;
@@ -846,28 +859,28 @@ void lse_partial_kernel(PartialArgs a) {
     // With a valid log2-unit copy of the first cloud for this c (log2_ready), the matrix cores produce t c x.y
     // (t, the copy's unit, a power of two; 1 for the usual score scales) and the exponentials take the scores
     // with the exact rescaling by 1 / t fused into the max subtraction. The column term
-    // t c (gh / 2 + eps log b / 2) then comes from the column cloud's potential in log2 units R = (c / 2) gh
-    // when the caller keeps one (u2, the on-device loop: t (R + log2(e) log b), one rounding), else from gh,
-    // scaled by t c. Otherwise the kernel works in units scaled by sigma = s_rows s_cols (a power of two):
-    // column terms times sigma, c divided by it.
+    // t c (gh / 2 + eps log b / 2) then comes, in the on-device loop (u2), from the column cloud's potential in
+    // log2 units plus the low part of its log2 weights, u2 = (c / 2) gh + Ll, and the high part Lh: t (Lh + u2),
+    // one rounding, where Lh + Ll = log2(e) log b - L0 carries the log weights to double precision relative to
+    // the cloud's integer offset L0 (header word 5; the merge adds it back); otherwise from gh, scaled by t c.
+    // Otherwise the kernel works in units scaled by sigma = s_rows s_cols (a power of two): column terms times
+    // sigma, c divided by it.
     if constexpr (CT == kF16x2) {
         if (a.mode == kHalfStep && cb != 0.0f && cb == c && cb_s2 == (ROLE == 0 ? sy : sx)) {
             const float it = 1.0f / cb_t;                  // exact
             // The usual unit t = 1 gets its own inlined copy: with c = 1 a constant, each exponential's argument is
             // the two-operand a - m (v_sub_f32) instead of the three-operand fma.
-            const float K = column_weight_offset(cb_t, wmax);
             if (a.u2 != nullptr && cb_t == 1.0f)
-                segments<NC, ROLE, CT, true>(a, p, wv, a.u2, 1.0f, kLog2e, kLog2eLo, 1.0f, K, 1.0f, 1.0f, lds_y,
-                                             lds_col);
+                segments<NC, ROLE, CT, true>(a, p, wv, a.u2, a.v2, 1.0f, 1.0f, 0.0f, 1.0f, 1.0f, 1.0f, lds_y, lds_col);
             else if (a.u2 != nullptr)
-                segments<NC, ROLE, CT, true>(a, p, wv, a.u2, 1.0f, kLog2e, kLog2eLo, cb_t, K, it, it, lds_y, lds_col);
+                segments<NC, ROLE, CT, true>(a, p, wv, a.u2, a.v2, 1.0f, 1.0f, 0.0f, cb_t, it, it, lds_y, lds_col);
             else
-                segments<NC, ROLE, CT, true>(a, p, wv, a.u, alpha, beta, 0.0f, c * cb_t, 0.0f, it, it, lds_y, lds_col);
+                segments<NC, ROLE, CT, true>(a, p, wv, a.u, a.v, alpha, beta, 0.0f, c * cb_t, it, it, lds_y, lds_col);
             return;
         }
     }
     const float sigma = sx * sy, inv_sigma = (1.0f / sx) * (1.0f / sy);
-    segments<NC, ROLE, CT, false>(a, p, wv, a.u, alpha, beta, 0.0f, sigma, 0.0f, c * inv_sigma, inv_sigma, lds_y,
+    segments<NC, ROLE, CT, false>(a, p, wv, a.u, a.v, alpha, beta, 0.0f, sigma, c * inv_sigma, inv_sigma, lds_y,
                                   lds_col);
 }
 

@@ -44,7 +44,8 @@ _c_float_p = ctypes.c_void_p             # device pointers travel as integers
 
 class SkCloud(ctypes.Structure):
     _fields_ = [("pk", ctypes.c_void_p), ("sq", ctypes.c_void_p), ("log_w", ctypes.c_void_p),
-                ("w", ctypes.c_void_p), ("off", ctypes.c_void_p), ("n", ctypes.c_int), ("npad", ctypes.c_int)]
+                ("w", ctypes.c_void_p), ("off", ctypes.c_void_p), ("n", ctypes.c_int), ("npad", ctypes.c_int),
+                ("log_w_lo", ctypes.c_void_p)]
 
 
 class SkState(ctypes.Structure):
@@ -249,19 +250,23 @@ class HipCloud:
         _check_range("points", max(float(pts.max()), -float(pts.min())) if pts.size else 0.0)   # no |pts| copy
         npad = pad_points(n)
         self.n, self.npad, self.d, self.device, self.role = n, npad, d, device, role
-        # |p|^2 (float64 sums), log w, w and the offset in one host array and one copy to the device; padding
-        # points have |p|^2 = 0, log weight PAD_LOG_WEIGHT (weight exactly 0) and no offset
-        vec = np.zeros((3 if off is None else 4, npad), dtype=np.float32)
+        # |p|^2 (float64 sums), log w, w, the low part of log w and the offset in one host array and one copy to
+        # the device; padding points have |p|^2 = 0, log weight PAD_LOG_WEIGHT (weight exactly 0) and no offset.
+        # log_w_lo = log w - fp32(log w) lets the on-device loop carry the log weights to float64 precision, so
+        # that the two marginals' total masses agree (a mismatch of a few 1e-8 from fp32 log weights moves a
+        # balanced iteration's potentials by eps times it per iteration).
+        vec = np.zeros((4 if off is None else 5, npad), dtype=np.float32)
         vec[0, :n] = np.einsum("ij,ij->i", pts, pts)   # float64 sums, as the reference's, then cast
         L = np.full(npad, PAD_LOG_WEIGHT)
         L[:n] = log_w
         vec[1] = L
         vec[2] = np.exp(L)
+        vec[3, :n] = L[:n] - vec[1, :n].astype(np.float64)
         if off is not None:
-            vec[3, :n] = off
+            vec[4, :n] = off
         dv = torch.from_numpy(vec).to(device)
-        self.sq, self.log_w, self.w = dv[0], dv[1], dv[2]
-        self.off = dv[3] if off is not None else None
+        self.sq, self.log_w, self.w, self.log_w_lo = dv[0], dv[1], dv[2], dv[3]
+        self.off = dv[4] if off is not None else None
         # the points unpadded (the packing pads them to npad x kp with zeros), cast into pinned host memory and
         # copied asynchronously (the caching host allocator keeps the buffer until the copy has run)
         host32 = torch.empty((n, d), dtype=torch.float32, pin_memory=True)
@@ -271,7 +276,7 @@ class HipCloud:
 
     def c_struct(self) -> SkCloud:
         return SkCloud(self.pk.data_ptr(), self.sq.data_ptr(), self.log_w.data_ptr(), self.w.data_ptr(),
-                       _ptr(self.off), self.n, self.npad)
+                       _ptr(self.off), self.n, self.npad, self.log_w_lo.data_ptr())
 
 
 def bake_log2(first: HipCloud, second: HipCloud, sc: torch.Tensor) -> None:

@@ -138,6 +138,9 @@ int sk_half_step_f32(const void* x_pk, const float* xsq, const float* off, int r
  * sk_half_step_workspace_bytes() exceeds SK_NOALLOC_SCRATCH_BYTES is rejected with SK_E_WORKSPACE before
  * anything is enqueued. Every call on one GPU shares that GPU's array: calls that overlap on one GPU
  * (several host threads, or several streams running at once) race and must be serialised by the caller.
+ * The first call on each device looks the array's device address up (hipGetSymbolAddress) and keeps it: make
+ * that first call outside any stream capture; later calls enqueue only the two kernel launches, which a
+ * capture records as kernel nodes (no allocation, no memset).
  */
 #define SK_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
 int sk_half_step_noalloc_f32(const void* x_pk, const float* xsq, const float* off, int rows_pad,

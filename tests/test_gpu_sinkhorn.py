@@ -135,15 +135,25 @@ def test_stress_65k_last_update_matches_float64_on_sampled_columns():
 @pytest.mark.parametrize("log2", ["0", "1"])
 def test_both_score_paths_match_reference(monkeypatch, log2):
     """The loop with x's log2-unit copy (scores in log2 units, the default) and without it (TRNOPT_HIP_LOG2=0:
-    scores scaled on the VALU): the 2048 x 2048 d 64 workload, 100 fixed iterations, and an eps-scaling solve
-    (a copy remade at every eps of the schedule), both within 1e-5 of the oracle's float64 run."""
+    scores scaled on the VALU, the form the loop falls back to only for clouds whose copy cannot exist: all-zero
+    coordinates or score scales beyond 2^+-40): the 2048 x 2048 d 64 workload, 100 fixed iterations, against the
+    oracle's float64 run, with the reference's own float32 op sequence on the same inputs as the bar (there
+    6.1e-6 / 2.8e-6 for f / g). The log2-unit path must be at least as accurate as that sequence (measured 2.8e-6 /
+    1.4e-6); the fallback, which adds eps log w / 2 to the carried potential with a rounding every half-step and so
+    has no exact float fixed point in this cold regime, within 1.5 times it (measured 8.8e-6 / 4.0e-6). Then an
+    eps-scaling solve (a copy remade at every eps of the schedule) within 1e-5."""
     monkeypatch.setenv("TRNOPT_HIP_LOG2", log2)
     x, y = data.balanced_gaussian()
     o = dict(eps=0.1, normalize=False, max_iters=100, fixed_iters=True)
     print("hip 2048 d64, log2 copy", log2, flush=True)
     res = sinkhorn(x, y, opts=hip_opts(**o))
     r64 = ref.sinkhorn_ref(x, y, dtype=torch.float64, **o)
-    assert inf_rel(res.f, r64.f) < 1e-5 and inf_rel(res.g, r64.g) < 1e-5, (inf_rel(res.f, r64.f), inf_rel(res.g, r64.g))
+    r32 = ref.sinkhorn_ref(x, y, dtype=torch.float32, **o)
+    ef, eg = inf_rel(res.f, r64.f), inf_rel(res.g, r64.g)
+    rf, rg = inf_rel(r32.f, r64.f), inf_rel(r32.g, r64.g)
+    print(f"  |f - f64| {ef:.2e} |g - g64| {eg:.2e}; the reference's float32 sequence {rf:.2e} {rg:.2e}", flush=True)
+    bar = 1.0 if log2 == "1" else 1.5
+    assert ef <= bar * rf and eg <= bar * rg, (ef, eg, rf, rg)
     x, y = data.clouds(n=600, m=500, d=16, seed=4)
     o = dict(eps=0.05, eps_start=1.0, eps_decay=0.8, max_iters=60, fixed_iters=True)   # 14 eps steps, then 0.05
     res = sinkhorn(x, y, opts=hip_opts(**o))

@@ -13,6 +13,7 @@ from trnopt.plan import plan_marginals, pull_back
 from trnopt.sinkhorn import SinkhornOptions, sinkhorn, transport_plan
 
 CPU = SinkhornOptions(kernel="torch", backend=Backend.preset("cpu"))
+F32 = SinkhornOptions(kernel="torch", backend=Backend.preset("cpu-float32"))
 ROCM = SinkhornOptions(kernel="hip", backend=Backend.preset("rocm"))
 
 
@@ -92,18 +93,23 @@ def test_pull_back_rejects_bad_vectors():
 @pytest.mark.gpu
 @pytest.mark.parametrize("unbalanced", [False, True])
 def test_gpu_marginals_match_float64(hip, unbalanced):
-    """Two sk_half_step_f32 launches against the float64 torch path on the same potentials."""
+    """Two sk_half_step_f32 launches (scores in log2 units: x's copy made for the result's eps) against the float64
+    torch path on the same potentials, within 1.5 times the error of the same computation in float32 (the
+    reference's float32 op sequence: measured 3.1e-6 / 1.8e-6 relative, the kernel 3.1e-6 / 2.1e-6), and 1e-6
+    absolute."""
     x, y = data.balanced_gaussian(n=2048, m=1500, d=32)
     opts = dict(eps=0.05, normalize="median", max_iters=400, tol=1e-6)
     if unbalanced:
         opts["rho"] = (1.0, 50.0)
     res = sinkhorn(x, y, opts=SinkhornOptions(kernel="hip", backend=Backend.preset("rocm"), **opts))
     r64, c64 = plan_marginals(x, y, res, opts=CPU)
+    r32, c32 = plan_marginals(x, y, res, opts=F32)
     print("marginals on the fused kernel, unbalanced", unbalanced, flush=True)
     rows, cols = plan_marginals(x, y, res, opts=ROCM)
-    print(f"  relative {_rel(rows, r64):.2e} {_rel(cols, c64):.2e}; absolute {np.abs(rows - r64).max():.2e} "
-          f"{np.abs(cols - c64).max():.2e}", flush=True)
-    assert _rel(rows, r64) < 2e-5 and _rel(cols, c64) < 2e-5, (_rel(rows, r64), _rel(cols, c64))
+    print(f"  relative {_rel(rows, r64):.2e} {_rel(cols, c64):.2e} (float32 sequence {_rel(r32, r64):.2e} "
+          f"{_rel(c32, c64):.2e}); absolute {np.abs(rows - r64).max():.2e} {np.abs(cols - c64).max():.2e}", flush=True)
+    assert _rel(rows, r64) <= 1.5 * _rel(r32, r64) and _rel(cols, c64) <= 1.5 * _rel(c32, c64), \
+        (_rel(rows, r64), _rel(cols, c64), _rel(r32, r64), _rel(c32, c64))
     assert np.abs(rows - r64).max() <= 1e-6 and np.abs(cols - c64).max() <= 1e-6
     if unbalanced:
         assert _rel(rows, res.row_mass) < 2e-5
@@ -111,17 +117,23 @@ def test_gpu_marginals_match_float64(hip, unbalanced):
 
 @pytest.mark.gpu
 def test_gpu_pull_back_matches_float64(hip):
+    """wot's ancestor pull-back on the fused kernel against float64, within 1.5 times the float32 sequence's
+    error (measured 3.0e-6 of the largest probability; the kernel 2.4e-6)."""
     x, y = data.balanced_gaussian(n=1000, m=1200, d=16)
     res = sinkhorn(x, y, opts=SinkhornOptions(kernel="hip", backend=Backend.preset("rocm"), eps=0.05,
                                              normalize="median", max_iters=300, tol=1e-6))
     v = np.zeros(len(y))
     v[:300] = 1.0
     want = pull_back(x, y, res, v, opts=CPU)
+    g32 = pull_back(x, y, res, v, opts=F32)
     print("pull-back on the fused kernel", flush=True)
     got = pull_back(x, y, res, v, opts=ROCM)
-    print(f"  pull-back max error {np.abs(np.exp(got) - np.exp(want)).max() / np.exp(want).max():.2e} of max p",
-          flush=True)
-    assert np.abs(np.exp(got) - np.exp(want)).max() < 2e-5 * np.exp(want).max()
+
+    def err(p):
+        return np.abs(np.exp(p) - np.exp(want)).max() / np.exp(want).max()
+
+    print(f"  pull-back max error {err(got):.2e} of max p (float32 sequence {err(g32):.2e})", flush=True)
+    assert err(got) <= 1.5 * err(g32), (err(got), err(g32))
 
 
 # --------------------------------------------------------------------------------------------------------

@@ -1,7 +1,7 @@
 """The no-allocation half-step (sk_half_step_noalloc_f32) against sk_half_step_f32 through the C ABI: the same
 kernels with the partial slots in the library's static device scratch instead of a caller workspace, so the
 outputs must be bit-identical, on two calls in a row (the second smaller, over the slots the first left behind),
-and a shape beyond the scratch must be refused before anything runs."""
+and replayed from a captured HIP graph."""
 
 import numpy as np
 import pytest
@@ -62,14 +62,44 @@ def test_noalloc_half_step_matches_the_workspace_entry_point(hip, first, second)
             assert torch.equal(ma, mb)
 
 
-def test_noalloc_refuses_shapes_beyond_the_scratch(hip):
-    """2,097,184 rows need 16 MiB + 256 bytes of slots: refused with SK_E_WORKSPACE (-3) before any launch."""
+def test_noalloc_half_step_replays_from_a_captured_graph(hip):
+    """For callers under HIP graph capture: after one eager call on the device (which looks up the scratch's
+    device address with hipGetSymbolAddress, outside any capture), the no-alloc half-step is captured as its two
+    kernel launches (no allocation, no memset node) and replayed; every replay, with the program's own eager work
+    and synchronisations between them, gives the eager result bit for bit. (A shape beyond the scratch is refused
+    before any launch: checked on the host, tests/test_host_abi.py.)"""
+    rows, m, d, eps, kappa = 700, 900, 24, 0.07, 0.95
+    X, Y, gh = _pair(hip, rows, m, d, seed=11)
     lb = hip.lib()
-    rows_pad, m_pad, d = (1 << 21) + 32, 32, 4
-    assert lb.sk_half_step_workspace_bytes(rows_pad, m_pad, d) > 16 << 20
-    buf = torch.zeros(1024, dtype=torch.float32, device=DEV)
-    p = buf.data_ptr()
-    st = lb.sk_half_step_noalloc_f32(p, p, None, rows_pad, p, p, p, m_pad, d, 0, p, None, p + 1024, None, None, 1,
-                                     torch.cuda.current_stream().cuda_stream)
-    assert st == -3
-    assert b"static scratch" in lb.sk_last_error()
+    sc = hip.scalars(eps, kappa, DEV)
+
+    def call(fh, stream):
+        return lb.sk_half_step_noalloc_f32(X.pk.data_ptr(), X.sq.data_ptr(), X.off.data_ptr(), X.npad,
+                                           Y.pk.data_ptr(), gh.data_ptr(), Y.log_w.data_ptr(), Y.npad, X.d, 0,
+                                           sc.data_ptr(), None, fh.data_ptr(), None, None, X.n, stream)
+
+    eager = torch.zeros(X.npad, dtype=torch.float32, device=DEV)
+    assert call(eager, torch.cuda.current_stream().cuda_stream) == 0, lb.sk_last_error()
+    torch.cuda.synchronize()
+    assert torch.isfinite(eager).all()
+    out = torch.zeros(X.npad, dtype=torch.float32, device=DEV)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        graph.capture_begin(capture_error_mode="thread_local")
+        try:
+            st = call(out, side.cuda_stream)
+        finally:
+            graph.capture_end()
+    torch.cuda.current_stream().wait_stream(side)
+    assert st == 0, lb.sk_last_error()
+    for k in range(4):
+        print(f"noalloc graph replay {k}", flush=True)
+        out.fill_(float(k) + 0.5)                   # eager work between the replays
+        eager2 = torch.zeros_like(eager)
+        assert call(eager2, torch.cuda.current_stream().cuda_stream) == 0   # the scratch used eagerly meanwhile
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), (out - eager).abs().max()
+        assert torch.equal(eager2, eager)

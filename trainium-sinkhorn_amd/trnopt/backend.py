@@ -50,17 +50,14 @@ class Backend:
 
     def compile_fn(self, f):
         """f through torch.compile when this backend compiles, else f itself. One compiled function per
-        (function, compiler, shape mode) for the whole process: pass problem data as arguments."""
+        (function, compiler) for the whole process: pass problem data as arguments. (The Neuron presets' static
+        shape mode has no device to run on here; torch.compile picks its own shape mode.)"""
         if not self.compile:
             return f
-        dynamic = False if self.device.startswith("neuron") else None
-        if dynamic is False:
-            import torch._dynamo as dynamo
-            dynamo.config.recompile_limit = max(dynamo.config.recompile_limit, 256)
-        key = (f, self.compile_backend or "inductor", dynamic)
+        key = (f, self.compile_backend or "inductor")
         fn = _compiled.get(key)
         if fn is None:
-            fn = _compiled[key] = torch.compile(f, backend=key[1], dynamic=dynamic)
+            fn = _compiled[key] = torch.compile(f, backend=key[1])
         return fn
 
     def tensor(self, a) -> torch.Tensor:

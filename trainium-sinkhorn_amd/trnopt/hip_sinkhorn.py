@@ -291,17 +291,23 @@ def bake_log2(first: HipCloud, second: HipCloud, sc: torch.Tensor) -> None:
 
 
 def half_step(side: HipCloud, other: HipCloud, other_h: torch.Tensor, sc: torch.Tensor, use_off: bool = True,
-              out: torch.Tensor | None = None) -> torch.Tensor:
+              out: torch.Tensor | None = None, log2: bool = False) -> torch.Tensor:
     """One fused half-step: the new shifted potential of `side`'s points (side.npad,) against `other`.
 
     The counterpart of _NkiStep.__call__ (src/trnopt/sinkhorn.py:185-193) and of make_half_step_kernel's
-    kernel (src/trnopt/nki_sinkhorn.py:175-228): sc = {2/eps, 1/eps, eps, kappa} on the device."""
+    kernel (src/trnopt/nki_sinkhorn.py:175-228): sc = {2/eps, 1/eps, eps, kappa} on the device. The scores come
+    in log2 units from the matrix cores when the first cloud of the pair carries its log2-unit copy for sc[0]
+    (bake_log2; the on-device loop keeps one for its current eps), else they are scaled on the VALU. log2=True
+    makes that copy first (one more launch over the first cloud), for callers with no copy of their own."""
     _require_device_f32("other_h", other_h, other.npad)
     _require_device_f32("sc", sc, 4)
     if side.d != other.d:
         raise ValueError("clouds of different dimension")
     if side.role == other.role:
         raise ValueError("a half-step pairs a first cloud (role 0) with a second (role 1)")
+    if log2:
+        first, second = (side, other) if side.role == 0 else (other, side)
+        bake_log2(first, second, sc)
     lb = lib()
     ws = _workspace(lb.sk_half_step_workspace_bytes(side.npad, other.npad, side.d), side.device)
     if out is None:

@@ -57,7 +57,8 @@ def _lse_torch(rows, cols, h_cols, log_w_cols, eps, be, block=2048) -> np.ndarra
 
 def _lse_hip(rows, log_w_rows, cols, h_cols, log_w_cols, eps, opts: SinkhornOptions, role: int) -> np.ndarray:
     """The same on the fused kernel: one sk_half_step_f32 with |x|^2 = 0, no offset, kappa = 1, so that its
-    output is exactly -eps lse."""
+    output is exactly -eps lse, with the scores in log2 units from the matrix cores (the first cloud's log2-unit
+    copy made for this eps first)."""
     from . import hip_sinkhorn as hk
     dev = torch.device(opts.backend.device)
     if dev.index is None:
@@ -68,7 +69,7 @@ def _lse_hip(rows, log_w_rows, cols, h_cols, log_w_cols, eps, opts: SinkhornOpti
         h = torch.zeros(C.npad, dtype=torch.float32, device=dev)
         h[:C.n] = torch.as_tensor(h_cols, dtype=torch.float32)
         R.sq = torch.zeros_like(R.sq)
-        out = hk.half_step(R, C, h, hk.scalars(eps, 1.0, dev), use_off=False)
+        out = hk.half_step(R, C, h, hk.scalars(eps, 1.0, dev), use_off=False, log2=True)
         return (-out[:R.n].to("cpu", torch.float64) / eps).numpy()
 
 

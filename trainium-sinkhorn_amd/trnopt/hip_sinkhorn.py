@@ -261,7 +261,9 @@ class HipCloud:
         L[:n] = log_w
         vec[1] = L
         vec[2] = np.exp(L)
-        vec[3, :n] = L[:n] - vec[1, :n].astype(np.float64)
+        with np.errstate(invalid="ignore"):
+            lo = L[:n] - vec[1, :n].astype(np.float64)
+        vec[3, :n] = np.where(np.isfinite(lo), lo, 0.0)      # (a log weight of -inf has no low part)
         if off is not None:
             vec[4, :n] = off
         dv = torch.from_numpy(vec).to(device)

@@ -275,6 +275,7 @@ def test_matches_torch_path_iteration_for_iteration():
     res = sinkhorn(x, y, opts=hip_opts(**o))
     r32 = ref.sinkhorn_ref(x, y, dtype=torch.float32, **o)
     assert res.converged and r32.converged
+    print("iterations hip", res.iterations, "float32 sequence", r32.iterations, flush=True)
     assert abs(res.iterations - r32.iterations) <= 10
     assert inf_rel(res.f, r32.f) < 1e-4
 
@@ -319,6 +320,7 @@ def test_eps_scaling_matches_torch_path():
     o = dict(eps=0.02, tol=1e-5, max_iters=20_000, eps_start=2.0, eps_decay=0.8)
     res = sinkhorn(x, y, opts=hip_opts(**o))
     r32 = ref.sinkhorn_ref(x, y, dtype=torch.float32, **o)
+    print("iterations hip", res.iterations, "float32 sequence", r32.iterations, flush=True)
     assert res.converged and abs(res.iterations - r32.iterations) <= 10
     assert plan_err(transport_plan(x, y, res), ref.transport_plan(x, y, r32)) < F32_TOL
 
@@ -348,6 +350,7 @@ def test_wot_formulation_matches_wot_scaling(staged):
     r32 = ref.sinkhorn_ref(x, y, np.full(I, 1 / I), np.full(J, 1 / J), eps=eps, rho=(lam1, lam2), normalize="median",
                            tol=1e-6, max_iters=20_000, check_every=5, eps_stages=wot_eps_stages(eps) if staged else None,
                            a_target=G / I, b_target=np.full(J, G.mean() / J), dtype=torch.float32)
+    print("iterations hip", res.iterations, "float32 sequence", r32.iterations, flush=True)
     assert abs(res.iterations - r32.iterations) <= 10
 
 
@@ -407,7 +410,8 @@ def _mass_floor(res, x, y):
 def test_single_cell_unbalanced_matches_oracle_and_float64():
     """The single-cell-shaped unbalanced solve at its full size (7,355 x 8,962, d 30, eps 0.05, rho (1, 50),
     median cost, tol 1e-6, floored to 5e-6 in float32, wot formulation): against the oracle's float32 run of the
-    reference's op sequence on the CPU (iterations within max(30, 20 %), potentials within 1e-5, masses within
+    reference's op sequence on the CPU (iterations within one check, 10, of its count: measured 210 and 210;
+    potentials within 1e-5, masses within
     1e-4) and against float64 through size-independent properties (the last g update recomputed at sampled
     columns, one more f update at sampled rows within the stopping tolerance, masses equal to the float64 plan's
     row and column sums). A kernel whose log-sum-exp carried an iteration-dependent rounding offset stalled at
@@ -423,7 +427,7 @@ def test_single_cell_unbalanced_matches_oracle_and_float64():
     assert rh.converged and r32.converged, (rh.iterations, rh.error, r32.iterations, r32.error)
     print("iterations hip", rh.iterations, "oracle", r32.iterations, "potentials", inf_rel(rh.f, r32.f),
           inf_rel(rh.g, r32.g), flush=True)
-    assert abs(rh.iterations - r32.iterations) <= max(30, r32.iterations // 5), (rh.iterations, r32.iterations)
+    assert abs(rh.iterations - r32.iterations) <= 10, (rh.iterations, r32.iterations)
     assert inf_rel(rh.f, r32.f) < 1e-5 and inf_rel(rh.g, r32.g) < 1e-5
     assert np.abs(rh.row_mass / r32.row_mass - 1).max() < 1e-4
     g_gap, f_step, mass = _check_unbalanced_fixed_point(x, y, rh, a, b, w, b, (1.0, 50.0), 5e-6,
@@ -465,6 +469,7 @@ def test_wot_pipeline_three_pairs_matches_torch_path():
         a = wot_transport_map(pts[t], pts[t + 1], growth_iters=3, opts=gpu)
         b = wot_transport_map(pts[t], pts[t + 1], growth_iters=3, opts=cpu)
         assert a.result.converged and b.result.converged
+        print("  iterations hip", a.iterations, "float32 sequence", b.iterations, flush=True)
         assert abs(a.iterations - b.iterations) <= max(20, b.iterations // 10), (a.iterations, b.iterations)
         for Ga, Gb in zip(a.learned_growth, b.learned_growth):
             assert np.abs(Ga / Gb - 1).max() < 1e-3

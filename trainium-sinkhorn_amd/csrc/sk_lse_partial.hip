@@ -90,6 +90,16 @@ static_assert(32 * kRowBlocksK * kWavesK == kRowsPerGroup, "a row group is 256 r
 
 __device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// A workgroup barrier that orders LDS only: the release / acquire fences are restricted to the local address
+// space, so that the wave waits for its LDS accesses (lgkmcnt) but not for its global loads in flight. (The
+// fences of __syncthreads also cover global memory and made every wave wait for all its outstanding operand
+// loads at the barrier.) For barriers that protect LDS buffers only.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Hardware hands consecutive workgroup ids to the 8 XCDs in turn; renumber so that the workgroups of one
 // XCD own one contiguous range of the work.
 __device__ __forceinline__ int xcd_contiguous(int b, int P) {
@@ -539,9 +549,11 @@ struct Staged {
 };
 
 // Column terms computed into LDS once per run of col_tiles(fold) tiles (streamed variant), 16 bytes per column
-// with FOLD (98 KB of LDS), 4 without (33 KB).
+// with FOLD (98 KB of LDS), 4 without (33 KB), plus one spare entry (col_sink) that the staging's lanes past the
+// run's end write to, so that every staging store is unconditional.
 constexpr int col_tiles(bool fold) { return fold ? 192 : 256; }
-constexpr int col_floats(bool fold) { return fold ? col_tiles(fold) * 32 * 4 : (col_tiles(fold) + 1) * 32; }
+constexpr int col_sink(bool fold) { return fold ? col_tiles(fold) * 32 : (col_tiles(fold) + 1) * 32; }
+constexpr int col_floats(bool fold) { return fold ? (col_sink(fold) + 1) * 4 : col_sink(fold) + 1; }
 constexpr int kColBatch = 8;
 constexpr int kStreamMaxChunks = 4;
 
@@ -588,36 +600,52 @@ struct Streamed {
         // Column terms into LDS, tile t at (t - cbase) * 32. Without FOLD: tiles [t0 - 1, t1), one float per
         // column (the update of tile t0 - 1 still runs while tile t0's MFMAs do). With FOLD: tiles [t0, t1), each
         // column term q stored as the A operand of one bf16 MFMA, eight bf16 values whose sum is q exactly
-        // (column_operand).
+        // (column_operand). Eight column terms per thread per batch, all sixteen loads in flight before the first
+        // use (a run of up to 256 tiles takes at most five batches, a typical segment one).
         int cbase = tb - 1;
-        auto stage_cols = [&](int t0, int t1) {
-            __syncthreads();
-            const int n = (t1 - t0 + (FOLD ? 0 : 1)) * 32, base = (t0 - (FOLD ? 0 : 1)) * 32;
-            // Eight column terms per thread per batch, all sixteen loads in flight before the first use (a
-            // run of up to 256 tiles takes at most five batches, a typical segment one).
-            for (int k0 = 0; k0 < n; k0 += kColBatch * kBlockK) {
-                float uu[kColBatch], vv[kColBatch];
+        auto load_batch = [&](int n, int base, int k0, float (&uu)[kColBatch], float (&vv)[kColBatch]) {
 #pragma unroll
-                for (int q = 0; q < kColBatch; ++q) {
-                    const int k = k0 + q * kBlockK + tid, j = base + k;
-                    const int jc = (k < n && j >= 0) ? j : 0;     // clamped in bounds; not stored
-                    uu[q] = cu[jc];
-                    vv[q] = cv[jc];
-                }
+            for (int q = 0; q < kColBatch; ++q) {
+                const int k = k0 + q * kBlockK + tid, j = base + k;
+                const int jc = (k < n && j >= 0) ? j : 0;         // clamped in bounds; not stored
+                uu[q] = cu[jc];
+                vv[q] = cv[jc];
+            }
+        };
+        // Every store is unconditional (lanes past the run write the spare entry col_sink): behind a branch the
+        // compiler moved the first load of each batch into it, where it waited alone.
+        auto store_batch = [&](int n, int base, int k0, const float (&uu)[kColBatch], const float (&vv)[kColBatch]) {
 #pragma unroll
-                for (int q = 0; q < kColBatch; ++q) {
-                    const int k = k0 + q * kBlockK + tid, j = base + k;
-                    if (k < n && j >= 0) {
-                        const float v = fmaxf(cs * fmaf(beta, vv[q], fmaf(beta_lo, vv[q], alpha * uu[q])), kPadScore);
-                        if constexpr (FOLD) {
-                            reinterpret_cast<bf16x8*>(lds_col)[k] = column_operand(v);
-                        } else {
-                            lds_col[k] = v;
-                        }
-                    }
+            for (int q = 0; q < kColBatch; ++q) {
+                const int k = k0 + q * kBlockK + tid, j = base + k;
+                const int ks = (k < n && j >= 0) ? k : col_sink(FOLD);
+                const float v = fmaxf(cs * fmaf(beta, vv[q], fmaf(beta_lo, vv[q], alpha * uu[q])), kPadScore);
+                if constexpr (FOLD) {
+                    reinterpret_cast<bf16x8*>(lds_col)[ks] = column_operand(v);
+                } else {
+                    lds_col[ks] = v;
                 }
             }
-            __syncthreads();
+        };
+        // The run [t0, t1): the first batch's loads, then `between` (the segment's prologue issues its first
+        // operand tiles there), then the barrier that frees the buffer, the stores and any further batches. The
+        // loads of the hardware's in-order counter complete in issue order, so the column terms, which the
+        // staging needs first, are requested before the operand tiles, and waiting for them does not wait for
+        // the tiles. (Inside the loop over a workgroup's segments the compiler also waited for every earlier
+        // load at the first batch's loop header when the batches were one loop: the first batch is straight-line.)
+        auto stage_cols = [&](int t0, int t1, auto&& between) {
+            const int n = (t1 - t0 + (FOLD ? 0 : 1)) * 32, base = (t0 - (FOLD ? 0 : 1)) * 32;
+            float uu[kColBatch], vv[kColBatch];
+            load_batch(n, base, 0, uu, vv);
+            between();
+            lds_barrier();          // every wave is done reading the previous run's column terms
+            store_batch(n, base, 0, uu, vv);
+            for (int k0 = kColBatch * kBlockK; k0 < n; k0 += kColBatch * kBlockK) {
+                float u2[kColBatch], v2[kColBatch];
+                load_batch(n, base, k0, u2, v2);
+                store_batch(n, base, k0, u2, v2);
+            }
+            lds_barrier();          // the run's column terms are in LDS for every wave
             cbase = t0 - (FOLD ? 0 : 1);
         };
         T yA[NC][kPieces], yB[NC][kPieces];
@@ -675,13 +703,14 @@ struct Streamed {
         // Tiles in pairs so the accumulator and operand buffers alternate without copies; the operand load of
         // the tile after the last is the last tile again (in bounds, unused).
         const int last = te - 1;
-        // The first two operand tiles are requested before the column terms, so that the latencies of the row
-        // operands, the operands and the column terms overlap.
+        // The first two operand tiles are requested right behind the first batch of column terms, so that the
+        // latencies of the row operands, the column terms and the operands overlap.
         int cend = tb + kColTiles < te ? tb + kColTiles : te;
         int t = tb;
-        load_y(t, yA);
-        load_y(t + 1 < te ? t + 1 : last, yB);
-        stage_cols(tb, cend);
+        stage_cols(tb, cend, [&] {
+            load_y(t, yA);
+            load_y(t + 1 < te ? t + 1 : last, yB);
+        });
         tile(accA, accB, nullptr, yA, t, false);
         ++t;
         // The restaging of the column terms (once per kColTiles tiles) and the segment's end are the unlikely
@@ -690,7 +719,7 @@ struct Streamed {
         while (t < te) {
             if (__builtin_expect(t >= cend, 0)) {
                 cend = t + kColTiles < te ? t + kColTiles : te;
-                stage_cols(t, cend);
+                stage_cols(t, cend, [] {});
             }
             load_y(t + 1 < te ? t + 1 : last, yA);
             tile(accB, accA, colp_of(t - 1), yB, t, true);
@@ -701,7 +730,7 @@ struct Streamed {
             }
             if (__builtin_expect(t >= cend, 0)) {
                 cend = t + kColTiles < te ? t + kColTiles : te;
-                stage_cols(t, cend);
+                stage_cols(t, cend, [] {});
             }
             load_y(t + 1 < te ? t + 1 : last, yB);
             tile(accA, accB, colp_of(t - 1), yA, t, true);
@@ -813,6 +842,11 @@ __device__ __forceinline__ void segments(const PartialArgs& a, int p, int wv, co
             Staged<NC, ROLE, CT, L2>::run(a, rb0, tb, te, slot, cu, cv, alpha, beta, beta_lo, cs, c, inv_sigma, lds_y,
                                           lds_col);
         if (a.group_counters != nullptr) arrive(a, g);
+        // The segment's stores complete here, as an s_waitcnt the compiler sees (vmcnt(0); expcnt and lgkmcnt
+        // unrestricted, gfx9 encoding): otherwise the loop's back edge carries the slot stores, whose address and
+        // data registers the next prologue reuses, and the compiler's wait for them there (its counts cannot
+        // tell a store from a load) also held back every operand load of the first segment's prologue.
+        __builtin_amdgcn_s_waitcnt(0x0F70);
         u += te - tb;
     }
 }

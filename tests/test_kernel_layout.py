@@ -14,7 +14,7 @@ import pytest
 from scipy.special import logsumexp
 
 TILE, WAVES, XCDS, RB, BLOCK = 32, 4, 8, 2, 256   # streamed variant: 4 waves of 2 row blocks
-WAVES_K, RB_K, BLOCK_K = 8, 1, 512                 # staged variant: 8 waves of 1 row block
+WAVES_K, RB_K, BLOCK_K = 4, 2, 256                 # staged variant: the same 4 waves of 2 row blocks
 STREAM_MAX_CHUNKS, COL_TILES = 4, 256        # streamed variant: nc <= 4; column terms staged per 256 tiles
 FOLD_COL_TILES = 192                         # ... per 192 tiles with the f16x2 contraction (folded, 16 B each)
 SEG_COST_STREAMED, SEG_COST_STAGED = 6, 2    # cost of a row-group boundary in tiles (sk_kernels.hip make_plan)
@@ -316,9 +316,10 @@ def staged_protocol(segments, nc, pieces, products, tps, ahead=2):
             if fold:
                 read(("c", cq, tt), clamp(t))
             for i in range(NS):
-                cc, p = i // products, i % products
+                # MFMA slot i: chunk cc, product p, row block b (b innermost, as the kernel issues them)
+                cc, p, b = i // (products * RB_K), (i // RB_K) % products, i % RB_K
                 g = ph * nc + cc
-                if p == 0:
+                if p == 0 and b == 0:
                     if cc + LA < nc:
                         read_chunk((g + LA) % (2 * nc), ycur, clamp(t))
                     else:

@@ -39,18 +39,18 @@
 // otherwise. The max is subtracted before scaling, exp2(c (a - M)), so the dominant term
 // is exactly 1.
 //
-// Layout of one workgroup (one row group of 256 rows): wave w owns kRowBlocksK blocks of 32 rows of the
-// group (its fp16 pieces stay in registers for the whole work segment), and all waves walk the same column
-// tiles. Two ways to feed the column tiles, chosen by size and built as separate variants:
-//   - streamed (kp <= 64; 4 waves, one per SIMD, 2 row blocks each): every wave loads the tile's pieces
-//     straight into registers one tile ahead; the four waves of the CU read the same addresses at about the
-//     same time and share them through L1. The column terms of the whole segment are computed once into LDS
-//     (as MFMA operands with the fp16 contraction). No per-tile barrier.
-//   - staged (kp > 64, where a register double buffer no longer fits; 8 waves, two per SIMD, 1 row block
-//     each): the workgroup stages the tiles and their column terms (as bf16 MFMA operands with the fp16
-//     contraction) once in LDS, in steps of two tiles (one with the bf16 contraction) through a ring of three
-//     step buffers, two steps ahead, one barrier per step; each wave reads its column operands chunk by chunk
-//     a few chunks ahead of their MFMAs.
+// Layout of one workgroup (one row group of 256 rows): 4 waves, one per SIMD, and wave w owns 2 blocks of 32
+// rows of the group (its fp16 pieces stay in registers for the whole work segment); all waves walk the same
+// column tiles. Two ways to feed the column tiles, chosen by size and built as separate variants:
+//   - streamed (kp <= 64): every wave loads the tile's pieces straight into registers one tile ahead; the four
+//     waves of the CU read the same addresses at about the same time and share them through L1. The column
+//     terms of the whole segment are computed once into LDS (as MFMA operands with the fp16 contraction). No
+//     per-tile barrier.
+//   - staged (kp > 64, where a register double buffer no longer fits): the workgroup stages the tiles and their
+//     column terms (as bf16 MFMA operands with the fp16 contraction) once in LDS, in steps of two tiles (one
+//     with the bf16 contraction) through a ring of three step buffers, two steps ahead, one barrier per step;
+//     each wave reads its column operands chunk by chunk a few chunks ahead of their MFMAs, once for both of
+//     its row blocks.
 // MFMA orientation: A = 32 columns, B = 32 rows, so lane l's 16 accumulators all belong to row l % 32
 // (columns 8 (r / 4) + 4 (l / 32) + r % 4); row reductions stay inside a lane and lanes l, l + 32 are merged
 // once per segment.
@@ -72,19 +72,14 @@
 namespace sk {
 namespace {
 
-// Waves per workgroup and 32-row blocks per wave of this build's variant; a row group is 256 rows in both.
-//   streamed (kp <= 64): 4 waves, one per SIMD, 2 row blocks each (64 rows of operands and two accumulator chains
-//     per wave, the epilogue interleaved with the MFMAs at compile time);
-//   staged (kp > 64): 8 waves, two per SIMD, one row block each. A wave then holds its row operands (kp / 2
-//     registers), a ring of a few column chunks (32 registers at kp 128), two accumulator sets (32) and the
-//     registers of the step in flight within 256 registers with the MFMA results in VGPRs, where two row blocks
-//     per wave needed ~370 and moved every result out of AGPRs (about 90 VALU instructions per tile); and the two
-//     waves of a SIMD overlap one's exponentials with the other's MFMAs.
-#if SK_PARTIAL_LARGE
-constexpr int kWavesK = 8, kRowBlocksK = 1, kWavesPerSimd = 2;
-#else
+// Waves per workgroup and 32-row blocks per wave, both variants: 4 waves, one per SIMD, 2 row blocks each (two
+// accumulator chains per wave, the epilogue interleaved with the MFMAs at compile time). With one wave per SIMD a
+// wave may use all 512 registers of its lanes, VGPRs and AGPRs: at kp 128 the staged variant holds its row
+// operands (128 registers), a ring of column chunks, two accumulator sets per row block and the step in flight in
+// about 390, the MFMA results in VGPRs and part of the operands in AGPRs, which the MFMAs read directly (a few
+// copies per tile, no scratch). Against 8 waves of one row block (two per SIMD, within 256 registers) it reads
+// each staged chunk from LDS once for two row blocks, half the LDS reads.
 constexpr int kWavesK = 4, kRowBlocksK = 2, kWavesPerSimd = 1;
-#endif
 constexpr int kBlockK = 64 * kWavesK;
 static_assert(32 * kRowBlocksK * kWavesK == kRowsPerGroup, "a row group is 256 rows in both variants");
 

@@ -221,30 +221,24 @@ def mfma_32x32x16(Aop, Bop):
     return D[m, (lane % 32)[:, None]]
 
 
-def ring_depth(nc, pieces):
+def ring_depth(nc):
     """Register slots of the staged kernel's column-chunk ring (sk_lse_partial.hip ring_depth)."""
-    top = 4 if pieces > 2 else 2 * nc
-    for dd in range(4, top + 1):
-        if (2 * nc) % dd == 0:
-            return dd
-    return 2
+    return 4 if (2 * nc) % 4 == 0 else 2
 
 
-def staged_protocol(segments, nc, pieces, products, tps, ahead=2):
-    """Replay the LDS protocol of the staged kernel (sk_lse_partial.hip Staged::run) over the work segments of one
-    workgroup, in program order, with barrier epochs: a write becomes visible to the other waves at the next
-    barrier, and waves interleave arbitrarily between barriers. Asserts that every read (column chunks into the
-    register ring, the column MFMA's operand, the column terms of the previous tile without FOLD) sees data
-    staged for the tile it belongs to (min(t, last)), written in an earlier epoch and not rewritten in the same
-    epoch, and that every MFMA takes its chunk from the ring slot holding it. `ahead` is the stage distance in
-    steps (two in the kernel; other values are planted mistakes). Returns the number of barriers."""
-    fold = pieces == 2
-    D = ring_depth(nc, pieces)
+def staged_protocol(segments, nc, pieces, products, ahead=2):
+    """Replay the LDS protocol of the staged kernel (sk_lse_partial.hip Staged::run, the bf16 row log-sum-exp above
+    kp 64) over the work segments of one workgroup, in program order, with barrier epochs: a write becomes visible
+    to the other waves at the next barrier, and waves interleave arbitrarily between barriers. Asserts that every
+    read (column chunks into the register ring, the column terms of the previous tile) sees data staged for the
+    tile it belongs to (min(t, last)), written in an earlier epoch and not rewritten in the same epoch, and that
+    every MFMA takes its chunk from the ring slot holding it. `ahead` is the stage distance in tiles (two in the
+    kernel; other values are planted mistakes). Returns the number of barriers."""
+    D = ring_depth(nc)
     LA = D - 1
     NS = products * nc * RB_K
-    nsets = 2 if tps == 1 else 1
     stage_slot = NS // 2
-    visible = {}                  # ("y", lds tile) / ("c", column buffer, tile of step) -> tile id
+    visible = {}                  # ("y", lds tile buffer) / ("c", column buffer) -> tile id
     pending = {}                  # writes of the current epoch
     reads = set()                 # regions read in the current epoch
     barriers = [0]
@@ -267,22 +261,14 @@ def staged_protocol(segments, nc, pieces, products, tps, ahead=2):
     for tb, te in segments:
         last = te - 1
         clamp = lambda t: t if t < te else last                           # noqa: E731
-        sets = [None] * nsets                      # tile ids held by each register set (per tile of the step)
+        sets = [None, None]                        # the tile id held by each register set (tile and column inputs)
 
-        def prefetch(sset, t0):
-            sets[sset] = [clamp(t0 + tt) for tt in range(tps)]
-
-        def stage_tile(sset, tt, ybuf):
-            write(("y", ybuf * tps + tt), sets[sset][tt])
-
-        def stage_cols(sset, cbuf):
-            for tt in range(tps):
-                write(("c", cbuf, tt), sets[sset][tt])
+        def prefetch(sset, t):
+            sets[sset] = clamp(t)
 
         def stage(sset, ybuf, cbuf):
-            for tt in range(tps):
-                stage_tile(sset, tt, ybuf)
-            stage_cols(sset, cbuf)
+            write(("y", ybuf), sets[sset])
+            write(("c", cbuf), sets[sset])
 
         ring = {}
         yq, cq = 0, 0
@@ -291,57 +277,40 @@ def staged_protocol(segments, nc, pieces, products, tps, ahead=2):
             read(("y", ytile), tile)
             ring[g % D] = (tile, g % nc)
 
-        if nsets == 2:
-            prefetch(0, tb)
-            prefetch(1, tb + tps)
-            stage(0, 0, 0)
-            stage(1, 1, 1)
-            prefetch(0, tb + 2 * tps)
-            prefetch(1, tb + 3 * tps)
-        else:
-            prefetch(0, tb)
-            stage(0, 0, 0)
-            prefetch(0, tb + tps)
-            stage(0, 1, 1)
-            prefetch(0, tb + 2 * tps)
+        prefetch(0, tb)
+        prefetch(1, tb + 1)
+        stage(0, 0, 0)
+        stage(1, 1, 1)
+        prefetch(0, tb + 2)
+        prefetch(1, tb + 3)
         barrier()
         for g in range(LA):
             read_chunk(g, 0, clamp(tb))
 
         def tile(ph, t, prev):
             nonlocal yq, cq
-            tt = ph % tps
-            ycur = yq * tps + tt
-            ynext = ycur + 1 if tt + 1 < tps else ((yq + 1) % 3) * tps
-            if fold:
-                read(("c", cq, tt), clamp(t))
+            ynext = (yq + 1) % 3
             for i in range(NS):
                 # MFMA slot i: chunk cc, product p, row block b (b innermost, as the kernel issues them)
                 cc, p, b = i // (products * RB_K), (i // RB_K) % products, i % RB_K
                 g = ph * nc + cc
                 if p == 0 and b == 0:
                     if cc + LA < nc:
-                        read_chunk((g + LA) % (2 * nc), ycur, clamp(t))
+                        read_chunk((g + LA) % (2 * nc), yq, clamp(t))
                     else:
                         read_chunk((g + LA) % (2 * nc), ynext, clamp(t + 1))
                 assert ring[g % D] == (clamp(t), cc), (t, cc, ring[g % D])
-                if i == 0 and prev is not None and not fold:
-                    read(("c",) + prev[0], prev[1])                       # the previous tile's column terms
-                if tt == 0:
-                    sset = 0 if nsets == 1 else ph
-                    if i == stage_slot - 2:
-                        stage_cols(sset, (cq + ahead) % 4)
-                    for u in range(tps):
-                        if i == stage_slot + 2 * u:
-                            stage_tile(sset, u, (yq + ahead) % 3)
-                        if i == stage_slot + 2 * u + 1:
-                            sets[sset][u] = clamp(t + (2 + nsets) * tps + u)
-                    if i == stage_slot + 2 * tps:
-                        pass                                              # the column inputs: same tile ids
-            if ph % tps == tps - 1:
-                yq, cq = (yq + 1) % 3, (cq + 1) % 4
-                barrier()
-            return ((cq if ph % tps != tps - 1 else (cq + 3) % 4, tt), clamp(t))
+                if i == 0 and prev is not None:
+                    read(("c", prev[0]), prev[1])                         # the previous tile's column terms
+                if i == stage_slot - 2:
+                    write(("c", (cq + ahead) % 4), sets[ph])
+                if i == stage_slot:
+                    write(("y", (yq + ahead) % 3), sets[ph])
+                if i == stage_slot + 1:
+                    sets[ph] = clamp(t + 4)                               # the tile four ahead, then its column inputs
+            yq, cq = (yq + 1) % 3, (cq + 1) % 4
+            barrier()
+            return ((cq + 3) % 4, clamp(t))
 
         prev = tile(0, tb, None)
         t = tb + 1
@@ -351,8 +320,7 @@ def staged_protocol(segments, nc, pieces, products, tps, ahead=2):
             t += 2
         if t < te:
             prev = tile(1, t, prev)
-        if not fold:
-            read(("c",) + prev[0], prev[1])                               # the last update's column terms
+        read(("c", prev[0]), prev[1])                                     # the last update's column terms
         barrier()
     return barriers[0]
 
@@ -371,7 +339,7 @@ def emulate_lse(xa, ya, role=0, ncu=256, per_cu=1, c=np.log2(np.e), contraction=
     kp, rp, mp = pad_dim(K), pad_points(rows), pad_points(m)
     nc = kp // 16
     tile16 = nc * PIECES * 64
-    staged_variant = nc > STREAM_MAX_CHUNKS
+    staged_variant = nc > STREAM_MAX_CHUNKS and contraction != "f16x2"   # sk_lse_partial.hip streamed_form
     waves, rbk, block = (WAVES_K, RB_K, BLOCK_K) if staged_variant else (WAVES, RB, BLOCK)
     per_thread = -(-tile16 // block)
     sx, xr = pack(xa, rows, K, contraction)
@@ -405,7 +373,7 @@ def emulate_lse(xa, ya, role=0, ncu=256, per_cu=1, c=np.log2(np.e), contraction=
             assert 0 <= slot < slots
             seen[g, tb:te] += 1
             staged = {}
-            if nc <= STREAM_MAX_CHUNKS:
+            if not staged_variant:
                 # streamed: column terms of runs of col_tiles tiles into LDS; operands straight from memory.
                 # Folded (f16x2): 16 bytes per column, the A operand of the column MFMA (lane l: column l % 32).
                 col_tiles = FOLD_COL_TILES if fold else COL_TILES
@@ -430,20 +398,14 @@ def emulate_lse(xa, ya, role=0, ncu=256, per_cu=1, c=np.log2(np.e), contraction=
                 assert max(loads) * tile16 + tile16 - 1 < yc.shape[0]
             if staged_variant:
                 # staged: the LDS protocol of the ring (asserted), then each tile's operands and column terms
-                staged_protocol([(tb, te)], nc, PIECES, len(FIRST_), 2 if contraction == "f16x2" else 1)
+                staged_protocol([(tb, te)], nc, PIECES, len(FIRST_))
                 for k in range(per_thread):
                     idx = np.where(tid + k * block < tile16, tid + k * block, tile16 - 1)
                     assert idx.max() < tile16 and (te - 1) * tile16 + idx.max() < yc.shape[0]
                 for t in range(tb, te):
                     assert t * 32 + 31 < mp
                     gi = t * tile16 + np.arange(tile16)
-                    if fold:
-                        q = np.zeros((64, 8), dtype=np.float32)
-                        for sl, piece in enumerate(fold_rule[0](u[t * 32 + (lane & 31)])):
-                            q[:, sl] = piece
-                        staged[t] = (yc[gi].copy(), q)
-                    else:
-                        staged[t] = (yc[gi].copy(), u[t * 32 + np.arange(32)].copy())
+                    staged[t] = (yc[gi].copy(), u[t * 32 + np.arange(32)].copy())
             for wv in range(waves):
                 rb0 = (g * waves + wv) * rbk
                 for bb in range(rbk):
@@ -849,31 +811,30 @@ def test_folded_column_terms_cover_small_and_mixed_scale_clouds(case):
 
 
 @pytest.mark.parametrize("nc", [5, 6, 7, 8])
-@pytest.mark.parametrize("ct", ["f16x2", "bf16x3"])
-def test_staged_ring_protocol(nc, ct):
-    """The staged kernel's LDS ring (three step buffers, four column buffers, steps of two tiles with f16x2 and
-    one with bf16x3, the column chunks read ahead into a register ring) over segments of every length from 1 to
-    13 tiles, one after another in one workgroup as the work split hands them out: every read sees its own
-    tile's data, staged in an earlier barrier epoch and not rewritten in its own; one barrier per step plus two
-    per segment."""
-    pieces, first, _ = CONTRACTIONS[ct]
-    tps = 2 if ct == "f16x2" else 1
+def test_staged_ring_protocol(nc):
+    """The staged kernel's LDS ring (the bf16 row log-sum-exp above kp 64: three tile buffers, four column
+    buffers, the column chunks read ahead into a register ring) over segments of every length from 1 to 13 tiles,
+    one after another in one workgroup as the work split hands them out: every read sees its own tile's data,
+    staged in an earlier barrier epoch and not rewritten in its own; one barrier per tile plus two per segment."""
+    pieces, first, _ = CONTRACTIONS["bf16x3"]
     lengths = range(1, 14)
     segs, t0 = [], 0
     for n in lengths:
         segs.append((t0, t0 + n))
         t0 += n + 3
-    nb = staged_protocol(segs, nc, pieces, len(first), tps)
-    assert nb == sum(2 + (n if tps == 1 else n // 2) for n in lengths)
+    nb = staged_protocol(segs, nc, pieces, len(first))
+    assert nb == sum(2 + n for n in lengths)
 
 
+@pytest.mark.parametrize("nc", [5, 8])
 @pytest.mark.parametrize("ahead", [1, 3])
-def test_staged_ring_protocol_catches_a_wrong_stage_distance(ahead):
-    """Planted mistakes: staging the step `ahead` steps ahead instead of two. One ahead writes the buffer of the
-    step whose first chunks the current step's last tile reads; three ahead (into buffer q % 3, the current
-    step's own) rewrites operands still being read."""
+def test_staged_ring_protocol_catches_a_wrong_stage_distance(nc, ahead):
+    """Planted mistakes: staging the tile `ahead` tiles ahead instead of two. One ahead writes the buffer whose
+    first chunks the current tile's last MFMAs read; three ahead (into buffer q % 3, the current tile's own)
+    rewrites operands still being read."""
+    pieces, first, _ = CONTRACTIONS["bf16x3"]
     with pytest.raises(AssertionError):
-        staged_protocol([(0, 9)], 8, 2, 3, 2, ahead=ahead)
+        staged_protocol([(0, 9)], nc, pieces, len(first), ahead=ahead)
 
 
 def _round_down_f32(v):

@@ -41,23 +41,22 @@
 //
 // Layout of one workgroup (one row group of 256 rows): 4 waves, one per SIMD, and wave w owns 2 blocks of 32
 // rows of the group (its fp16 pieces stay in registers for the whole work segment); all waves walk the same
-// column tiles. Two ways to feed the column tiles, chosen by size and built as separate variants:
-//   - streamed (kp <= 64): every wave loads the tile's pieces straight into registers one tile ahead; the four
-//     waves of the CU read the same addresses at about the same time and share them through L1. The column
-//     terms of the whole segment are computed once into LDS (as MFMA operands with the fp16 contraction). No
-//     per-tile barrier.
-//   - staged (kp > 64, where a register double buffer no longer fits): the workgroup stages the tiles and their
-//     column terms (as bf16 MFMA operands with the fp16 contraction) once in LDS, in steps of two tiles (one
-//     with the bf16 contraction) through a ring of three step buffers, two steps ahead, one barrier per step;
-//     each wave reads its column operands chunk by chunk a few chunks ahead of their MFMAs, once for both of
-//     its row blocks.
+// column tiles. Two ways to feed the column tiles (streamed_form):
+//   - streamed (every fp16 half-step, and the bf16 row log-sum-exp up to kp 64): every wave loads the tile's
+//     pieces straight into registers one tile ahead; the four waves of the CU read the same addresses at about
+//     the same time and share them through L1. The column terms of the whole segment are computed once into LDS
+//     (as MFMA operands with the fp16 contraction). No per-tile barrier.
+//   - staged (the bf16 row log-sum-exp above kp 64, whose three pieces per coordinate no longer fit in registers
+//     twice): the workgroup stages the tiles and their column terms once in LDS through a ring of three tile
+//     buffers, two tiles ahead, one barrier per tile; each wave reads its column operands chunk by chunk a few
+//     chunks ahead of their MFMAs, once for both of its row blocks.
 // MFMA orientation: A = 32 columns, B = 32 rows, so lane l's 16 accumulators all belong to row l % 32
 // (columns 8 (r / 4) + 4 (l / 32) + r % 4); row reductions stay inside a lane and lanes l, l + 32 are merged
 // once per segment.
 //
-// This file is compiled twice: SK_PARTIAL_LARGE = 0 builds the streamed instantiations (nc <= 4),
-// SK_PARTIAL_LARGE = 1 the staged ones (nc > 4), both with MFMA results forced into VGPRs
-// (-mllvm -amdgpu-mfma-vgpr-form: the epilogue reads them without copies).
+// This file is compiled twice: SK_PARTIAL_LARGE = 0 builds the instantiations of nc <= 4, SK_PARTIAL_LARGE = 1
+// those of nc > 4 (kp 80 to 128), both with MFMA results forced into VGPRs (-mllvm -amdgpu-mfma-vgpr-form: the
+// epilogue reads them without copies).
 
 #include <type_traits>
 #include <utility>
@@ -74,11 +73,10 @@ namespace {
 
 // Waves per workgroup and 32-row blocks per wave, both variants: 4 waves, one per SIMD, 2 row blocks each (two
 // accumulator chains per wave, the epilogue interleaved with the MFMAs at compile time). With one wave per SIMD a
-// wave may use all 512 registers of its lanes, VGPRs and AGPRs: at kp 128 the staged variant holds its row
-// operands (128 registers), a ring of column chunks, two accumulator sets per row block and the step in flight in
-// about 390, the MFMA results in VGPRs and part of the operands in AGPRs, which the MFMAs read directly (a few
-// copies per tile, no scratch). Against 8 waves of one row block (two per SIMD, within 256 registers) it reads
-// each staged chunk from LDS once for two row blocks, half the LDS reads.
+// wave may use all 512 registers of its lanes, VGPRs and AGPRs: at kp 128 the streamed variant holds its row
+// operands (128 registers), two column tiles (128), two accumulator sets per row block and the epilogue in about
+// 390, the MFMA results in VGPRs and part of the operands in AGPRs, which the MFMAs read directly (about 30
+// register copies per tile, no scratch).
 constexpr int kWavesK = 4, kRowBlocksK = 2, kWavesPerSimd = 1;
 constexpr int kBlockK = 64 * kWavesK;
 static_assert(32 * kRowBlocksK * kWavesK == kRowsPerGroup, "a row group is 256 rows in both variants");
@@ -296,19 +294,13 @@ __device__ __forceinline__ void store_rows(const PartialArgs& a, const float (&M
 
 // Register ring of the staged kernel's column operands: chunk g of a pair of tiles (g = 0 .. 2 nc - 1) sits in
 // slot g % D, read D - 1 chunks ahead of its MFMAs; D divides 2 nc so that the slots repeat every two tiles.
-constexpr int ring_depth(int nc, int pieces) {
-    const int top = pieces > 2 ? 4 : 2 * nc;          // three-piece chunks: at most 4 slots (48 registers)
-    for (int dd = 4; dd <= top; ++dd)
-        if ((2 * nc) % dd == 0) return dd;
-    return 2;
-}
+constexpr int ring_depth(int nc) { return (2 * nc) % 4 == 0 ? 4 : 2; }   // three-piece chunks: at most 48 registers
 
-// Tiles per step of the staged kernel: two with the fp16 contraction (96 KB of column operands in flight at
-// kp 128), one with the bf16 one (whose tiles are 1.5 times larger).
-constexpr int staged_step_tiles(int ct) { return ct == kF16x2 ? 2 : 1; }
-
+// The staged kernel: the general row log-sum-exp (three bf16 pieces, six products, ROLE 0, no log2-unit copy)
+// above kp 64, where its operands no longer fit in registers twice. (The fp16 half-steps stream at every kp.)
 template <int NC, int ROLE, int CT, bool L2>
 struct Staged {
+    static_assert(CT == kBF16x3 && ROLE == 0 && !L2, "the staged kernel runs the bf16 row log-sum-exp only");
     using C = Contract<CT>;
     using T = typename C::T;
     static constexpr int kPieces = C::pieces;
@@ -317,35 +309,30 @@ struct Staged {
     static constexpr int TILE16 = NC * kPieces * 64;   // 16-byte units per packed 32-point tile
     static constexpr int PER_THREAD = (TILE16 + kBlockK - 1) / kBlockK;
     static constexpr int NS = kProducts * NC * RB;     // MFMA slots per tile
-    static constexpr bool FOLD = CT == kF16x2;         // column terms added by the matrix pipe
-    static constexpr int D = ring_depth(NC, kPieces);  // register slots of column chunks
+    static constexpr int D = ring_depth(NC);           // register slots of column chunks
     static constexpr int LA = D - 1;                   // chunks read ahead
-    static constexpr int TPS = staged_step_tiles(CT);  // tiles per step (one barrier per step)
-    static constexpr int NSETS = TPS == 1 ? 2 : 1;     // register sets of staged steps in flight
-    static constexpr int kStageSlot = NS / 2;          // the MFMA slots from which the step two ahead is staged
+    static constexpr int kStageSlot = NS / 2;          // the MFMA slots from which the tile two ahead is staged
 
     // Rows rb0 .. rb0 + RB - 1 against column tiles [tb, te); writes one (M, S) per row into `slot`.
     //
-    // Pipeline, in steps of TPS tiles (step q: tiles tb + TPS q ..; its operands in LDS buffer q % 3, its column
-    // terms in column buffer q % 4):
-    //   - from half-way through each step's first tile, spread over a few MFMA slots, step q + 2 is
-    //     written to LDS from registers (its buffer held step q - 1, which every wave finished before the barrier
-    //     that ended it) and the same registers are loaded with step q + 2 + NSETS: about two tiles of latency
-    //     cover for the global loads;
-    //   - the column operands of a tile are read chunk by chunk, LA chunks ahead of their MFMAs, the last ones
-    //     of a tile already reading the first chunks of the next (staged at least a step earlier, visible since
-    //     the barrier that ended that step), so that the matrix pipe does not wait on LDS after a barrier;
-    //   - one barrier per step.
+    // Pipeline, tile by tile (tile q = tb + q: its operands in LDS buffer q % 3, its column terms in column buffer
+    // q % 4):
+    //   - from half-way through each tile, spread over a few MFMA slots, tile q + 2 is written to LDS from
+    //     registers (its buffer held tile q - 1, which every wave finished before the barrier that ended it) and the
+    //     same registers are loaded with tile q + 4 (two register sets, by the parity of q): about two tiles of
+    //     latency cover for the global loads;
+    //   - the column operands of a tile are read chunk by chunk, LA chunks ahead of their MFMAs, the last ones of a
+    //     tile already reading the first chunks of the next (staged at least a tile earlier, visible since the
+    //     barrier that ended that tile), so that the matrix pipe does not wait on LDS after a barrier;
+    //   - one barrier per tile.
     __device__ __forceinline__ static void run(const PartialArgs& a, int rb0, int tb, int te, int slot, const float* cu,
                                                const float* cv, float alpha, float beta, float beta_lo, float cs,
                                                float c, float inv_sigma, T* lds_y, float* lds_col) {
         const int tid = tid_x();
         const int lane = tid & 63;
         const int h = lane >> 5;
-        // With L2 the first cloud of the pair (the rows for ROLE 0, the columns for ROLE 1) is read from its
-        // log2-unit copy.
-        const T* xt = L2 && ROLE == 0 ? packed_log2_tiles<T>(a.xr, a.nrb * 32, NC) : packed_tiles<T>(a.xr);
-        const T* yt = L2 && ROLE == 1 ? packed_log2_tiles<T>(a.yc, a.s.nt * 32, NC) : packed_tiles<T>(a.yc);
+        const T* xt = packed_tiles<T>(a.xr);
+        const T* yt = packed_tiles<T>(a.yc);
 
         T xv[RB][NC][kPieces];
 #pragma unroll
@@ -364,53 +351,44 @@ struct Staged {
             S[b] = 0.0f;
         }
 
-        // Staging of one step. Thread `tid` copies the 16-byte units tid, tid + kBlockK, ... of each tile (clamped:
-        // threads mapped to the same unit write the same value), and lane l of every wave the inputs of the column
-        // term of column l % 32 of tile (l / 32) % TPS (the waves write the same values). Branch-free, so that a
-        // whole tile is one basic block and the epilogue stays between the MFMAs. The loads land in registers that
+        // Staging of one tile. Thread `tid` copies the 16-byte units tid, tid + kBlockK, ... of the tile (clamped:
+        // threads mapped to the same unit write the same value), and lane l % 32 of every wave the inputs of the
+        // column term of column l % 32 (the lanes and waves write the same values). Branch-free, so that a whole
+        // tile is one basic block and the epilogue stays between the MFMAs. The loads land in registers that
         // nothing reads until the stage (the column term itself is formed there), so that no instruction in
-        // between waits for them. With FOLD each column term is staged as the A operand of the column MFMA, exact bf16
-        // pieces (column_operand), 16 bytes per column.
+        // between waits for them.
         const int last = te - 1;
-        const int cl = lane & (32 * TPS - 1);             // column (cl % 32) of tile cl / 32 of the step
+        const int cl = lane & 31;                           // column of the tile
         unsigned offb[PER_THREAD];                          // byte offsets of this thread's units in a tile
 #pragma unroll
         for (int k = 0; k < PER_THREAD; ++k)
             offb[k] = (unsigned)(tid + k * kBlockK < TILE16 ? tid + k * kBlockK : TILE16 - 1) * 16u;
-        T pf[NSETS][TPS][PER_THREAD];
-        float pv[NSETS], pu[NSETS];
-        auto tile_ptr = [&](int t) { return reinterpret_cast<const char*>(yt + (size_t)(t < te ? t : last) * TILE16); };
-        auto prefetch_tile = [&](int s, int tt, int t0) {
-            const char* src = tile_ptr(t0 + tt);
+        T pf[2][PER_THREAD];
+        float pv[2], pu[2];
+        auto prefetch_tile = [&](int s, int t) {
+            const char* src = reinterpret_cast<const char*>(yt + (size_t)(t < te ? t : last) * TILE16);
 #pragma unroll
-            for (int k = 0; k < PER_THREAD; ++k) pf[s][tt][k] = *reinterpret_cast<const T*>(src + offb[k]);
+            for (int k = 0; k < PER_THREAD; ++k) pf[s][k] = *reinterpret_cast<const T*>(src + offb[k]);
         };
-        auto prefetch_cols = [&](int s, int t0) {
-            const int t = t0 + cl / 32 < te ? t0 + cl / 32 : last;
-            pv[s] = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(cv + t * 32) + (cl % 32) * 4);
-            pu[s] = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(cu + t * 32) + (cl % 32) * 4);
+        auto prefetch_cols = [&](int s, int t) {
+            const int tc = t < te ? t : last;
+            pv[s] = cv[tc * 32 + cl];
+            pu[s] = cu[tc * 32 + cl];
         };
-        auto stage_tile = [&](int s, int tt, int ybuf) {
-            char* dst = reinterpret_cast<char*>(lds_y + (ybuf * TPS + tt) * TILE16);
+        auto stage_tile = [&](int s, int ybuf) {
+            char* dst = reinterpret_cast<char*>(lds_y + ybuf * TILE16);
 #pragma unroll
-            for (int k = 0; k < PER_THREAD; ++k) *reinterpret_cast<T*>(dst + offb[k]) = pf[s][tt][k];
+            for (int k = 0; k < PER_THREAD; ++k) *reinterpret_cast<T*>(dst + offb[k]) = pf[s][k];
         };
         auto stage_cols = [&](int s, int cbuf) {
-            const float pc = fmaxf(cs * fmaf(beta, pv[s], fmaf(beta_lo, pv[s], alpha * pu[s])), kPadScore);
-            if constexpr (FOLD) {
-                reinterpret_cast<bf16x8*>(lds_col)[cbuf * TPS * 32 + cl] = column_operand(pc);
-            } else {
-                lds_col[cbuf * TPS * 32 + cl] = pc;
-            }
+            lds_col[cbuf * 32 + cl] = fmaxf(cs * fmaf(beta, pv[s], fmaf(beta_lo, pv[s], alpha * pu[s])), kPadScore);
         };
-        auto prefetch = [&](int s, int t0) {
-#pragma unroll
-            for (int tt = 0; tt < TPS; ++tt) prefetch_tile(s, tt, t0);
-            prefetch_cols(s, t0);
+        auto prefetch = [&](int s, int t) {
+            prefetch_tile(s, t);
+            prefetch_cols(s, t);
         };
         auto stage = [&](int s, int ybuf, int cbuf) {
-#pragma unroll
-            for (int tt = 0; tt < TPS; ++tt) stage_tile(s, tt, ybuf);
+            stage_tile(s, ybuf);
             stage_cols(s, cbuf);
         };
         // The ring of column chunks: slot g % D holds chunk g of the current pair of tiles.
@@ -421,125 +399,93 @@ struct Staged {
 #pragma unroll
             for (int p = 0; p < kPieces; ++p) yr[g % D][p] = lds_y[ytile * TILE16 + (cc * kPieces + p) * 64 + lane];
         };
-        // With FOLD, the B operand of the column MFMA (column_ones).
-        const bf16x8 colB = column_ones(h);
 
         f32x16 accA[RB], accB[RB];
-        Online<RB, L2, FOLD> on;
-        // Ring positions of the current step: LDS buffers yq = q % 3 and cq = q % 4.
+        Online<RB, false, false> on;
+        // Ring positions of the current tile: LDS buffers yq = q % 3 and cq = q % 4.
         int yq = 0, cq = 0;
         auto nxt3 = [](int v) { return v == 2 ? 0 : v + 1; };
         auto nxt4 = [](int v) { return (v + 1) & 3; };
-        // Tile t of phase PH (t - tb even: 0, odd: 1), tile TT = PH % TPS of its step: MFMAs into accN from zero,
-        // the column MFMA, and (epi) the update of the previous tile (accP, its column terms at colp) spread
-        // between them, one slot per MFMA, fenced so that the compiler keeps the interleave. The step's first
-        // tile stages step q + 2 and loads step q + 2 + NSETS.
+        // Tile t of phase PH (t - tb even: 0, odd: 1): MFMAs into accN from zero, and (epi) the update of the previous
+        // tile (accP, its column terms at colp) spread between them, one slot per MFMA, fenced so that the compiler
+        // keeps the interleave; tile t + 2 staged and tile t + 4 loaded into register set PH.
         auto tile = [&](auto PH, int t, f32x16 (&accN)[RB], f32x16 (&accP)[RB], const float* colp, bool epi) {
             constexpr int ph = decltype(PH)::value;
-            constexpr int tt = ph % TPS;
             auto col4 = [&](int q) { return *reinterpret_cast<const f32x4*>(colp + 8 * q); };
-            const int ycur = yq * TPS + tt;                                   // LDS tile of this tile
-            const int ynext = tt + 1 < TPS ? ycur + 1 : nxt3(yq) * TPS;      // and of the next
-            bf16x8 colA;
-            if constexpr (FOLD) colA = reinterpret_cast<const bf16x8*>(lds_col)[(cq * TPS + tt) * 32 + (lane & 31)];
+            const int ynext = nxt3(yq);
 #pragma unroll
             for (int b = 0; b < RB; ++b) accN[b] = f32x16{};
             static_for<0, NS>([&](auto I) {
                 constexpr int i = decltype(I)::value;
                 constexpr int cc = i / (kProducts * RB), p = (i / RB) % kProducts, b = i % RB;
-                constexpr int rp = ROLE == 0 ? C::first[p] : C::second[p];
-                constexpr int cp = ROLE == 0 ? C::second[p] : C::first[p];
                 constexpr int g = ph * NC + cc;           // this chunk's place in the pair of tiles
                 if constexpr (p == 0 && b == 0) {
                     // the chunk LA ahead: of this tile, or the first ones of the next
                     if constexpr (cc + LA < NC)
-                        read_chunk(std::integral_constant<int, (g + LA) % (2 * NC)>{}, ycur);
+                        read_chunk(std::integral_constant<int, (g + LA) % (2 * NC)>{}, yq);
                     else
                         read_chunk(std::integral_constant<int, (g + LA) % (2 * NC)>{}, ynext);
                 }
-                accN[b] = C::mfma(yr[g % D][cp], xv[b][cc][rp], accN[b]);
+                accN[b] = C::mfma(yr[g % D][C::second[p]], xv[b][cc][C::first[p]], accN[b]);
                 if (epi) {
-                    constexpr int k0 = op_begin<RB, FOLD>(i, NS), k1 = op_begin<RB, FOLD>(i + 1, NS);
+                    constexpr int k0 = op_begin<RB, false>(i, NS), k1 = op_begin<RB, false>(i + 1, NS);
                     static_for<k0, k1>([&](auto K) { on.template step<decltype(K)::value>(accP, col4, M, S, c); });
                 }
-                // The step's staging, spread over a few slots: each tile's units (and the column terms) are written
-                // out before the same registers are loaded again.
-                if constexpr (tt == 0) {
-                    constexpr int s = NSETS == 1 ? 0 : ph;
-                    if constexpr (i == kStageSlot - 2) stage_cols(s, nxt4(nxt4(cq)));
-                    static_for<0, TPS>([&](auto U) {
-                        constexpr int u = decltype(U)::value;
-                        if constexpr (i == kStageSlot + 2 * u) stage_tile(s, u, nxt3(nxt3(yq)));
-                        if constexpr (i == kStageSlot + 2 * u + 1) prefetch_tile(s, u, t + (2 + NSETS) * TPS);
-                    });
-                    if constexpr (i == kStageSlot + 2 * TPS) prefetch_cols(s, t + (2 + NSETS) * TPS);
-                }
+                // The staging, spread over a few slots: the tile's units (and the column terms) are written out
+                // before the same registers are loaded again.
+                if constexpr (i == kStageSlot - 2) stage_cols(ph, nxt4(nxt4(cq)));
+                if constexpr (i == kStageSlot) stage_tile(ph, nxt3(nxt3(yq)));
+                if constexpr (i == kStageSlot + 1) prefetch_tile(ph, t + 4);
+                if constexpr (i == kStageSlot + 2) prefetch_cols(ph, t + 4);
                 __builtin_amdgcn_sched_barrier(0);
             });
-            // The column terms last, after the whole dot product: x.y is formed identically in both directions.
-            if constexpr (FOLD) {
-#pragma unroll
-                for (int b = 0; b < RB; ++b)
-                    accN[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(colA, colB, accN[b], 0, 0, 0);
-            }
         };
         auto update = [&](f32x16 (&accP)[RB], const float* colp) {
             auto col4 = [&](int q) { return *reinterpret_cast<const f32x4*>(colp + 8 * q); };
             static_for<0, RB * kOps>([&](auto K) { on.template step<decltype(K)::value>(accP, col4, M, S, c); });
         };
-        // Column terms (without FOLD) of tile tt of the step in column buffer cbuf.
-        auto colp_of = [&](int cbuf, int tt) { return lds_col + (cbuf * TPS + tt) * 32 + 4 * h; };
-        // After a tile: to the next step (every TPS tiles) and a barrier there.
-        auto advance = [&](auto PH) {
-            constexpr int ph = decltype(PH)::value;
-            if constexpr (ph % TPS == TPS - 1) {
-                yq = nxt3(yq);
-                cq = nxt4(cq);
-                __syncthreads();
-            }
+        // Column terms of the tile in column buffer cbuf, as this lane's accumulators take them.
+        auto colp_of = [&](int cbuf) { return lds_col + cbuf * 32 + 4 * h; };
+        // After a tile: to the next buffers and a barrier there.
+        auto advance = [&]() {
+            yq = nxt3(yq);
+            cq = nxt4(cq);
+            __syncthreads();
         };
 
-        // Prologue: steps 0 and 1 staged, steps 2 .. 1 + NSETS in the register sets, the first chunks of tile tb
+        // Prologue: tiles tb and tb + 1 staged, tb + 2 and tb + 3 in the register sets, the first chunks of tile tb
         // read. Every prefetch / stage is unconditional (tiles past the last one are the last one again).
-        if constexpr (NSETS == 2) {
-            prefetch(0, tb);
-            prefetch(1, tb + TPS);
-            stage(0, 0, 0);
-            stage(1, 1, 1);
-            prefetch(0, tb + 2 * TPS);
-            prefetch(1, tb + 3 * TPS);
-        } else {
-            prefetch(0, tb);
-            stage(0, 0, 0);
-            prefetch(0, tb + TPS);
-            stage(0, 1, 1);
-            prefetch(0, tb + 2 * TPS);
-        }
+        prefetch(0, tb);
+        prefetch(1, tb + 1);
+        stage(0, 0, 0);
+        stage(1, 1, 1);
+        prefetch(0, tb + 2);
+        prefetch(1, tb + 3);
         __syncthreads();
         static_for<0, LA>([&](auto G) { read_chunk(G, 0); });
         int t = tb;
         tile(std::integral_constant<int, 0>{}, t, accA, accB, nullptr, false);
-        advance(std::integral_constant<int, 0>{});
+        advance();
         ++t;
         // Tiles in pairs (phase 1 then phase 0), so that the accumulators keep their registers; the column terms
-        // of the tile before (without FOLD) are in column buffer cq - 1 after a step boundary, else cq.
+        // of the tile before are in column buffer cq - 1.
         while (te - t >= 2) {
-            tile(std::integral_constant<int, 1>{}, t, accB, accA, colp_of(TPS == 1 ? (cq + 3) & 3 : cq, 0), true);
-            advance(std::integral_constant<int, 1>{});
-            tile(std::integral_constant<int, 0>{}, t + 1, accA, accB, colp_of((cq + 3) & 3, TPS - 1), true);
-            advance(std::integral_constant<int, 0>{});
+            tile(std::integral_constant<int, 1>{}, t, accB, accA, colp_of((cq + 3) & 3), true);
+            advance();
+            tile(std::integral_constant<int, 0>{}, t + 1, accA, accB, colp_of((cq + 3) & 3), true);
+            advance();
             t += 2;
         }
         if (t < te) {
-            tile(std::integral_constant<int, 1>{}, t, accB, accA, colp_of(TPS == 1 ? (cq + 3) & 3 : cq, 0), true);
-            advance(std::integral_constant<int, 1>{});
-            update(accB, colp_of((cq + 3) & 3, TPS - 1));
+            tile(std::integral_constant<int, 1>{}, t, accB, accA, colp_of((cq + 3) & 3), true);
+            advance();
+            update(accB, colp_of((cq + 3) & 3));
         } else {
-            update(accA, colp_of(TPS == 1 ? (cq + 3) & 3 : cq, 0));
+            update(accA, colp_of((cq + 3) & 3));
         }
         // The next segment's prologue rewrites the first buffers: every wave is done with them first.
         __syncthreads();
-        store_rows<RB, L2>(a, M, S, rb0, slot, c, inv_sigma, lane);
+        store_rows<RB, false>(a, M, S, rb0, slot, c, inv_sigma, lane);
     }
 };
 
@@ -551,6 +497,11 @@ constexpr int col_sink(bool fold) { return fold ? col_tiles(fold) * 32 : (col_ti
 constexpr int col_floats(bool fold) { return fold ? (col_sink(fold) + 1) * 4 : col_sink(fold) + 1; }
 constexpr int kColBatch = 8;
 constexpr int kStreamMaxChunks = 4;
+// The streamed kernel serves every fp16 half-step (up to kp 128, where one wave per SIMD holds its row operands and
+// two column tiles in VGPRs and AGPRs) and the bf16 row log-sum-exp up to kp 64; the staged one that row
+// log-sum-exp above kp 64 (three pieces per coordinate). At kp 128 streaming measured 3.4 % faster than staging the
+// fp16 tiles through LDS (4.963-4.968 against 5.140-5.145 ms per iteration, 65,536 x 65,536 stress clouds).
+constexpr bool streamed_form(int nc, int ct) { return ct == kF16x2 || nc <= kStreamMaxChunks; }
 
 template <int NC, int ROLE, int CT, bool L2>
 struct Streamed {
@@ -830,7 +781,7 @@ __device__ __forceinline__ void segments(const PartialArgs& a, int p, int wv, co
         // Waves past the last row block recompute it (their rows are not stored) so that every wave takes part
         // in the workgroup's barriers.
         const int rb0 = (g * kWavesK + wv) * kRowBlocksK;
-        if constexpr (NC <= kStreamMaxChunks)
+        if constexpr (streamed_form(NC, CT))
             Streamed<NC, ROLE, CT, L2>::run(a, rb0, tb, te, slot, cu, cv, alpha, beta, beta_lo, cs, c, inv_sigma,
                                             lds_col);
         else
@@ -864,9 +815,9 @@ void lse_partial_kernel(PartialArgs a) {
                  "s"(a.s.ftot), "s"(a.s.q), "s"(a.s.r), "s"(a.group_counters));
     asm volatile("" ::"s"(sc0), "s"(sc2), "s"(sx), "s"(sy), "s"(cb), "s"(cb_s2), "s"(cb_t), "v"(skip));
     if (skip != 0) return;
-    constexpr bool kStream = NC <= kStreamMaxChunks;
-    constexpr int kLdsY = kStream ? 1 : 3 * staged_step_tiles(CT) * NC * Contract<CT>::pieces * 64;
-    constexpr int kLdsCol = kStream ? col_floats(CT == kF16x2) : 4 * staged_step_tiles(CT) * 32 * (CT == kF16x2 ? 4 : 1);
+    constexpr bool kStream = streamed_form(NC, CT);
+    constexpr int kLdsY = kStream ? 1 : 3 * NC * Contract<CT>::pieces * 64;     // staged: three tile buffers
+    constexpr int kLdsCol = kStream ? col_floats(CT == kF16x2) : 4 * 32;        // staged: four column buffers
     __shared__ typename Contract<CT>::T lds_y[kLdsY];
     __shared__ __attribute__((aligned(16))) float lds_col[kLdsCol];
     const int wv = __builtin_amdgcn_readfirstlane(tid_x() >> 6);   // one value per wave

@@ -17,7 +17,7 @@ TILE, WAVES, XCDS, RB, BLOCK = 32, 4, 8, 2, 256   # streamed variant: 4 waves of
 WAVES_K, RB_K, BLOCK_K = 4, 2, 256                 # staged variant: the same 4 waves of 2 row blocks
 STREAM_MAX_CHUNKS, COL_TILES = 4, 256        # streamed variant: nc <= 4; column terms staged per 256 tiles
 FOLD_COL_TILES = 192                         # ... per 192 tiles with the f16x2 contraction (folded, 16 B each)
-SEG_COST_STREAMED, SEG_COST_STAGED = 6, 2    # cost of a row-group boundary in tiles (sk_kernels.hip make_plan)
+SEG_COST_NARROW, SEG_COST_WIDE = 6, 4       # cost of a row-group boundary in tiles, kp <= 64 / above (make_plan)
 ROWS_PER_GROUP = TILE * RB * WAVES
 EMPTY = -1.0e30
 FIRST = [0, 0, 1]              # fp16x2 (half-steps): (first-cloud piece, second-cloud piece) of the products
@@ -196,7 +196,7 @@ def plan(rows_pad, m_pad, ncu=256, per_cu=1, nc=4, alpha=None):
     work = ngroups * nt
     P = max(1, min(ncu * per_cu, 1024, work))
     if alpha is None:
-        alpha = SEG_COST_STREAMED if nc <= STREAM_MAX_CHUNKS else SEG_COST_STAGED
+        alpha = SEG_COST_NARROW if nc <= STREAM_MAX_CHUNKS else SEG_COST_WIDE
     s = Split(nt, ngroups, P, alpha)
     slots = max(s.last(g) - s.first(g) + 1 for g in range(ngroups))
     return nrb, nt, ngroups, s, slots

@@ -341,9 +341,11 @@ struct Plan {
 // The cost of a row-group boundary in tiles (Split::alpha): what a second segment adds to a workgroup, its
 // row operands, column-term staging and stores (about 3 us against 0.7-0.84 us per 32-column tile at kp 64,
 // 10k x 10k), and in the on-device loop the arrival count (and maybe merge) of the first row group. Swept on
-// the 10k x 10k d 64 loop: 6 tiles, 1.4 % faster than 4, 5 and 7 within 0.3 %. TRNOPT_HIP_SEG_COST overrides it.
-constexpr int kSegCostStreamed = 6;
-constexpr int kSegCostStaged = 2;
+// the 10k x 10k d 64 loop: 6 tiles, 1.4 % faster than 4, 5 and 7 within 0.3 %. Above kp 64, where a tile takes
+// up to twice as long: 4, swept on the 20k x 20k d 128 loop (0.5084-0.5089 ms per iteration against 0.5097-0.5103
+// with 2 and 0.5089-0.5096 with 6). TRNOPT_HIP_SEG_COST overrides it.
+constexpr int kSegCostNarrow = 6;     // kp <= 64
+constexpr int kSegCostWide = 4;       // kp 80 to 128
 
 Plan make_plan(int rows_pad, int m_pad, int kp) {
     Plan pl;
@@ -358,7 +360,7 @@ Plan make_plan(int rows_pad, int m_pad, int kp) {
     if (P > 1024) P = 1024;
     if (P > work) P = work;
     if (P < 1) P = 1;
-    int alpha = env_int("TRNOPT_HIP_SEG_COST", pl.nc <= 4 ? kSegCostStreamed : kSegCostStaged);
+    int alpha = env_int("TRNOPT_HIP_SEG_COST", pl.nc <= 4 ? kSegCostNarrow : kSegCostWide);
     if (alpha < 0 || alpha > 64) alpha = 0;
     const long long ftot = work + (long long)alpha * (pl.ngroups - 1);
     pl.s.nt = pl.nt;

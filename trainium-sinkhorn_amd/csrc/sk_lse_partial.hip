@@ -43,8 +43,9 @@
 // rows of the group (its fp16 pieces stay in registers for the whole work segment); all waves walk the same
 // column tiles. Two ways to feed the column tiles (streamed_form):
 //   - streamed (every fp16 half-step, and the bf16 row log-sum-exp up to kp 64): every wave loads the tile's
-//     pieces straight into registers one tile ahead; the four waves of the CU read the same addresses at about
-//     the same time and share them through L1. The column terms of the whole segment are computed once into LDS
+//     pieces straight into registers one tile ahead (above kp 64 chunk by chunk, into the registers of the chunk
+//     just used); the four waves of the CU read the same addresses at about the same time and share them
+//     through L1. The column terms of the whole segment are computed once into LDS
 //     (as MFMA operands with the fp16 contraction). No per-tile barrier.
 //   - staged (the bf16 row log-sum-exp above kp 64, whose three pieces per coordinate no longer fit in registers
 //     twice): the workgroup stages the tiles and their column terms once in LDS through a ring of three tile
@@ -74,9 +75,9 @@ namespace {
 // Waves per workgroup and 32-row blocks per wave, both variants: 4 waves, one per SIMD, 2 row blocks each (two
 // accumulator chains per wave, the epilogue interleaved with the MFMAs at compile time). With one wave per SIMD a
 // wave may use all 512 registers of its lanes, VGPRs and AGPRs: at kp 128 the streamed variant holds its row
-// operands (128 registers), two column tiles (128), two accumulator sets per row block and the epilogue in about
-// 390, the MFMA results in VGPRs and part of the operands in AGPRs, which the MFMAs read directly (about 30
-// register copies per tile, no scratch).
+// operands (128 registers), one tile's column operands as a ring of chunks (64), two accumulator sets per row
+// block and the epilogue in about 350, the MFMA results in VGPRs and part of the operands in AGPRs, which the
+// MFMAs read directly (32 register copies per tile, no scratch).
 constexpr int kWavesK = 4, kRowBlocksK = 2, kWavesPerSimd = 1;
 constexpr int kBlockK = 64 * kWavesK;
 static_assert(32 * kRowBlocksK * kWavesK == kRowsPerGroup, "a row group is 256 rows in both variants");
@@ -514,6 +515,11 @@ struct Streamed {
     static constexpr int NS = kProducts * NC * RB;
     static constexpr bool FOLD = CT == kF16x2;      // column terms added by the matrix pipe
     static constexpr int kColTiles = col_tiles(FOLD);
+    // Above kp 64 the next tile's operands come as a ring of chunks instead of a second whole tile: chunk cc of
+    // tile t + 1 is loaded into the registers of chunk cc of tile t as soon as the last MFMA of that chunk has
+    // issued, one tile ahead as before, in half the registers (350 instead of 388 at kp 128: 0.9 % faster on the
+    // 65,536 x 65,536 d 128 stress clouds; at kp 64, where both forms fit, 1 % slower).
+    static constexpr bool RING = NC > kStreamMaxChunks;
 
     __device__ __forceinline__ static void run(const PartialArgs& a, int rb0, int tb, int te, int slot, const float* cu,
                                                const float* cv, float alpha, float beta, float beta_lo, float cs,
@@ -601,11 +607,17 @@ struct Streamed {
         // otherwise form a 64-bit vector address for them: four more VALU instructions per tile).
         size_t ystep = 4 * 64;                          // opaque once, so that the pointer stays a global one
         if constexpr (NC * kPieces > 4) asm volatile("" : "+s"(ystep));
-        auto load_y = [&](int t, T (&yv)[NC][kPieces]) {
+        auto load_y_chunk = [&](int t, T (&yv)[NC][kPieces], int cc) {
             const T* b0 = yt + (size_t)t * TILE16;
 #pragma unroll
-            for (int k = 0; k < NC * kPieces; ++k)
-                yv[k / kPieces][k % kPieces] = (b0 + (k / 4) * ystep)[(k % 4) * 64 + lane];
+            for (int p = 0; p < kPieces; ++p) {
+                const int k = cc * kPieces + p;
+                yv[cc][p] = (b0 + (k / 4) * ystep)[(k % 4) * 64 + lane];
+            }
+        };
+        auto load_y = [&](int t, T (&yv)[NC][kPieces]) {
+#pragma unroll
+            for (int cc = 0; cc < NC; ++cc) load_y_chunk(t, yv, cc);
         };
         auto colp_of = [&](int t) { return lds_col + (t - cbase) * 32 + 4 * h; };
         // With FOLD, the A operand of tile t's column MFMA (lane l: column l % 32; lanes 32-63 meet zeros in B)
@@ -615,11 +627,12 @@ struct Streamed {
 
         f32x16 accA[RB], accB[RB];
         Online<RB, L2, FOLD> on;
-        auto tile = [&](f32x16 (&accN)[RB], f32x16 (&accP)[RB], const float* colp, const T (&yv)[NC][kPieces],
-                        int t, bool epi) {
+        auto tile = [&](f32x16 (&accN)[RB], f32x16 (&accP)[RB], const float* colp, T (&yv)[NC][kPieces], int t,
+                        bool epi) {
             auto col4 = [&](int q) { return *reinterpret_cast<const f32x4*>(colp + 8 * q); };
             bf16x8 colA;
             if constexpr (FOLD) colA = colA_of(t);
+            const int tn = t + 1 < te ? t + 1 : te - 1;     // RING: the tile whose chunks replace this one's
 #pragma unroll
             for (int b = 0; b < RB; ++b) accN[b] = f32x16{};
             static_for<0, NS>([&](auto I) {
@@ -632,6 +645,7 @@ struct Streamed {
                     constexpr int k0 = op_begin<RB, FOLD>(i, NS), k1 = op_begin<RB, FOLD>(i + 1, NS);
                     static_for<k0, k1>([&](auto K) { on.template step<decltype(K)::value>(accP, col4, M, S, c); });
                 }
+                if constexpr (RING && p == kProducts - 1 && b == RB - 1) load_y_chunk(tn, yv, cc);
                 __builtin_amdgcn_sched_barrier(0);
             });
             // The column terms last, after the whole dot product: x.y is formed identically in both directions.
@@ -655,10 +669,33 @@ struct Streamed {
         int t = tb;
         stage_cols(tb, cend, [&] {
             load_y(t, yA);
-            load_y(t + 1 < te ? t + 1 : last, yB);
+            if constexpr (!RING) load_y(t + 1 < te ? t + 1 : last, yB);
         });
         tile(accA, accB, nullptr, yA, t, false);
         ++t;
+        if constexpr (RING) {
+            // the same loop with the one ring of operands, its next tile loaded inside tile()
+            while (t < te) {
+                if (__builtin_expect(t >= cend, 0)) {
+                    cend = t + kColTiles < te ? t + kColTiles : te;
+                    stage_cols(t, cend, [] {});
+                }
+                tile(accB, accA, colp_of(t - 1), yA, t, true);
+                ++t;
+                if (__builtin_expect(t >= te, 0)) {
+                    update(accB, colp_of(t - 1));
+                    goto done;
+                }
+                if (__builtin_expect(t >= cend, 0)) {
+                    cend = t + kColTiles < te ? t + kColTiles : te;
+                    stage_cols(t, cend, [] {});
+                }
+                tile(accA, accB, colp_of(t - 1), yA, t, true);
+                ++t;
+            }
+            update(accA, colp_of(t - 1));
+            goto done;
+        }
         // The restaging of the column terms (once per kColTiles tiles) and the segment's end are the unlikely
         // branches: laid out of line, so that consecutive tiles fall through with no taken branch between them
         // (with one wave per SIMD a taken branch costs the wave about 25 cycles in which nothing issues).

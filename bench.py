@@ -396,7 +396,7 @@ def workload_stress(cpu):
             "data": "synthetic", "iterations": r.iterations,
             "ms_per_iteration": round(r.seconds * 1e3 / max(r.iterations, 1), 3),
             "config": {"workload": "balanced 65536 x 65536, d 128, eps 1.0 -> 0.01 (0.7 per stage), 280 its"}}
-    # the fp16 pipe the staged kernel runs on, over whole iterations (both half-steps, merges and control included)
+    # the fp16 pipe the kernel runs on, over whole iterations (both half-steps, merges and control included)
     t_it = r.seconds / max(r.iterations, 1)
     alg_it = 2 * 2.0 * len(x) * len(y) * (128 + 1)
     flop_it = 2 * PRODUCTS * 2.0 * len(x) * len(y) * 128

@@ -181,7 +181,8 @@ def test_merge_in_partial_kernel_is_bit_identical(monkeypatch, case):
     merge kernel, and the default choice per pass give bit-identical potentials and iteration counts: fixed iterations; an eps schedule
     (the log2-unit copy remade by the control); an unbalanced solve stopped by its checks; 100,000 x 64
     points (391 row groups of one or two tiles: workgroups with several segments), 64 x 100,000 (one
-    row group of the f update split over 256 workgroups, 256 slots), and d 100 (the staged kernel)."""
+    row group of the f update split over 256 workgroups, 256 slots), and d 100 (kp 112: the ring of column
+    chunks)."""
     if case == "2048-d64":
         x, y = data.balanced_gaussian()
         o = dict(eps=0.1, normalize=False, max_iters=100, fixed_iters=True)

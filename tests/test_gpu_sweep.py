@@ -2,7 +2,7 @@
 float32 inputs (examples/nki_sinkhorn_check.py:60-73, brute.half_step_f64).
 
 Each case draws the row and column counts (1 to 3,000, log-uniform: ragged, single points, many padding
-rows and columns), the dimension (1 to 128: every K chunk count, so the streamed and the staged kernels), the
+rows and columns), the dimension (1 to 128: every K chunk count, the ring of column chunks above kp 64 included), the
 two clouds' scales independently (1e-3 to 1e3: mixed scales put the column terms far above the dot products
 in the kernel's units), eps relative to the typical cost (1e-3 to 1e2: from a single dominant score per row
 to nearly flat rows), kappa (1 or in (0.5, 1)), offsets or none, random weights and column potentials. Both
@@ -72,7 +72,7 @@ def test_half_step_random_sweep(hip, k):
 
 # A few points against a large cloud and the reverse, up to a million points: one row group whose columns are
 # split over every workgroup (256 partial slots per row for the merge), and hundreds to thousands of row groups
-# against a single column tile; the staged kernel (d 100) and d 1-2 as well.
+# against a single column tile; d 100 (the ring of column chunks) and d 1-2 as well.
 EXTREME = [(5, 150_000, 16), (150_000, 5, 16), (3, 60_000, 100), (60_000, 3, 100), (2, 200_000, 2),
            (40_000, 1, 64), (1_000_000, 7, 16), (9, 1_000_000, 4)]
 

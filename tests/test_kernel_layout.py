@@ -15,7 +15,7 @@ from scipy.special import logsumexp
 
 TILE, WAVES, XCDS, RB, BLOCK = 32, 4, 8, 2, 256   # streamed variant: 4 waves of 2 row blocks
 WAVES_K, RB_K, BLOCK_K = 4, 2, 256                 # staged variant: the same 4 waves of 2 row blocks
-STREAM_MAX_CHUNKS, COL_TILES = 4, 256        # streamed variant: nc <= 4; column terms staged per 256 tiles
+STREAM_MAX_CHUNKS, COL_TILES = 4, 256        # bf16 row-LSE streams up to nc 4 (fp16: every nc); terms per 256 tiles
 FOLD_COL_TILES = 192                         # ... per 192 tiles with the f16x2 contraction (folded, 16 B each)
 SEG_COST_NARROW, SEG_COST_WIDE = 6, 4       # cost of a row-group boundary in tiles, kp <= 64 / above (make_plan)
 ROWS_PER_GROUP = TILE * RB * WAVES

@@ -7,7 +7,7 @@ directory); nothing is compiled at import time. Two translation units:
 
 * sk_lse_partial.hip -- the MFMA partial (max, sum) kernel, built with -fno-honor-nans -mno-amdgpu-ieee
   (no NaN ever reaches it; this drops the IEEE canonicalisation of every MFMA result before a max), twice:
-  the streamed instantiations (kp <= 64) and the staged ones (kp > 64), both with MFMA results in VGPRs
+  the instantiations of kp <= 64 and those of kp 80 to 128, both with MFMA results in VGPRs
   (-amdgpu-mfma-vgpr-form: the epilogue reads them without copies);
 * sk_kernels.hip -- packing, finalisation, the on-device loop and the C ABI, built with default NaN
   semantics (the loop state stores NaN for "not checked yet").

@@ -216,6 +216,30 @@ int sk_loop_init_f32(const sk_loop_f32* L, void* stream);
 int sk_loop_run_f32(const sk_loop_f32* L, int iters, void* stream);
 
 /*
+ * Several loops at once: `count` independent solves of the same d (each set up and initialised as above, on its
+ * own workspace), such as the consecutive pairs of a wot pipeline (examples/singlecell_wot.py:84-89, which runs
+ * them one after another through sinkhorn(); this is the batched form of sk_loop_run_f32 for them). Each
+ * iteration is two launches, the f updates of all the loops and then their g updates, each loop's pass split over
+ * its own share of the GPU's workgroups (in proportion to its work) and merged inside the launch, with each loop's
+ * control as in sk_loop_run_f32: small solves fill the GPU together. A loop's splits differ from its own launches'
+ * (fewer workgroups), so its potentials agree with sk_loop_run_f32's to float32 rounding, not bit for bit; with
+ * count 1 the splits, and the results, are the same. A loop whose `done` is set does nothing; the others go on.
+ *
+ * sk_loop_batch_plan: the workgroups each loop's f and g pass gets (workgroups[2k], workgroups[2k + 1]) for loops
+ * of nx_pad[k] x ny_pad[k] points (host arithmetic only).
+ * sk_loop_batch_init_f32: writes the launches' argument blocks for loops[0 .. count) into ws
+ * (sk_loop_batch_workspace_bytes(count) bytes, 256-byte aligned) and returns in launch[3] what
+ * sk_loop_run_batch_f32 needs; synchronises the stream. Call it again whenever the loops change.
+ * sk_loop_run_batch_f32: enqueues `iters` iterations of the loops last initialised into ws.
+ * No counterpart in the reference (its pipeline solves one pair at a time).
+ */
+size_t sk_loop_batch_workspace_bytes(int count);
+int sk_loop_batch_plan(const int* nx_pad, const int* ny_pad, int count, int d, int* workgroups);
+int sk_loop_batch_init_f32(const sk_loop_f32* const* loops, int count, void* ws, size_t ws_bytes, int* launch,
+                           void* stream);
+int sk_loop_run_batch_f32(const void* ws, size_t ws_bytes, int count, const int* launch, int iters, void* stream);
+
+/*
  * Median of the squared-Euclidean cost over all pairs, the normalisation cost / median(cost) of
  * normalization(how="median") (src/trnopt/sinkhorn.py:229-233), which the reference evaluates on the host
  * over the materialised n x m float64 matrix:

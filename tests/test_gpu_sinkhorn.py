@@ -493,9 +493,9 @@ def test_wot_transport_maps_in_flight_equal_one_at_a_time(monkeypatch, graphs):
     gpu = SinkhornOptions(kernel="hip", backend=ROCM, check_every=5, max_iters=50_000)
     kw = dict(growth_iters=2, tol=1e-6, stage_tol=1e-6, opts=gpu)
     print("pairs in flight, graphs", graphs, flush=True)
-    many = wot_transport_maps(pairs, streams=4, **kw)
+    many = wot_transport_maps(pairs, streams=4, batch=False, **kw)
     print("pairs one at a time", flush=True)
-    one = wot_transport_maps(pairs, streams=1, **kw)
+    one = wot_transport_maps(pairs, streams=1, batch=False, **kw)
     for k, (a, b) in enumerate(zip(many, one)):
         assert a.result.converged and a.iterations == b.iterations, k
         np.testing.assert_array_equal(a.result.f, b.result.f)
@@ -508,7 +508,7 @@ def test_wot_transport_maps_in_flight_equal_one_at_a_time(monkeypatch, graphs):
 def test_wot_pipeline_38_pairs_at_full_size():
     """The pipeline workload at its full size: 39 time points (log-uniform cell counts in [1,500, 9,000], 175,000
     cells, d 30), 38 consecutive wot maps, each with its GPU median normalisation, wot's eps stages, tol 1e-6
-    and 3 growth iterations (src/trnopt/singlecell.py:61-86, README.md:19-24), several pairs in flight as the
+    and 3 growth iterations (src/trnopt/singlecell.py:61-86, README.md:19-24), all the pairs batched as the
     benchmark runs them. Every pair converges and its
     masses are the float64 plan's row and column sums of its potentials; the largest pair meets the float64
     fixed-point pins (last g update at sampled columns, next f update within tolerance), and the smallest pair
@@ -517,14 +517,14 @@ def test_wot_pipeline_38_pairs_at_full_size():
     import sys
     from pathlib import Path
     sys.path.insert(0, str(Path(__file__).resolve().parent.parent))
-    from bench import PIPELINE_STREAMS, pipeline_sizes, single_cell_inputs
+    from bench import pipeline_sizes, single_cell_inputs
     from trnopt.singlecell import wot_transport_maps
     sizes = pipeline_sizes()
     assert len(sizes) == 39 and abs(int(sizes.sum()) - 175_000) < 50
     gpu = SinkhornOptions(kernel="hip", backend=ROCM, check_every=5, max_iters=50_000)
     clouds = [single_cell_inputs(n=int(sizes[t]), m=int(sizes[t + 1]), t0=t, t1=t + 1)[:2] for t in range(38)]
-    # as the benchmark runs them: several pairs in flight
-    maps = wot_transport_maps(clouds, streams=PIPELINE_STREAMS, growth_iters=3, tol=1e-6, stage_tol=1e-6, opts=gpu)
+    # as the benchmark runs them: each growth iteration of all the pairs in one batched loop
+    maps = wot_transport_maps(clouds, batch=True, growth_iters=3, tol=1e-6, stage_tol=1e-6, opts=gpu)
     iters = 0
     for k, tm in enumerate(maps):
         assert tm.result.converged and len(tm.learned_growth) == 3, k

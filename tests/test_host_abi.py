@@ -128,6 +128,77 @@ def test_noalloc_half_step_validates_like_the_workspace_entry_point(hk):
     assert b"static scratch" in lb.sk_last_error()
 
 
+def _pass_cost(rows_pad, m_pad, kp):
+    """A pass's length on its split's cost line: row groups (256 rows) x column tiles (32), plus the cost of each
+    row-group boundary (6 tiles up to kp 64, 4 above: make_plan)."""
+    ngroups, nt = -(-rows_pad // 256), m_pad // 32
+    return ngroups * nt + (6 if kp <= 64 else 4) * (ngroups - 1)
+
+
+def _smallest_even_share(costs, total):
+    """The smallest per-workgroup cost T at which one workgroup per ceil(cost / T) tiles (one at least) fits
+    `total` workgroups, by bisection over T."""
+    need = lambda T: sum(max(1, -(-c // T)) for c in costs)       # noqa: E731
+    lo, hi = 1, max(costs)
+    while lo < hi:
+        mid = (lo + hi) // 2
+        lo, hi = (lo, mid) if need(mid) <= total else (mid + 1, hi)
+    return lo
+
+
+@pytest.mark.parametrize("count,d", [(1, 64), (1, 30), (2, 30), (5, 128), (38, 30), (300, 16)])
+def test_batch_plan_shares_the_workgroups_by_work(hk, count, d):
+    """sk_loop_batch_plan (host arithmetic, no device call): each loop's f and g pass get workgroups so that no
+    workgroup carries more tiles than the smallest even share T of the 256 CUs, at least one each, every CU used
+    while a pass has more tiles than workgroups; one loop gets the split of its own launches, min(256, tiles)."""
+    lb = hk.lib()
+    rng = np.random.default_rng(count + d)
+    sizes = np.exp(rng.uniform(np.log(2), np.log(9000), size=(count, 2))).astype(int)
+    nx = [hk.pad_points(int(a)) for a, _ in sizes]
+    ny = [hk.pad_points(int(b)) for _, b in sizes]
+    kp = hk.pad_dim(d)
+    wg = (ctypes.c_int * (2 * count))()
+    assert lb.sk_loop_batch_plan((ctypes.c_int * count)(*nx), (ctypes.c_int * count)(*ny), count, d, wg) == 0
+    for side, costs in ((0, [_pass_cost(nx[k], ny[k], kp) for k in range(count)]),
+                        (1, [_pass_cost(ny[k], nx[k], kp) for k in range(count)])):
+        P = [wg[2 * k + side] for k in range(count)]
+        assert min(P) >= 1 and all(P[k] <= max(1, costs[k]) for k in range(count))
+        if count <= 256:
+            assert sum(P) == min(256, sum(costs))
+        else:
+            assert P == [1] * count
+        T = _smallest_even_share(costs, 256)
+        assert max(-(-c // p) for c, p in zip(costs, P)) <= T
+        if count == 1:
+            assert P == [min(256, costs[0])]
+
+
+def test_batch_entry_points_validate_before_any_device_call(hk):
+    lb = hk.lib()
+    assert lb.sk_loop_batch_workspace_bytes(0) == 0 and lb.sk_loop_batch_workspace_bytes(1025) == 0
+    one = lb.sk_loop_batch_workspace_bytes(1)
+    assert 0 < one < lb.sk_loop_batch_workspace_bytes(38)
+    ints = (ctypes.c_int * 2)(64, 64)
+    out = (ctypes.c_int * 4)()
+    assert lb.sk_loop_batch_plan(None, ints, 1, 30, out) == -1
+    assert lb.sk_loop_batch_plan(ints, ints, 0, 30, out) == -2
+    assert lb.sk_loop_batch_plan(ints, ints, 1, 200, out) == -2                 # d beyond SK_KP_MAX
+    assert lb.sk_loop_batch_plan((ctypes.c_int * 1)(40), ints, 1, 30, out) == -2   # not a multiple of 32
+    loops = (ctypes.POINTER(hk.SkLoop) * 1)(ctypes.pointer(hk.SkLoop()))
+    launch = (ctypes.c_int * 3)()
+    assert lb.sk_loop_batch_init_f32(None, 1, 4096, one, launch, None) == -1
+    assert lb.sk_loop_batch_init_f32(loops, 0, 4096, one, launch, None) == -2
+    assert lb.sk_loop_batch_init_f32(loops, 1, 4096, one - 1, launch, None) == -3
+    assert lb.sk_loop_batch_init_f32(loops, 1, 4096 + 16, one, launch, None) == -1   # misaligned
+    assert lb.sk_loop_batch_init_f32(loops, 1, 4096, one, launch, None) == -1        # the loop's null pointers
+    assert lb.sk_loop_run_batch_f32(4096, one, 1, (ctypes.c_int * 3)(2, 0, 5), 1, None) == -1
+    assert lb.sk_loop_run_batch_f32(4096, one, 1, (ctypes.c_int * 3)(9, 5, 5), 1, None) == -1   # kp 144
+    assert lb.sk_loop_run_batch_f32(4096, one, 1, (ctypes.c_int * 3)(2, 5, 2000), 1, None) == -1
+    assert lb.sk_loop_run_batch_f32(4096, one - 1, 1, (ctypes.c_int * 3)(2, 5, 5), 1, None) == -3
+    assert lb.sk_loop_run_batch_f32(4096, one, 1, (ctypes.c_int * 3)(2, 5, 5), -1, None) == -1
+    assert b"iters" in lb.sk_last_error()
+
+
 # ---------------------------------------------------------------------------------------------------------
 # Selection and validation of the Python API (src/trnopt/sinkhorn.py:196-208, 254-276; backend.py:30-48)
 

@@ -175,5 +175,16 @@ hipError_t launch_partial_large(const PartialArgs& a, int nc, hipStream_t stream
 inline hipError_t launch_partial(const PartialArgs& a, int nc, hipStream_t stream) {
     return nc <= 4 ? launch_partial_small(a, nc, stream) : launch_partial_large(a, nc, stream);
 }
+// The grouped partial kernel of the fp16 half-steps (rows_role `role` in every pass): nmap workgroups, workgroup b
+// running workgroup map[b] & 0xffff of pass map[b] >> 16 of args[0 .. count) (device memory, kp = 16 nc each).
+hipError_t launch_grouped_small(const PartialArgs* args, const unsigned* map, int count, int nmap, int nc, int role,
+                                hipStream_t stream);
+hipError_t launch_grouped_large(const PartialArgs* args, const unsigned* map, int count, int nmap, int nc, int role,
+                                hipStream_t stream);
+inline hipError_t launch_grouped(const PartialArgs* args, const unsigned* map, int count, int nmap, int nc, int role,
+                                 hipStream_t stream) {
+    return nc <= 4 ? launch_grouped_small(args, map, count, nmap, nc, role, stream)
+                   : launch_grouped_large(args, map, count, nmap, nc, role, stream);
+}
 
 }  // namespace sk

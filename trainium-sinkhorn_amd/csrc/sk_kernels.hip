@@ -347,7 +347,9 @@ struct Plan {
 constexpr int kSegCostNarrow = 6;     // kp <= 64
 constexpr int kSegCostWide = 4;       // kp 80 to 128
 
-Plan make_plan(int rows_pad, int m_pad, int kp) {
+// P_req > 0: that many workgroups (the grouped launches of sk_loop_run_batch_f32), else one per CU (times
+// TRNOPT_HIP_WG_PER_CU); at most 1024 and at most one per unit either way.
+Plan make_plan(int rows_pad, int m_pad, int kp, int P_req = 0) {
     Plan pl;
     pl.nc = kp / 16;
     pl.nrb = rows_pad / SK_TILE;
@@ -356,7 +358,7 @@ Plan make_plan(int rows_pad, int m_pad, int kp) {
     const long long work = (long long)pl.ngroups * pl.nt;
     int per_cu = env_int("TRNOPT_HIP_WG_PER_CU", 1);
     if (per_cu < 1 || per_cu > 4) per_cu = 1;
-    long long P = (long long)cu_count() * per_cu;
+    long long P = P_req > 0 ? P_req : (long long)cu_count() * per_cu;
     if (P > 1024) P = 1024;
     if (P > work) P = work;
     if (P < 1) P = 1;
@@ -421,7 +423,7 @@ struct Pass {
     char* rebake;   // with state: the packed first cloud, whose log2-unit copy the control remakes on a new eps
 };
 
-hipError_t run_pass(const Pass& ps, const Plan& pl, hipStream_t st) {
+PartialArgs pass_args(const Pass& ps, const Plan& pl) {
     PartialArgs a;
     a.xr = ps.xr;
     a.yc = ps.yc;
@@ -456,6 +458,11 @@ hipError_t run_pass(const Pass& ps, const Plan& pl, hipStream_t st) {
     a.state = ps.state;
     a.cfg = ps.cfg;
     a.rebake = ps.rebake;
+    return a;
+}
+
+hipError_t run_pass(const Pass& ps, const Plan& pl, hipStream_t st) {
+    const PartialArgs a = pass_args(ps, pl);
     hipError_t e = launch_partial(a, pl.nc, st);
     if (e != hipSuccess || ps.group_counters != nullptr) return e;
     hipLaunchKernelGGL(merge_kernel, dim3(pl.ngroups), dim3(kRowsPerGroup), 0, st, a);
@@ -853,29 +860,16 @@ int sk_loop_init_f32(const sk_loop_f32* L, void* stream) {
     return e == hipSuccess ? SK_OK : hip_fail(e, "sk_loop_init_f32");
 }
 
-int sk_loop_run_f32(const sk_loop_f32* L, int iters, void* stream) {
-    if (L == nullptr || L->state == nullptr || L->fh == nullptr || L->gh == nullptr || L->ws == nullptr)
-        return fail(SK_E_ARG, "sk_loop_run_f32: null pointer");
-    if (int r = check_cloud(L->x, "x")) return r;
-    if (int r = check_cloud(L->y, "y")) return r;
-    if (int r = check_kp(L->d)) return r;
-    if (iters < 0) return fail(SK_E_ARG, "sk_loop_run_f32: iters %d < 0", iters);
-    const size_t need = sk_loop_workspace_bytes(L->x.npad, L->y.npad, L->d);
-    if (need == 0) return fail(SK_E_SHAPE, "sk_loop: %d x %d is too large for one launch", L->x.npad, L->y.npad);
-    if (L->ws_bytes < need) return fail(SK_E_WORKSPACE, "sk_loop_run_f32: workspace %zu < %zu bytes", L->ws_bytes, need);
-    if (((uintptr_t)L->ws & 255) != 0) return fail(SK_E_ARG, "sk_loop_run_f32: workspace must be 256-byte aligned");
-    const int kp = sk_pad_dim(L->d);
-    const LoopLayout lo = loop_layout(L);
-    const Plan& pf = lo.pf;
-    const Plan& pg = lo.pg;
-    float2* part = lo.part;
-    float2* meas = lo.meas;
-    sk_state* st = L->state;
-    const int* skip = &st->done;
-    const LoopCfg cfg = loop_cfg(L);
-    hipStream_t hs = (hipStream_t)stream;
+}  // extern "C"
 
-    Pass f = {};
+namespace {
+
+// The loop's two passes over its workspace layout: the f update (rows x against y; counts the iteration) and the g
+// update (rows y against x; convergence partials, loop control).
+void loop_passes(const sk_loop_f32* L, const LoopLayout& lo, Pass& f, Pass& g) {
+    const int kp = sk_pad_dim(L->d);
+    sk_state* st = L->state;
+    f = Pass{};
     f.xr = L->x.pk;
     f.rows_pad = L->x.npad;
     f.yc = L->y.pk;
@@ -886,7 +880,7 @@ int sk_loop_run_f32(const sk_loop_f32* L, int iters, void* stream) {
     f.u2 = lo.rg;
     f.v2 = lo.lyh;
     f.sc = st->sc_x;
-    f.skip = skip;
+    f.skip = &st->done;
     f.mode = kHalfStep;
     f.rows_role = 0;
     f.contraction = kF16x2;
@@ -898,10 +892,10 @@ int sk_loop_run_f32(const sk_loop_f32* L, int iters, void* stream) {
     f.cols_l2lo = lo.lyl;
     f.n_store = L->x.npad;
     f.tick = st;
-    f.part = part;
-    f.group_counters = fused_merge(pf) ? lo.counters + 1 : nullptr;
+    f.part = lo.part;
+    f.group_counters = fused_merge(lo.pf) ? lo.counters + 1 : nullptr;
 
-    Pass g = {};
+    g = Pass{};
     g.xr = L->y.pk;
     g.rows_pad = L->y.npad;
     g.yc = L->x.pk;
@@ -912,7 +906,7 @@ int sk_loop_run_f32(const sk_loop_f32* L, int iters, void* stream) {
     g.u2 = lo.rf;
     g.v2 = lo.lxh;
     g.sc = st->sc_y;
-    g.skip = skip;
+    g.skip = &st->done;
     g.mode = kHalfStep;
     g.rows_role = 1;
     g.contraction = kF16x2;
@@ -923,20 +917,246 @@ int sk_loop_run_f32(const sk_loop_f32* L, int iters, void* stream) {
     g.rows_l2lo = lo.lyl;
     g.cols_l2lo = lo.lxl;
     g.n_store = L->y.npad;
-    g.meas = meas;
+    g.meas = lo.meas;
     g.w = L->y.w;
     g.n_real = L->y.n;
-    g.part = part;
+    g.part = lo.part;
     g.counters = lo.counters;
     g.state = st;
-    g.cfg = cfg;
+    g.cfg = loop_cfg(L);
     g.rebake = log2_enabled() ? (char*)const_cast<void*>(L->x.pk) : nullptr;
-    g.group_counters = fused_merge(pg) ? lo.counters + 1 : nullptr;
+    g.group_counters = fused_merge(lo.pg) ? lo.counters + 1 : nullptr;
+}
 
+int check_loop(const sk_loop_f32* L, const char* where) {
+    if (L == nullptr || L->state == nullptr || L->fh == nullptr || L->gh == nullptr || L->ws == nullptr)
+        return fail(SK_E_ARG, "%s: null pointer", where);
+    if (int r = check_cloud(L->x, "x")) return r;
+    if (int r = check_cloud(L->y, "y")) return r;
+    if (int r = check_kp(L->d)) return r;
+    const size_t need = sk_loop_workspace_bytes(L->x.npad, L->y.npad, L->d);
+    if (need == 0) return fail(SK_E_SHAPE, "sk_loop: %d x %d is too large for one launch", L->x.npad, L->y.npad);
+    if (L->ws_bytes < need) return fail(SK_E_WORKSPACE, "%s: workspace %zu < %zu bytes", where, L->ws_bytes, need);
+    if (((uintptr_t)L->ws & 255) != 0) return fail(SK_E_ARG, "%s: workspace must be 256-byte aligned", where);
+    return SK_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int sk_loop_run_f32(const sk_loop_f32* L, int iters, void* stream) {
+    if (int r = check_loop(L, "sk_loop_run_f32")) return r;
+    if (iters < 0) return fail(SK_E_ARG, "sk_loop_run_f32: iters %d < 0", iters);
+    const LoopLayout lo = loop_layout(L);
+    Pass f, g;
+    loop_passes(L, lo, f, g);
+    hipStream_t hs = (hipStream_t)stream;
     for (int k = 0; k < iters; ++k) {
-        hipError_t e = run_pass(f, pf, hs);
-        if (e == hipSuccess) e = run_pass(g, pg, hs);
+        hipError_t e = run_pass(f, lo.pf, hs);
+        if (e == hipSuccess) e = run_pass(g, lo.pg, hs);
         if (e != hipSuccess) return hip_fail(e, "sk_loop_run_f32");
+    }
+    return SK_OK;
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------------------------------
+// Several loops at once (independent solves of the same d, such as the pairs of a wot pipeline): each launch runs
+// one pass of every loop, each on its own share of the workgroups, so that small solves fill the GPU together
+// instead of each paying a launch and its latencies per pass.
+
+namespace {
+
+constexpr int kBatchMapEntries = 1024;      // workgroups of one grouped launch, at most
+constexpr int kBatchMaxLoops = 1024;
+
+struct BatchLayout {
+    size_t args_f, args_g, map_f, map_g, bytes;
+};
+
+BatchLayout batch_layout(int count) {
+    BatchLayout b;
+    const size_t args = align_up((size_t)count * sizeof(PartialArgs));
+    const size_t map = align_up((size_t)kBatchMapEntries * sizeof(unsigned));
+    b.args_f = 0;
+    b.args_g = args;
+    b.map_f = 2 * args;
+    b.map_g = 2 * args + map;
+    b.bytes = 2 * args + 2 * map;
+    return b;
+}
+
+// Workgroups per pass: P_k = ceil(cost_k / T), with T the smallest per-workgroup cost (tiles, row-group boundaries
+// included) at which the P_k add up to at most `total`, so that every workgroup of the launch carries about T
+// tiles; then the workgroups left over, one at a time, to the pass with the largest cost per workgroup (while it
+// has more tiles than workgroups). Each pass gets one workgroup at least (then the sum is the number of passes if
+// that is larger). A single pass gets min(total, cost) workgroups: the split of its own launches.
+std::vector<int> share_workgroups(const std::vector<long long>& cost, int total) {
+    long long lo = 1, hi = 1;
+    for (long long c : cost) hi = std::max(hi, c);
+    auto need = [&](long long T) {
+        long long n = 0;
+        for (long long c : cost) n += std::max(1LL, (c + T - 1) / T);
+        return n;
+    };
+    while (lo < hi) {
+        const long long mid = lo + (hi - lo) / 2;
+        if (need(mid) <= total) hi = mid; else lo = mid + 1;
+    }
+    std::vector<int> P(cost.size());
+    long long used = 0;
+    for (size_t k = 0; k < cost.size(); ++k) {
+        P[k] = (int)std::max(1LL, (cost[k] + lo - 1) / lo);
+        used += P[k];
+    }
+    for (; used < total; ++used) {
+        size_t best = cost.size();
+        for (size_t k = 0; k < cost.size(); ++k)
+            if (P[k] < cost[k] && (best == cost.size() || cost[k] * P[best] > cost[best] * P[k])) best = k;
+        if (best == cost.size()) break;
+        ++P[best];
+    }
+    return P;
+}
+
+// The cost of a pass on the cost line of its split (tiles plus one boundary cost per row group after the first).
+long long pass_cost(const Plan& pl) { return (long long)pl.s.ftot; }
+
+// The map of one grouped launch: workgroup b runs workgroup p of pass k, map[b] = k << 16 | p; the passes' workgroups
+// are numbered in order and placed as the single-pass kernel places its own (the workgroups of one XCD hold one
+// contiguous range, xcd_contiguous); entries past the launch name no pass.
+std::vector<unsigned> batch_map(const std::vector<int>& P) {
+    std::vector<unsigned> order;
+    for (size_t k = 0; k < P.size(); ++k)
+        for (int p = 0; p < P[k]; ++p) order.push_back((unsigned)k << 16 | (unsigned)p);
+    const int n = (int)order.size();
+    std::vector<unsigned> map(kBatchMapEntries, 0xffffffffu);
+    const int q = n / kXcds, r = n % kXcds;
+    for (int b = 0; b < n; ++b) {
+        const int xcd = b % kXcds, idx = b / kXcds;
+        map[b] = order[xcd * q + (xcd < r ? xcd : r) + idx];
+    }
+    return map;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t sk_loop_batch_workspace_bytes(int count) {
+    if (count < 1 || count > kBatchMaxLoops) return 0;
+    return batch_layout(count).bytes;
+}
+
+int sk_loop_batch_plan(const int* nx_pad, const int* ny_pad, int count, int d, int* workgroups) {
+    if (nx_pad == nullptr || ny_pad == nullptr || workgroups == nullptr)
+        return fail(SK_E_ARG, "sk_loop_batch_plan: null pointer");
+    if (count < 1 || count > kBatchMaxLoops) return fail(SK_E_SHAPE, "sk_loop_batch_plan: count %d", count);
+    if (int r = check_kp(d)) return r;
+    const int kp = sk_pad_dim(d), total = cu_count();
+    std::vector<long long> cf(count), cg(count);
+    for (int k = 0; k < count; ++k) {
+        if (nx_pad[k] < SK_TILE || ny_pad[k] < SK_TILE || nx_pad[k] % SK_TILE || ny_pad[k] % SK_TILE)
+            return fail(SK_E_SHAPE, "sk_loop_batch_plan: loop %d: %d x %d", k, nx_pad[k], ny_pad[k]);
+        cf[k] = pass_cost(make_plan(nx_pad[k], ny_pad[k], kp));
+        cg[k] = pass_cost(make_plan(ny_pad[k], nx_pad[k], kp));
+    }
+    const std::vector<int> pf = share_workgroups(cf, total), pg = share_workgroups(cg, total);
+    for (int k = 0; k < count; ++k) {
+        workgroups[2 * k] = std::min(pf[k], 1024);
+        workgroups[2 * k + 1] = std::min(pg[k], 1024);
+    }
+    return SK_OK;
+}
+
+int sk_loop_batch_init_f32(const sk_loop_f32* const* loops, int count, void* ws, size_t ws_bytes, int* launch,
+                           void* stream) {
+    if (loops == nullptr || ws == nullptr || launch == nullptr) return fail(SK_E_ARG, "sk_loop_batch_init_f32: null pointer");
+    if (count < 1 || count > kBatchMaxLoops)
+        return fail(SK_E_SHAPE, "sk_loop_batch_init_f32: count %d (1 to %d)", count, kBatchMaxLoops);
+    const size_t need = sk_loop_batch_workspace_bytes(count);
+    if (ws_bytes < need) return fail(SK_E_WORKSPACE, "sk_loop_batch_init_f32: workspace %zu < %zu bytes", ws_bytes, need);
+    if (((uintptr_t)ws & 255) != 0) return fail(SK_E_ARG, "sk_loop_batch_init_f32: workspace must be 256-byte aligned");
+    const int d = loops[0] != nullptr ? loops[0]->d : 0;
+    std::vector<int> nx(count), ny(count), wg(2 * (size_t)count);
+    for (int k = 0; k < count; ++k) {
+        if (int r = check_loop(loops[k], "sk_loop_batch_init_f32")) return r;
+        if (loops[k]->d != d) return fail(SK_E_SHAPE, "sk_loop_batch_init_f32: loop %d has d %d, loop 0 %d", k, loops[k]->d, d);
+        nx[k] = loops[k]->x.npad;
+        ny[k] = loops[k]->y.npad;
+    }
+    if (int r = sk_loop_batch_plan(nx.data(), ny.data(), count, d, wg.data())) return r;
+    const int kp = sk_pad_dim(d);
+    std::vector<PartialArgs> af(count), ag(count);
+    std::vector<int> pf(count), pg(count);
+    long long nf = 0, ng = 0;
+    for (int k = 0; k < count; ++k) {
+        const sk_loop_f32* L = loops[k];
+        const LoopLayout lo = loop_layout(L);
+        const Plan bf = make_plan(L->x.npad, L->y.npad, kp, wg[2 * k]);
+        const Plan bg = make_plan(L->y.npad, L->x.npad, kp, wg[2 * k + 1]);
+        // the loop's workspace holds the partial slots of its own plans; a plan on fewer workgroups has no more
+        if (!bf.ok || !bg.ok || partial_bytes(bf, L->x.npad) > partial_bytes(lo.pf, L->x.npad) ||
+            partial_bytes(bg, L->y.npad) > partial_bytes(lo.pg, L->y.npad) ||
+            std::max(bf.ngroups, bg.ngroups) + 1 > lo.ncounters)
+            return fail(SK_E_SHAPE, "sk_loop_batch_init_f32: loop %d does not fit its workspace on %d / %d workgroups", k,
+                        wg[2 * k], wg[2 * k + 1]);
+        Pass f, g;
+        loop_passes(L, lo, f, g);
+        // every row group is merged inside the grouped kernel (its last workgroup), so no merge launch follows
+        f.group_counters = lo.counters + 1;
+        g.group_counters = lo.counters + 1;
+        af[k] = pass_args(f, bf);
+        ag[k] = pass_args(g, bg);
+        pf[k] = bf.s.P;
+        pg[k] = bg.s.P;
+        nf += bf.s.P;
+        ng += bg.s.P;
+    }
+    if (nf > kBatchMapEntries || ng > kBatchMapEntries)
+        return fail(SK_E_SHAPE, "sk_loop_batch_init_f32: %lld / %lld workgroups > %d", nf, ng, kBatchMapEntries);
+    const std::vector<unsigned> mf = batch_map(pf), mg = batch_map(pg);
+    const BatchLayout bl = batch_layout(count);
+    char* base = (char*)ws;
+    hipStream_t hs = (hipStream_t)stream;
+    hipError_t e = hipMemcpyAsync(base + bl.args_f, af.data(), af.size() * sizeof(PartialArgs), hipMemcpyHostToDevice, hs);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(base + bl.args_g, ag.data(), ag.size() * sizeof(PartialArgs), hipMemcpyHostToDevice, hs);
+    if (e == hipSuccess) e = hipMemcpyAsync(base + bl.map_f, mf.data(), mf.size() * sizeof(unsigned), hipMemcpyHostToDevice, hs);
+    if (e == hipSuccess) e = hipMemcpyAsync(base + bl.map_g, mg.data(), mg.size() * sizeof(unsigned), hipMemcpyHostToDevice, hs);
+    // the host arrays die with this call: the copies complete before it returns
+    if (e == hipSuccess) e = hipStreamSynchronize(hs);
+    if (e != hipSuccess) return hip_fail(e, "sk_loop_batch_init_f32");
+    launch[0] = kp / 16;
+    launch[1] = (int)nf;
+    launch[2] = (int)ng;
+    return SK_OK;
+}
+
+int sk_loop_run_batch_f32(const void* ws, size_t ws_bytes, int count, const int* launch, int iters, void* stream) {
+    if (ws == nullptr || launch == nullptr) return fail(SK_E_ARG, "sk_loop_run_batch_f32: null pointer");
+    if (count < 1 || count > kBatchMaxLoops) return fail(SK_E_SHAPE, "sk_loop_run_batch_f32: count %d", count);
+    if (ws_bytes < sk_loop_batch_workspace_bytes(count))
+        return fail(SK_E_WORKSPACE, "sk_loop_run_batch_f32: workspace %zu < %zu bytes", ws_bytes,
+                    sk_loop_batch_workspace_bytes(count));
+    const int nc = launch[0], nf = launch[1], ng = launch[2];
+    if (nc < 1 || nc * 16 > SK_KP_MAX || nf < 1 || ng < 1 || nf > kBatchMapEntries || ng > kBatchMapEntries)
+        return fail(SK_E_ARG, "sk_loop_run_batch_f32: launch {%d, %d, %d} is not one sk_loop_batch_init_f32 returned",
+                    nc, nf, ng);
+    if (iters < 0) return fail(SK_E_ARG, "sk_loop_run_batch_f32: iters %d < 0", iters);
+    const BatchLayout bl = batch_layout(count);
+    const char* base = (const char*)ws;
+    const PartialArgs* af = (const PartialArgs*)(base + bl.args_f);
+    const PartialArgs* ag = (const PartialArgs*)(base + bl.args_g);
+    const unsigned* mf = (const unsigned*)(base + bl.map_f);
+    const unsigned* mg = (const unsigned*)(base + bl.map_g);
+    hipStream_t hs = (hipStream_t)stream;
+    for (int k = 0; k < iters; ++k) {
+        hipError_t e = launch_grouped(af, mf, count, nf, nc, 0, hs);
+        if (e == hipSuccess) e = launch_grouped(ag, mg, count, ng, nc, 1, hs);
+        if (e != hipSuccess) return hip_fail(e, "sk_loop_run_batch_f32");
     }
     return SK_OK;
 }

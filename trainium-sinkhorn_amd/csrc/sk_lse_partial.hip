@@ -740,13 +740,23 @@ __device__ __forceinline__ const PartialArgs& kernel_args() {
 // thread 0's atomic add follow all of them; the last arrival reads the slots with device-scope loads, which
 // miss the XCD's L2. No fence: a device-scope one would write back and invalidate the L2 under the operand
 // tiles the other workgroups of the XCD are streaming.
-__device__ inline void arrive(const PartialArgs& a, int g) {
+template <bool KARG>
+__device__ inline void arrive(const PartialArgs& a, const PartialArgs* kp, int g) {
     __shared__ int s_last;
     // The merge's own argument fields (epilogue vectors, loop state and configuration), requested here in one
-    // batch through a pointer the compiler cannot follow out of this function, so that they arrive while the
-    // stores and the counter make their round trips; the fields the segments use come from `a`, already held.
-    const PartialArgs* kp = &kernel_args();
-    asm volatile("" : "+s"(kp));
+    // batch through a pointer to the argument block (kp) the compiler cannot follow out of this function, so that
+    // they arrive while the stores and the counter make their round trips; the fields the segments use come from
+    // `a`, already held. KARG: kp is the kernel argument segment (an empty asm hides it); otherwise an argument
+    // block in device memory (the grouped kernel), hidden by taking its two halves through readfirstlane, which
+    // the compiler keeps in scalar registers where the asm's register constraint could not.
+    if constexpr (KARG) {
+        asm volatile("" : "+s"(kp));
+    } else {
+        const unsigned long long v = (unsigned long long)(uintptr_t)kp;
+        const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)v);
+        const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)(v >> 32));
+        kp = (const PartialArgs*)(uintptr_t)(((unsigned long long)hi << 32) | lo);
+    }
     PartialArgs m = a;
     m.xsq = kp->xsq;
     m.off = kp->off;
@@ -802,10 +812,10 @@ __device__ inline void arrive(const PartialArgs& a, int g) {
 // The work segments of workgroup p: a_ij = x_i . y_j + cs (alpha cu_j + (beta + beta_lo) cv_j) in the kernel's
 // units (the column term rounded once, then scaled by a power of two), scores exp2(c (a - M)) (with L2:
 // exp2(fma(a, c, -c M)), a in log2 units times the copy's unit t = 1 / c).
-template <int NC, int ROLE, int CT, bool L2>
-__device__ __forceinline__ void segments(const PartialArgs& a, int p, int wv, const float* cu, const float* cv,
-                                         float alpha, float beta, float beta_lo, float cs, float c, float inv_sigma,
-                                         typename Contract<CT>::T* lds_y, float* lds_col) {
+template <int NC, int ROLE, int CT, bool L2, bool KARG>
+__device__ __forceinline__ void segments(const PartialArgs& a, const PartialArgs* kp, int p, int wv, const float* cu,
+                                         const float* cv, float alpha, float beta, float beta_lo, float cs, float c,
+                                         float inv_sigma, typename Contract<CT>::T* lds_y, float* lds_col) {
     // The segment bounds are 32-bit integer arithmetic (the divisions expand to vector code); their results are
     // the same in every lane, and readfirstlane hands them to the scalar unit, so the tile loop's counters and
     // operand addresses stay in scalar registers.
@@ -824,7 +834,7 @@ __device__ __forceinline__ void segments(const PartialArgs& a, int p, int wv, co
         else
             Staged<NC, ROLE, CT, L2>::run(a, rb0, tb, te, slot, cu, cv, alpha, beta, beta_lo, cs, c, inv_sigma, lds_y,
                                           lds_col);
-        if (a.group_counters != nullptr) arrive(a, g);
+        if (a.group_counters != nullptr) arrive<KARG>(a, kp, g);
         // The segment's stores complete here, as an s_waitcnt the compiler sees (vmcnt(0); expcnt and lgkmcnt
         // unrestricted, gfx9 encoding): otherwise the loop's back edge carries the slot stores, whose address and
         // data registers the next prologue reuses, and the compiler's wait for them there (its counts cannot
@@ -834,9 +844,10 @@ __device__ __forceinline__ void segments(const PartialArgs& a, int p, int wv, co
     }
 }
 
-template <int NC, int ROLE, int CT>
-__global__ __launch_bounds__(kBlockK) __attribute__((amdgpu_waves_per_eu(kWavesPerSimd, kWavesPerSimd)))
-void lse_partial_kernel(PartialArgs a) {
+// Workgroup p of one pass with arguments a (kp: the same argument block, from which the merge inside the kernel
+// reads its own fields late; KARG: the kernel argument segment).
+template <int NC, int ROLE, int CT, bool KARG>
+__device__ __forceinline__ void partial_pass(const PartialArgs& a, const PartialArgs* kp, int p) {
     // Every scalar this launch needs (the loop's done flag, the eps scalars, both clouds' scales, the first
     // cloud's log2-copy tag) is requested at once, and the done flag tested after: one memory round trip before
     // the work starts.
@@ -858,7 +869,6 @@ void lse_partial_kernel(PartialArgs a) {
     __shared__ typename Contract<CT>::T lds_y[kLdsY];
     __shared__ __attribute__((aligned(16))) float lds_col[kLdsCol];
     const int wv = __builtin_amdgcn_readfirstlane(tid_x() >> 6);   // one value per wave
-    const int p = xcd_contiguous(wg_x(), a.s.P);
 
     // a_ij = x_i . y_j + alpha u_j + beta v_j in accumulator units, scores exp2(c (a - M)):
     // half-step: a = x . y + (gh + eps log b) / 2, c = (2 / eps) log2(e); plain row-LSE: a = xa . ya + mask,
@@ -888,17 +898,43 @@ void lse_partial_kernel(PartialArgs a) {
             // The usual unit t = 1 gets its own inlined copy: with c = 1 a constant, each exponential's argument is
             // the two-operand a - m (v_sub_f32) instead of the three-operand fma.
             if (a.u2 != nullptr && cb_t == 1.0f)
-                segments<NC, ROLE, CT, true>(a, p, wv, a.u2, a.v2, 1.0f, 1.0f, 0.0f, 1.0f, 1.0f, 1.0f, lds_y, lds_col);
+                segments<NC, ROLE, CT, true, KARG>(a, kp, p, wv, a.u2, a.v2, 1.0f, 1.0f, 0.0f, 1.0f, 1.0f, 1.0f, lds_y, lds_col);
             else if (a.u2 != nullptr)
-                segments<NC, ROLE, CT, true>(a, p, wv, a.u2, a.v2, 1.0f, 1.0f, 0.0f, cb_t, it, it, lds_y, lds_col);
+                segments<NC, ROLE, CT, true, KARG>(a, kp, p, wv, a.u2, a.v2, 1.0f, 1.0f, 0.0f, cb_t, it, it, lds_y, lds_col);
             else
-                segments<NC, ROLE, CT, true>(a, p, wv, a.u, a.v, alpha, beta, 0.0f, c * cb_t, it, it, lds_y, lds_col);
+                segments<NC, ROLE, CT, true, KARG>(a, kp, p, wv, a.u, a.v, alpha, beta, 0.0f, c * cb_t, it, it, lds_y, lds_col);
             return;
         }
     }
     const float sigma = sx * sy, inv_sigma = (1.0f / sx) * (1.0f / sy);
-    segments<NC, ROLE, CT, false>(a, p, wv, a.u, a.v, alpha, beta, 0.0f, sigma, c * inv_sigma, inv_sigma, lds_y,
+    segments<NC, ROLE, CT, false, KARG>(a, kp, p, wv, a.u, a.v, alpha, beta, 0.0f, sigma, c * inv_sigma, inv_sigma, lds_y,
                                   lds_col);
+}
+
+template <int NC, int ROLE, int CT>
+__global__ __launch_bounds__(kBlockK) __attribute__((amdgpu_waves_per_eu(kWavesPerSimd, kWavesPerSimd)))
+void lse_partial_kernel(PartialArgs a) {
+    partial_pass<NC, ROLE, CT, true>(a, &kernel_args(), xcd_contiguous(wg_x(), a.s.P));
+}
+
+// The grouped form (sk_loop_run_batch_f32): the passes of several independent loops in one launch, each on its
+// own share of the workgroups. Workgroup b runs workgroup p of pass k, map[b] = k << 16 | p, with pass k's
+// arguments args[k] in device memory; a workgroup past the map or naming no pass of this kp returns at once.
+template <int NC, int ROLE>
+__global__ __launch_bounds__(kBlockK) __attribute__((amdgpu_waves_per_eu(kWavesPerSimd, kWavesPerSimd)))
+void lse_partial_grouped_kernel(const PartialArgs* __restrict__ args, const unsigned* __restrict__ map, int count,
+                                int nmap) {
+    const int b = wg_x();
+    if (b >= nmap) return;
+    const unsigned e = __builtin_amdgcn_readfirstlane(map[b]);    // uniform: one entry per workgroup
+    const int k = (int)(e >> 16), p = (int)(e & 0xffffu);
+    if (k >= count) return;
+    // Through the constant address space, as the kernel argument segment is read: scalar loads, the fields in
+    // scalar registers as the pass expects them (the block does not change during the launch).
+    using ConstArgs = const __attribute__((address_space(4))) PartialArgs;
+    const PartialArgs* ap = (const PartialArgs*)((ConstArgs*)args + k);
+    if (ap->nc != NC || p >= ap->s.P) return;
+    partial_pass<NC, ROLE, kF16x2, false>(*ap, ap, p);
 }
 
 template <int NC>
@@ -914,9 +950,29 @@ hipError_t launch_nc(const PartialArgs& a, hipStream_t st) {
     return hipGetLastError();
 }
 
+template <int NC>
+hipError_t launch_grouped_nc(const PartialArgs* args, const unsigned* map, int count, int nmap, int role,
+                             hipStream_t st) {
+    if (role == 0)
+        hipLaunchKernelGGL((lse_partial_grouped_kernel<NC, 0>), dim3(nmap), dim3(kBlockK), 0, st, args, map, count, nmap);
+    else
+        hipLaunchKernelGGL((lse_partial_grouped_kernel<NC, 1>), dim3(nmap), dim3(kBlockK), 0, st, args, map, count, nmap);
+    return hipGetLastError();
+}
+
 }  // namespace
 
 #if SK_PARTIAL_LARGE
+hipError_t launch_grouped_large(const PartialArgs* args, const unsigned* map, int count, int nmap, int nc, int role,
+                                hipStream_t st) {
+    switch (nc) {
+        case 5: return launch_grouped_nc<5>(args, map, count, nmap, role, st);
+        case 6: return launch_grouped_nc<6>(args, map, count, nmap, role, st);
+        case 7: return launch_grouped_nc<7>(args, map, count, nmap, role, st);
+        case 8: return launch_grouped_nc<8>(args, map, count, nmap, role, st);
+        default: return hipErrorInvalidValue;
+    }
+}
 hipError_t launch_partial_large(const PartialArgs& a, int nc, hipStream_t st) {
     switch (nc) {
         case 5: return launch_nc<5>(a, st);
@@ -927,6 +983,16 @@ hipError_t launch_partial_large(const PartialArgs& a, int nc, hipStream_t st) {
     }
 }
 #else
+hipError_t launch_grouped_small(const PartialArgs* args, const unsigned* map, int count, int nmap, int nc, int role,
+                                hipStream_t st) {
+    switch (nc) {
+        case 1: return launch_grouped_nc<1>(args, map, count, nmap, role, st);
+        case 2: return launch_grouped_nc<2>(args, map, count, nmap, role, st);
+        case 3: return launch_grouped_nc<3>(args, map, count, nmap, role, st);
+        case 4: return launch_grouped_nc<4>(args, map, count, nmap, role, st);
+        default: return hipErrorInvalidValue;
+    }
+}
 hipError_t launch_partial_small(const PartialArgs& a, int nc, hipStream_t st) {
     switch (nc) {
         case 1: return launch_nc<1>(a, st);

@@ -94,6 +94,13 @@ _SIGS = {
     "sk_loop_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int, ctypes.c_int, ctypes.c_int]),
     "sk_loop_init_f32": (ctypes.c_int, [ctypes.POINTER(SkLoop), ctypes.c_void_p]),
     "sk_loop_run_f32": (ctypes.c_int, [ctypes.POINTER(SkLoop), ctypes.c_int, ctypes.c_void_p]),
+    "sk_loop_batch_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int]),
+    "sk_loop_batch_plan": (ctypes.c_int, [ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int), ctypes.c_int,
+                                          ctypes.c_int, ctypes.POINTER(ctypes.c_int)]),
+    "sk_loop_batch_init_f32": (ctypes.c_int, [ctypes.POINTER(ctypes.POINTER(SkLoop)), ctypes.c_int, ctypes.c_void_p,
+                                              ctypes.c_size_t, ctypes.POINTER(ctypes.c_int), ctypes.c_void_p]),
+    "sk_loop_run_batch_f32": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.POINTER(ctypes.c_int),
+                                             ctypes.c_int, ctypes.c_void_p]),
     "sk_cost_median_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int, ctypes.c_int, ctypes.c_int]),
     "sk_cost_median_f64": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                           ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
@@ -280,6 +287,15 @@ class HipCloud:
         return SkCloud(self.pk.data_ptr(), self.sq.data_ptr(), self.log_w.data_ptr(), self.w.data_ptr(),
                        _ptr(self.off), self.n, self.npad, self.log_w_lo.data_ptr())
 
+    def set_off(self, off: np.ndarray) -> None:
+        """A new offset log(target / weight) in place (the cloud was made with one), for a new solve on the same
+        points and weights: loops set up on this cloud keep their pointers."""
+        if self.off is None:
+            raise ValueError("set_off: the cloud was made without an offset")
+        v = np.zeros(self.npad, dtype=np.float32)
+        v[:self.n] = off
+        self.off.copy_(torch.from_numpy(v))
+
 
 def bake_log2(first: HipCloud, second: HipCloud, sc: torch.Tensor) -> None:
     """Make the first cloud's log2-unit copy for sc[0] = 2/eps against `second` (sk_bake_log2_f32): half-steps
@@ -369,13 +385,17 @@ class DeviceLoop:
 
     def __init__(self, X: HipCloud, Y: HipCloud, *, eps: float, rho_x, rho_y, sched, stages, tol: float,
                  stage_tol: float, max_iters: int, check_every: int, stage_max_iters: int, fixed_iters: bool,
-                 balanced: bool):
+                 balanced: bool, state: torch.Tensor | None = None):
         dev = X.device
         lb = lib()
         self.X, self.Y = X, Y
         self.fh = torch.zeros(X.npad, dtype=torch.float32, device=dev)
         self.gh = torch.zeros(Y.npad, dtype=torch.float32, device=dev)      # gh = 0: g0 = |y|^2 (sinkhorn.py:336)
-        self.state = torch.zeros(ctypes.sizeof(SkState), dtype=torch.uint8, device=dev)
+        if state is None:                  # (a DeviceLoopBatch keeps its loops' states in one block: a row of it)
+            state = torch.zeros(ctypes.sizeof(SkState), dtype=torch.uint8, device=dev)
+        if state.numel() != ctypes.sizeof(SkState) or state.dtype != torch.uint8 or state.data_ptr() % 8:
+            raise ValueError("state must be the loop's own 8-byte aligned uint8 block of sizeof(SkState) bytes")
+        self.state = state
         self._sched = torch.tensor(list(sched), dtype=torch.float64, device=dev) if len(sched) else None
         self._stages = torch.tensor(list(stages), dtype=torch.float64, device=dev) if len(stages) else None
         self.ws = _workspace(lb.sk_loop_workspace_bytes(X.npad, Y.npad, X.d), dev)
@@ -477,3 +497,78 @@ class DeviceLoop:
             if not inflight and queued >= self.max_iters:  # pragma: no cover - done must be set by then
                 return self.read_state()
 
+
+
+
+class DeviceLoopBatch:
+    """Several DeviceLoops of one d run together (sk_loop_run_batch_f32): each iteration is two launches, the f
+    updates of all the loops and then their g updates, each loop's pass on its own share of the GPU's workgroups
+    (in proportion to its work) and merged in the launch, each loop's control as in its own loop. For independent
+    small solves, such as the pairs of a wot pipeline, which alone leave most of the GPU idle during a launch's
+    latencies. A loop's splits are coarser than its own launches', so its potentials agree with DeviceLoop.run's to
+    float32 rounding (with one loop, bit for bit). The loops' states are rows of one device block (`states`, given
+    to each DeviceLoop as its `state`), read back in one copy per batch of iterations; a loop that is done idles
+    while the others go on."""
+
+    @staticmethod
+    def state_block(n: int, device) -> torch.Tensor:
+        """A zeroed (n, sizeof(SkState)) uint8 block whose row k is loop k's state."""
+        return torch.zeros((n, ctypes.sizeof(SkState)), dtype=torch.uint8, device=device)
+
+    def __init__(self, loops: list[DeviceLoop], states: torch.Tensor):
+        if not loops:
+            raise ValueError("DeviceLoopBatch needs at least one loop")
+        n = len(loops)
+        if states.shape != (n, ctypes.sizeof(SkState)) or any(
+                l.state.data_ptr() != states[k].data_ptr() for k, l in enumerate(loops)):
+            raise ValueError("each loop's state must be its row of `states` (DeviceLoopBatch.state_block)")
+        lb = lib()
+        self.loops, self.states = loops, states
+        self.ws = _workspace(lb.sk_loop_batch_workspace_bytes(n), loops[0].X.device)
+        self._ptrs = (ctypes.POINTER(SkLoop) * n)(*[ctypes.pointer(l._L) for l in loops])
+        self._launch = (ctypes.c_int * 3)()
+        self.max_iters = max(l.max_iters for l in loops)
+        self.check_every = min(l.check_every for l in loops)
+        self._pinned = [torch.empty(states.numel(), dtype=torch.uint8, pin_memory=True) for _ in range(2)]
+
+    def init(self) -> None:
+        for l in self.loops:
+            l.init()
+        _check(lib().sk_loop_batch_init_f32(self._ptrs, len(self.loops), self.ws.data_ptr(), self.ws.numel(),
+                                            self._launch, _stream()), "sk_loop_batch_init_f32")
+
+    def enqueue(self, iters: int) -> None:
+        _check(lib().sk_loop_run_batch_f32(self.ws.data_ptr(), self.ws.numel(), len(self.loops), self._launch,
+                                           int(iters), _stream()), "sk_loop_run_batch_f32")
+
+    def _parse(self, buf: torch.Tensor) -> list[SkState]:
+        raw = buf.numpy().tobytes()
+        sz = ctypes.sizeof(SkState)
+        return [SkState.from_buffer_copy(raw[k * sz:(k + 1) * sz]) for k in range(len(self.loops))]
+
+    def run(self, batch: int | None = None) -> list[SkState]:
+        """Run every loop to `done`. Returns the final states, in the loops' order. As DeviceLoop.run: batches of
+        iterations with the next one queued while the states of the one before are read."""
+        self.init()
+        batch = max(1, int(batch or max(self.check_every, 10)))
+        queued, slot, inflight = 0, 0, []
+        while True:
+            if queued < self.max_iters:
+                k = min(batch, self.max_iters - queued)
+                self.enqueue(k)
+                queued += k
+                buf = self._pinned[slot % 2]
+                slot += 1
+                buf.copy_(self.states.view(-1), non_blocking=True)
+                ev = torch.cuda.Event()
+                ev.record()
+                inflight.append((buf, ev))
+                if len(inflight) < 2 and queued < self.max_iters:
+                    continue
+            buf, ev = inflight.pop(0)
+            ev.synchronize()
+            sts = self._parse(buf)
+            if all(st.done for st in sts):
+                return sts
+            if not inflight and queued >= self.max_iters:  # pragma: no cover - done must be set by then
+                return self._parse(self.states.view(-1).to("cpu"))

@@ -51,40 +51,65 @@ def wot_transport_map(x0: np.ndarray, x1: np.ndarray, growth: np.ndarray | None 
                       tol: float = 1e-6, stage_tol: float = 1e-6, opts: SinkhornOptions | None = None) -> TransportMap:
     """One wot transport map between x0 (I cells) and x1 (J cells) (src/trnopt/singlecell.py:61-86). opts
     supplies backend, kernel, check_every and max_iters; eps, rho, normalize and the stages are set here."""
-    I, J = len(x0), len(x1)
-    G = np.ones(I) if growth is None else np.power(np.asarray(growth, dtype=np.float64), delta_days)
-    opts = opts or SinkhornOptions()
-    hip = _use_hip(opts, np.shape(x0)[1])
-    t = time.perf_counter()
-    # once per pair (the cost does not change across growth iterations); on the GPU when the fused path runs
-    norm = normalization(x0, x1, how="median", device=_gpu_device(opts) if hip and np.shape(x0)[1] <= 128 else None)
-    seconds = time.perf_counter() - t
-    base = replace(opts, eps=eps, rho=(lambda1, lambda2), normalize=norm,
-                   eps_stages=wot_eps_stages(eps), stage_tol=stage_tol, tol=tol, eps_start=None, fixed_iters=False)
-    a, b = np.full(I, 1.0 / I), np.full(J, 1.0 / J)
-    learned, iters, res = [], 0, None
-    for i in range(growth_iters):
-        if i > 0:
-            G = I * res.row_mass
-        learned.append(G)
+    w = _WotPair(x0, x1, growth, delta_days, eps, lambda1, lambda2, tol, stage_tol, opts)
+    for _ in range(growth_iters):
         t = time.perf_counter()
-        res = sinkhorn(x0, x1, a, b, base, a_target=G / I, b_target=np.full(J, G.mean() / J))
-        seconds += time.perf_counter() - t
-        iters += res.iterations
-    return TransportMap(result=res, learned_growth=learned, seconds=seconds, iterations=iters)
+        w.take(sinkhorn(**w.problem()), time.perf_counter() - t)
+    return w.transport_map()
 
 
-def wot_transport_maps(pairs, growth=None, delta_days=1.0, streams: int = 4, **kw) -> list:
+class _WotPair:
+    """One pair's wot solve across its growth iterations (src/trnopt/singlecell.py:61-86): the median
+    normalisation once, then per growth iteration the problem for sinkhorn() and the learned growth from its
+    result."""
+
+    def __init__(self, x0, x1, growth, delta_days, eps, lambda1, lambda2, tol, stage_tol, opts):
+        self.x0, self.x1 = x0, x1
+        self.I, self.J = I, J = len(x0), len(x1)
+        self.G = np.ones(I) if growth is None else np.power(np.asarray(growth, dtype=np.float64), delta_days)
+        opts = opts or SinkhornOptions()
+        hip = _use_hip(opts, np.shape(x0)[1])
+        t = time.perf_counter()
+        # once per pair (the cost does not change across growth iterations); on the GPU when the fused path runs
+        norm = normalization(x0, x1, how="median", device=_gpu_device(opts) if hip and np.shape(x0)[1] <= 128 else None)
+        self.seconds = time.perf_counter() - t
+        self.base = replace(opts, eps=eps, rho=(lambda1, lambda2), normalize=norm, eps_stages=wot_eps_stages(eps),
+                            stage_tol=stage_tol, tol=tol, eps_start=None, fixed_iters=False)
+        self.a, self.b = np.full(I, 1.0 / I), np.full(J, 1.0 / J)
+        self.learned, self.iters, self.res = [], 0, None
+
+    def problem(self) -> dict:
+        """sinkhorn()'s arguments for the next growth iteration (the row target from the last result's row sums)."""
+        if self.res is not None:
+            self.G = self.I * self.res.row_mass
+        self.learned.append(self.G)
+        return dict(x=self.x0, y=self.x1, a=self.a, b=self.b, opts=self.base, a_target=self.G / self.I,
+                    b_target=np.full(self.J, self.G.mean() / self.J))
+
+    def take(self, res: SinkhornResult, seconds: float) -> None:
+        self.res = res
+        self.seconds += seconds
+        self.iters += res.iterations
+
+    def transport_map(self) -> TransportMap:
+        return TransportMap(result=self.res, learned_growth=self.learned, seconds=self.seconds, iterations=self.iters)
+
+
+def wot_transport_maps(pairs, growth=None, delta_days=1.0, streams: int = 4, batch: bool = True, **kw) -> list:
     """wot_transport_map for every (x0, x1) of `pairs` -- the consecutive time points of a pipeline, whose maps
-    are independent -- with up to `streams` pairs in flight at once on the GPU (the reference's example runs them
-    one after the other, examples/singlecell_wot.py:84-89).
+    are independent -- solved together on the GPU (the reference's example runs them one after the other,
+    examples/singlecell_wot.py:84-89).
 
     growth: None or one growth array per pair; delta_days: a number or one per pair; kw: wot_transport_map's
-    other arguments (eps, lambda1, lambda2, growth_iters, tol, stage_tol, opts). On the fused path each pair runs
-    on its own HIP stream, driven by its own host thread: a small pair's kernels are mostly launch and load
-    latency, which the pairs beside it fill. A pair's kernels, work split and host steps do not depend on what
-    runs beside it, so every map equals wot_transport_map's for that pair bit for bit. With streams=1, or on the
-    torch path, the pairs run in order. Returns the TransportMaps in the order of `pairs`."""
+    other arguments (eps, lambda1, lambda2, growth_iters, tol, stage_tol, opts). On the fused path:
+      batch=True (default): each growth iteration of every pair in one batched solve (sinkhorn_batch: each launch
+        one half-step of every pair, each on its share of the GPU's workgroups), the pairs' maps equal to
+        wot_transport_map's to float32 rounding;
+      batch=False: up to `streams` pairs in flight, each on its own HIP stream driven by its own host thread; a
+        pair's kernels, work split and host steps do not depend on what runs beside it, so every map equals
+        wot_transport_map's for that pair bit for bit.
+    With streams=1 and batch=False, or on the torch path, the pairs run in order. Returns the TransportMaps in the
+    order of `pairs`."""
     import torch
     pairs = list(pairs)
     n = len(pairs)
@@ -99,7 +124,10 @@ def wot_transport_maps(pairs, growth=None, delta_days=1.0, streams: int = 4, **k
         x0, x1 = pairs[k]
         return wot_transport_map(x0, x1, growths[k], days[k], **kw)
 
-    if streams == 1 or n < 2 or not all(_use_hip(opts, np.shape(x0)[1]) for x0, _ in pairs):
+    fused = n >= 2 and all(_use_hip(opts, np.shape(x0)[1]) for x0, _ in pairs)
+    if fused and batch and len({np.shape(x0)[1] for x0, _ in pairs}) == 1:
+        return _wot_maps_batched(pairs, growths, days, **kw)
+    if streams == 1 or not fused:
         return [one(k) for k in range(n)]
     import threading
     from concurrent.futures import ThreadPoolExecutor
@@ -125,6 +153,31 @@ def wot_transport_maps(pairs, growth=None, delta_days=1.0, streams: int = 4, **k
     for s in pool:
         caller.wait_stream(s)
     return maps
+
+
+def _wot_maps_batched(pairs, growths, days, eps: float = 0.05, lambda1: float = 1.0, lambda2: float = 50.0,
+                      growth_iters: int = 1, tol: float = 1e-6, stage_tol: float = 1e-6,
+                      opts: SinkhornOptions | None = None) -> list:
+    """wot_transport_maps' batched form: every pair's normalisation, then each growth iteration of all the pairs as
+    one batched solve (sinkhorn_batch's), the pairs' clouds prepared and packed once for all growth iterations
+    (only the row and column targets change between them). A pair's `seconds` is its normalisation plus the whole
+    of each batch it took part in."""
+    from .sinkhorn import _HipBatch
+    ws = [_WotPair(x0, x1, growths[k], days[k], eps, lambda1, lambda2, tol, stage_tol, opts)
+          for k, (x0, x1) in enumerate(pairs)]
+    batch = None
+    for _ in range(growth_iters):
+        t = time.perf_counter()
+        problems = [w.problem() for w in ws]
+        if batch is None:
+            batch = _HipBatch(problems)
+            results = batch.solve()
+        else:
+            results = batch.solve([(q["a_target"], q["b_target"]) for q in problems])
+        dt = time.perf_counter() - t
+        for w, r in zip(ws, results):
+            w.take(r, dt)
+    return [w.transport_map() for w in ws]
 
 
 def wot_tmap(x0, x1, tm: TransportMap) -> np.ndarray:

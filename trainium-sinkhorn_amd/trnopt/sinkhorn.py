@@ -190,33 +190,44 @@ def _solve_torch(p, opts: SinkhornOptions):
 # ---------------------------------------------------------------------------------------------------------
 # The fused HIP path (kernel="hip")
 
-def _solve_hip(p, opts: SinkhornOptions):
+def _hip_setup(p, opts: SinkhornOptions, dev, state=None):
+    """The device side of one solve on the fused path: both clouds packed, the loop set up (not run)."""
     from . import hip_sinkhorn as hk
-    dev = torch.device(opts.backend.device)
-    if dev.index is None:
-        dev = torch.device("cuda", torch.cuda.current_device())
+    X = hk.HipCloud(p.xs, p.log_a, dev, p.off_x, role=0)
+    Y = hk.HipCloud(p.ys, p.log_b, dev, p.off_y, role=1)
+    loop = hk.DeviceLoop(X, Y, eps=opts.eps, rho_x=p.rho_x, rho_y=p.rho_y, sched=p.sched, stages=p.stages,
+                         tol=p.tol, stage_tol=p.stage_tol, max_iters=opts.max_iters,
+                         check_every=opts.check_every, stage_max_iters=opts.stage_max_iters,
+                         fixed_iters=opts.fixed_iters, balanced=p.balanced, state=state)
+    c1 = None if p.balanced else hk.scalars(opts.eps, 1.0, dev)     # requested before the loop's launches
+    return SimpleNamespace(X=X, Y=Y, loop=loop, c1=c1)
+
+
+def _hip_finish(p, s, st):
+    """f = fh + |x|^2 in float32 on the device, then float64, as the reference reads it back (:379-380); unbalanced,
+    also one balanced half-step each way (kappa = 1, no offset) at the final eps (:381-389). One read-back."""
+    from . import hip_sinkhorn as hk
+    X, Y, loop = s.X, s.Y, s.loop
+    parts = [(loop.fh + X.sq)[:X.n], (loop.gh + Y.sq)[:Y.n]]
+    if not p.balanced:
+        parts.append((hk.half_step(X, Y, loop.gh, s.c1, use_off=False) + X.sq)[:X.n])
+        parts.append((hk.half_step(Y, X, loop.fh, s.c1, use_off=False) + Y.sq)[:Y.n])
+    host = torch.cat(parts).to("cpu", torch.float64).numpy()
+    f, g = host[:X.n], host[X.n:X.n + Y.n]
+    fb = gb = None
+    if not p.balanced:
+        fb, gb = host[X.n + Y.n:2 * X.n + Y.n], host[2 * X.n + Y.n:]
+    return f, g, fb, gb, int(st.it), float(st.err), bool(st.converged)
+
+
+def _solve_hip(p, opts: SinkhornOptions):
+    dev = _gpu_device(opts)
     with torch.cuda.device(dev):
-        X = hk.HipCloud(p.xs, p.log_a, dev, p.off_x, role=0)
-        Y = hk.HipCloud(p.ys, p.log_b, dev, p.off_y, role=1)
-        loop = hk.DeviceLoop(X, Y, eps=opts.eps, rho_x=p.rho_x, rho_y=p.rho_y, sched=p.sched, stages=p.stages,
-                             tol=p.tol, stage_tol=p.stage_tol, max_iters=opts.max_iters,
-                             check_every=opts.check_every, stage_max_iters=opts.stage_max_iters,
-                             fixed_iters=opts.fixed_iters, balanced=p.balanced)
+        s = _hip_setup(p, opts, dev)
         t0 = time.perf_counter()
-        c1 = None if p.balanced else hk.scalars(opts.eps, 1.0, dev)     # requested before the loop's launches
-        st = loop.run()
-        # f = fh + |x|^2 in float32 on the device, then float64, as the reference reads it back (:379-380); unbalanced,
-        # also one balanced half-step each way (kappa = 1, no offset) at the final eps (:381-389). One read-back.
-        parts = [(loop.fh + X.sq)[:X.n], (loop.gh + Y.sq)[:Y.n]]
-        if not p.balanced:
-            parts.append((hk.half_step(X, Y, loop.gh, c1, use_off=False) + X.sq)[:X.n])
-            parts.append((hk.half_step(Y, X, loop.fh, c1, use_off=False) + Y.sq)[:Y.n])
-        host = torch.cat(parts).to("cpu", torch.float64).numpy()
-        f, g = host[:X.n], host[X.n:X.n + Y.n]
-        fb = gb = None
-        if not p.balanced:
-            fb, gb = host[X.n + Y.n:2 * X.n + Y.n], host[2 * X.n + Y.n:]
-    return f, g, fb, gb, int(st.it), float(st.err), bool(st.converged), t0
+        st = s.loop.run()
+        f, g, fb, gb, it, err, converged = _hip_finish(p, s, st)
+    return f, g, fb, gb, it, err, converged, t0
 
 
 def _use_hip(opts: SinkhornOptions, d: int) -> bool:
@@ -348,6 +359,10 @@ def sinkhorn(x, y, a=None, b=None, opts: SinkhornOptions | None = None, a_target
         f, g, fb, gb, it, err, converged, t0 = _solve_hip(p, opts)
     else:
         f, g, fb, gb, it, err, converged, t0 = _solve_torch(p, opts)
+    return _result(p, opts, f, g, fb, gb, it, err, converged, t0)
+
+
+def _result(p, opts: SinkhornOptions, f, g, fb, gb, it, err, converged, t0) -> SinkhornResult:
     row_mass = col_mass = None
     if not p.balanced:
         # the plan's marginals: row_i = a_i exp((f_i - fb_i) / eps), fb one balanced f update from g
@@ -358,6 +373,68 @@ def sinkhorn(x, y, a=None, b=None, opts: SinkhornOptions | None = None, a_target
     return SinkhornResult(f=f, g=g, iterations=it, error=err, converged=converged, cost=cost, seconds=seconds,
                           eps=opts.eps, rho=opts.rho, center=p.center, cost_scale=p.scale, row_mass=row_mass,
                           col_mass=col_mass)
+
+
+def sinkhorn_batch(problems) -> list:
+    """sinkhorn() for several independent problems at once on the fused path: `problems` is a list of dicts of
+    sinkhorn()'s arguments (x, y and optionally a, b, opts, a_target, b_target), all with kernel "hip" selected (or
+    "auto" on a ROCm GPU), one device and one d. Their loops run together (DeviceLoopBatch: each launch one pass of
+    every problem, on the GPU's workgroups in proportion to each problem's work), so that problems too small to
+    fill the GPU alone share it. Each result is sinkhorn()'s for its problem to float32 rounding (the partial
+    sums of a half-step are split over fewer workgroups; with one problem, bit for bit); `seconds` is the whole
+    batch's time. The reference solves such problems one after another (examples/singlecell_wot.py:84-89)."""
+    problems = list(problems)
+    return _HipBatch(problems).solve() if problems else []
+
+
+class _HipBatch:
+    """The problems of sinkhorn_batch, prepared, packed and set up once, then solved together, again whenever
+    asked with new marginal targets (wot's growth iterations: the same points, weights, normalisation and
+    options, only the targets change): each solve writes the new target offsets into the packed clouds and starts
+    every loop afresh (potentials zero, state initialised)."""
+
+    def __init__(self, problems):
+        from . import hip_sinkhorn as hk
+        prepared = []
+        for q in problems:
+            opts = q.get("opts") or SinkhornOptions()
+            if not _use_hip(opts, np.shape(q["x"])[1]):
+                raise ValueError("sinkhorn_batch runs the fused kernels: kernel 'hip' on a ROCm GPU, float32, d <= 128")
+            if max(1, int(opts.cores)) > 1:
+                raise ValueError("cores > 1 split rows across NeuronCores in the reference; this build runs on one GPU")
+            p = _prepare(q["x"], q["y"], q.get("a"), q.get("b"), opts, q.get("a_target"), q.get("b_target"), True)
+            prepared.append((p, opts))
+        if len({str(_gpu_device(o)) for _, o in prepared}) != 1 or len({p.xs.shape[1] for p, _ in prepared}) != 1:
+            raise ValueError("sinkhorn_batch: every problem must run on one device with one d")
+        self.prepared = prepared
+        self.dev = dev = _gpu_device(prepared[0][1])
+        with torch.cuda.device(dev):
+            states = hk.DeviceLoopBatch.state_block(len(prepared), dev)
+            self.setups = [_hip_setup(p, o, dev, state=states[k]) for k, (p, o) in enumerate(prepared)]
+            self.batch = hk.DeviceLoopBatch([su.loop for su in self.setups], states)
+        self._fresh = True
+
+    def solve(self, targets=None) -> list:
+        """Solve every problem; targets: one (a_target, b_target) per problem replacing its own (both given where
+        the problem had them), or None for the problems as given."""
+        with torch.cuda.device(self.dev):
+            if targets is not None:
+                for (p, _), su, (at, bt) in zip(self.prepared, self.setups, targets):
+                    if p.off_x is None or p.off_y is None:
+                        raise ValueError("solve(targets): the problem was made without marginal targets")
+                    p.off_x = _log_weights(at, len(p.xs), "a_target") - p.log_a
+                    p.off_y = _log_weights(bt, len(p.ys), "b_target") - p.log_b
+                    su.X.set_off(p.off_x)
+                    su.Y.set_off(p.off_y)
+            if not self._fresh:
+                for su in self.setups:
+                    su.loop.fh.zero_()
+                    su.loop.gh.zero_()              # g0 = |y|^2 (sinkhorn.py:336)
+            self._fresh = False
+            t0 = time.perf_counter()
+            sts = self.batch.run()
+            return [_result(p, o, *_hip_finish(p, su, st), t0)
+                    for (p, o), su, st in zip(self.prepared, self.setups, sts)]
 
 
 def transport_plan(x, y, res: SinkhornResult, a=None, b=None) -> np.ndarray:

@@ -3,6 +3,7 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
     python bench.py --profile [--reps R]     # for rocprofv3: R loop iterations, then a 256 MiB copy
     python bench.py --profile --workload stress-65k [--reps R]   # the same on the 65k d 128 stress clouds
+    python bench.py --profile --workload {single-cell, single-cell-pipeline} [--reps R]   # and the d 30 workloads
     python bench.py --workload {single-cell, single-cell-pipeline, stress-65k} [--no-cpu]
 
 Workload: synthetic balanced 10,000 x 10,000, d = 64, fp32, x ~ N(0, 1) (seed 0), y ~ N(0, 1) + 0.5
@@ -191,6 +192,34 @@ def profile_single_cell(reps):
           flush=True)
 
 
+def profile_pipeline(reps):
+    """The batched pipeline's counterpart of profile_run: the 38 pairs of the pipeline workload (median-normalised,
+    wot's formulation with uniform targets, as a first growth iteration) as one sinkhorn_batch held to `reps`
+    fixed iterations at eps 0.05 (the grouped partial kernel, kp 32: each launch one half-step of every pair), then
+    the same 256 MiB copy."""
+    import numpy as np
+    import torch
+    from trnopt import Backend, SinkhornOptions
+    from trnopt.sinkhorn import sinkhorn_batch
+    sizes = pipeline_sizes()
+    o = SinkhornOptions(eps=0.05, rho=(1.0, 50.0), normalize="median", max_iters=reps, fixed_iters=True,
+                        kernel="hip", backend=Backend.preset("rocm"))
+    qs = []
+    for t in range(len(sizes) - 1):
+        x0, x1 = single_cell_inputs(n=int(sizes[t]), m=int(sizes[t + 1]), t0=t, t1=t + 1)[:2]
+        I, J = len(x0), len(x1)
+        qs.append(dict(x=x0, y=x1, a=np.full(I, 1.0 / I), b=np.full(J, 1.0 / J), opts=o,
+                       a_target=np.full(I, 1.0 / I), b_target=np.full(J, 1.0 / J)))
+    res = sinkhorn_batch(qs)
+    src = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"profile: {res[0].iterations} batched iterations of the {len(qs)} pipeline pairs, then a 256 MiB copy",
+          flush=True)
+
+
 def _cpu_model():
     try:
         for line in Path("/proc/cpuinfo").read_text().splitlines():
@@ -359,6 +388,16 @@ def workload_pipeline(cpu):
             "config": {"workload": "39 time points, d 30, eps 0.05, rho (1, 50), wot stages, tol 1e-6, growth 3",
                        "form": "batched (each growth iteration of all the pairs in one loop)",
                        "streams_pairs_in_flight": PIPELINE_STREAMS}}
+    # the fp16 pipe over the whole batched run (host steps, medians and read-backs included)
+    alg = 2 * 2.0 * work * (30 + 1)
+    flop = 2 * PRODUCTS * 2.0 * work * 32
+    line["roofline"] = {"bound": "mfma", "achieved": round(alg / total / 1e12, 1), "peak": MFMA_F16_PEAK / 1e12,
+                        "unit": "TFLOP/s", "frac": round(alg / total / MFMA_F16_PEAK, 4),
+                        "executed": {"achieved": round(flop / total / 1e12, 1),
+                                     "frac": round(flop / total / MFMA_F16_PEAK, 4)},
+                        "basis": "algorithmic augmented-contraction FLOP of every pair's half-steps (iterations x "
+                                 "2 x 2 n0 n1 (d + 1); executed: the three fp16 products at kp 32) over the "
+                                 "pipeline's end-to-end time"}
     if cpu:
         x0, x1 = clouds[0]
         I, J = len(x0), len(x1)
@@ -450,10 +489,12 @@ def main():
             profile_stress(a.reps)
         elif a.workload == "single-cell":
             profile_single_cell(a.reps)
+        elif a.workload == "single-cell-pipeline":
+            profile_pipeline(a.reps)
         elif a.workload is None:
             profile_run(a.reps)
         else:
-            sys.exit("--profile takes the headline, --workload single-cell or --workload stress-65k")
+            sys.exit("--profile takes the headline, --workload single-cell, single-cell-pipeline or stress-65k")
         return
     if a.workload is not None:
         print(json.dumps(WORKLOADS[a.workload](not a.no_cpu)), flush=True)

@@ -276,12 +276,9 @@ class HipCloud:
         dv = torch.from_numpy(vec).to(device)
         self.sq, self.log_w, self.w, self.log_w_lo = dv[0], dv[1], dv[2], dv[3]
         self.off = dv[4] if off is not None else None
-        # the points unpadded (the packing pads them to npad x kp with zeros), cast into pinned host memory and
-        # copied asynchronously (the caching host allocator keeps the buffer until the copy has run)
-        host32 = torch.empty((n, d), dtype=torch.float32, pin_memory=True)
-        np.copyto(host32.numpy(), pts, casting="same_kind")
-        pts32 = host32.to(device, non_blocking=True)
-        self.pk = pack_cloud(pts32)
+        # the points unpadded (the packing pads them to npad x kp with zeros), cast to float32 on the host and
+        # copied from pageable memory (a pinned staging buffer for every cloud size bought nothing)
+        self.pk = pack_cloud(torch.from_numpy(pts.astype(np.float32)).to(device))
 
     def c_struct(self) -> SkCloud:
         return SkCloud(self.pk.data_ptr(), self.sq.data_ptr(), self.log_w.data_ptr(), self.w.data_ptr(),
@@ -415,7 +412,7 @@ class DeviceLoop:
         L.fixed_iters, L.balanced = int(bool(fixed_iters)), int(bool(balanced))
         L.ws, L.ws_bytes = self.ws.data_ptr(), self.ws.numel()
         self._L = L
-        self._pinned = [torch.empty(ctypes.sizeof(SkState), dtype=torch.uint8, pin_memory=True) for _ in range(2)]
+        self._pinned = None                   # two pinned state buffers, made by the first run (a batch has its own)
         self._graph = None
 
     def init(self) -> None:
@@ -473,6 +470,8 @@ class DeviceLoop:
             self.enqueue(self.max_iters)
             return self.read_state()
         batch = max(1, int(batch or max(self.check_every, 10)))
+        if self._pinned is None:
+            self._pinned = [torch.empty(ctypes.sizeof(SkState), dtype=torch.uint8, pin_memory=True) for _ in range(2)]
         queued = 0
         inflight = []                         # (pinned buffer, event) per enqueued batch, oldest first
         slot = 0

@@ -43,6 +43,26 @@ enum Mode { kHalfStep = 0, kPlainLse = 1 };
 // requested together with the launch's other scalars.
 __device__ const int kNoSkip = 0;
 
+// n / d for 0 <= n < 2^31 by one multiply-high, d in [1, 2^31] a divisor fixed per launch: with
+// 2^(k-1) < d <= 2^k and m = ceil(2^(31 + k) / d) (in [2^31, 2^32)), n m / 2^(31 + k) = n / d + delta with
+// 0 <= delta < n / 2^(31 + k) < 2^-k <= 1 / d, which no fraction of n / d reaches 1 with, so
+// floor(2n m / 2^32) >> k = floor(n / d) exactly. The prologue's divisions by the split's constants (seven per
+// segment, ~30 dependent instructions each on the vector unit) become two scalar instructions each.
+struct Div {
+    unsigned m;
+    int k;
+};
+inline Div make_div(int d) {
+    Div v;
+    v.k = 0;
+    while ((1LL << v.k) < d) ++v.k;
+    v.m = (unsigned)((((unsigned long long)1 << (31 + v.k)) + (unsigned long long)d - 1) / (unsigned long long)d);
+    return v;
+}
+__host__ __device__ inline int div_by(int n, const Div& v) {
+    return (int)((unsigned)(((unsigned long long)(2u * (unsigned)n) * v.m) >> 32) >> v.k);
+}
+
 // Work split shared by the partial and the merge kernels. The (row group, column tile) units are laid out on a
 // cost line: unit x of row group g = x / nt sits at position F(x) = x + alpha g, i.e. every row-group boundary
 // costs alpha positions, because a workgroup whose range crosses one starts a second segment (its row
@@ -57,24 +77,31 @@ struct Split {
     int alpha;       // cost of a row-group boundary, in tiles
     int ftot;        // ngroups * nt + alpha * (ngroups - 1)
     int q, r;        // ftot = q P + r
+    Div dP, dspan, dnt, dftot;   // division by P, nt + alpha, nt and ftot (set_divisors)
 };
+inline void set_divisors(Split& s) {
+    s.dP = make_div(s.P);
+    s.dspan = make_div(s.nt + s.alpha);
+    s.dnt = make_div(s.nt);
+    s.dftot = make_div(s.ftot);
+}
 
-// C_p, the first cost position of workgroup p (C_P = ftot).
-__host__ __device__ inline int cost_start(int p, const Split& s) { return p * s.q + (p * s.r) / s.P; }
+// C_p, the first cost position of workgroup p (C_P = ftot; p r < 2^20).
+__host__ __device__ inline int cost_start(int p, const Split& s) { return p * s.q + div_by(p * s.r, s.dP); }
 
 // The first unit at or after cost position c: inside a row group's span the unit at c, inside the boundary
 // gap after group g the first unit of group g + 1.
 __host__ __device__ inline int unit_at(int c, const Split& s) {
     const int span = s.nt + s.alpha;
-    const int g = c / span, rem = c - g * span;
+    const int g = div_by(c, s.dspan), rem = c - g * span;
     return g * s.nt + (rem < s.nt ? rem : s.nt);
 }
 
 // Workgroup p owns units [unit_at(C_p), unit_at(C_(p+1))). The owner of unit x is the largest p with
 // C_p <= F(x) (unit_at(C) <= x exactly when C <= F(x)), i.e. ((F(x) + 1) P - 1) / ftot.
 __host__ __device__ inline int owner_of(int x, const Split& s) {
-    const int fx = x + s.alpha * (x / s.nt);
-    const int p = fx < 0x7fffffff / s.P ? ((fx + 1) * s.P - 1) / s.ftot
+    const int fx = x + s.alpha * div_by(x, s.dnt);
+    const int p = fx < 0x7fffffff / s.P ? div_by((fx + 1) * s.P - 1, s.dftot)
                                         : (int)((((long long)fx + 1) * s.P - 1) / s.ftot);
     return p < s.P - 1 ? p : s.P - 1;
 }

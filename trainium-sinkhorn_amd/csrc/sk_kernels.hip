@@ -373,6 +373,7 @@ Plan make_plan(int rows_pad, int m_pad, int kp, int P_req = 0) {
     pl.s.q = (int)(ftot / P);
     pl.s.r = (int)(ftot % P);
     pl.ok = ftot < 0x7fffffffLL;
+    if (pl.ok) set_divisors(pl.s);
     int slots = 1;
     if (pl.ok)
         for (int g = 0; g < pl.ngroups; ++g) slots = std::max(slots, last_wg(g, pl.s) - first_wg(g, pl.s) + 1);

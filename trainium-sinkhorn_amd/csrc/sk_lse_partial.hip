@@ -821,7 +821,7 @@ __device__ __forceinline__ void segments(const PartialArgs& a, const PartialArgs
     // operand addresses stay in scalar registers.
     const int u1 = __builtin_amdgcn_readfirstlane(unit_at(cost_start(p + 1, a.s), a.s));
     for (int u = __builtin_amdgcn_readfirstlane(unit_at(cost_start(p, a.s), a.s)); u < u1;) {
-        const int g = __builtin_amdgcn_readfirstlane(u / a.s.nt);
+        const int g = __builtin_amdgcn_readfirstlane(div_by(u, a.s.dnt));
         const int tb = u - g * a.s.nt;
         const int te = u1 - u < a.s.nt - tb ? tb + (u1 - u) : a.s.nt;
         const int slot = __builtin_amdgcn_readfirstlane(p - first_wg(g, a.s));
@@ -860,7 +860,9 @@ __device__ __forceinline__ void partial_pass(const PartialArgs& a, const Partial
     // The argument fields the segments need, requested with the first batch of argument loads rather than
     // after the scalars have arrived.
     asm volatile("" ::"s"(a.nrb), "s"(a.rows_pad), "s"(a.mode), "s"(a.s.nt), "s"(a.s.P), "s"(a.s.alpha),
-                 "s"(a.s.ftot), "s"(a.s.q), "s"(a.s.r), "s"(a.group_counters));
+                 "s"(a.s.ftot), "s"(a.s.q), "s"(a.s.r), "s"(a.group_counters), "s"(a.s.dP.m), "s"(a.s.dP.k),
+                 "s"(a.s.dspan.m), "s"(a.s.dspan.k), "s"(a.s.dnt.m), "s"(a.s.dnt.k), "s"(a.s.dftot.m),
+                 "s"(a.s.dftot.k), "s"(a.u), "s"(a.v), "s"(a.u2), "s"(a.v2), "s"(a.part));
     asm volatile("" ::"s"(sc0), "s"(sc2), "s"(sx), "s"(sy), "s"(cb), "s"(cb_s2), "s"(cb_t), "v"(skip));
     if (skip != 0) return;
     constexpr bool kStream = streamed_form(NC, CT);

@@ -516,6 +516,42 @@ def _costs(s, starts):
     return np.array(out)
 
 
+def make_div(d):
+    """sk_common.h make_div: k the smallest with d <= 2^k, m = ceil(2^(31 + k) / d)."""
+    k = (d - 1).bit_length()
+    return -(-(1 << (31 + k)) // d), k
+
+
+def div_by(n, md):
+    """sk_common.h div_by: floor(2n m / 2^32) >> k, in 32-bit unsigned arithmetic as the kernels do it."""
+    m, k = md
+    assert 0 <= n < 2 ** 31 and 2 ** 31 <= m < 2 ** 32 or m == 2 ** 31
+    return (((2 * n) & 0xFFFFFFFF) * m >> 32) >> k
+
+
+def test_split_division_by_multiply_high_is_exact():
+    """The split's divisions by its per-launch constants (P, nt + alpha, nt, ftot) are one multiply-high each:
+    exact for every dividend below 2^31 (the split's positions and owner products, which the planner keeps
+    there). Divisors 1 to 2^31 at and around powers of two, the plans' usual sizes and random ones; dividends at
+    the multiples of the divisor and around them, the top of the range and random ones."""
+    rng = np.random.default_rng(17)
+    ds = {1, 2, 3, 7, 31, 32, 33, 313, 319, 1023, 1024, 1025, 2 ** 31 - 1, 2 ** 31}
+    ds |= {2 ** e + o for e in range(1, 31) for o in (-1, 0, 1)}
+    ds |= set(int(v) for v in rng.integers(1, 2 ** 31, 400))
+    for d in sorted(ds):
+        md = make_div(d)
+        top = (2 ** 31 - 1) // d * d
+        ns = {0, 1, d - 1, d, d + 1, 2 * d - 1, 2 * d, top - 1, top, 2 ** 31 - 2, 2 ** 31 - 1}
+        ns |= set(int(v) for v in rng.integers(0, 2 ** 31, 60))
+        for n in ns:
+            if 0 <= n < 2 ** 31:
+                assert div_by(n, md) == n // d, (n, d)
+    # a planted mistake (m rounded down instead of up) is caught
+    d = 3
+    m_floor = (1 << (31 + 2)) // d
+    assert any((((2 * n) * m_floor >> 32) >> 2) != n // d for n in range(0, 3000))
+
+
 def test_split_balances_segment_costs():
     """Workgroups whose range crosses a row-group boundary get about alpha fewer tiles: every workgroup's cost
     is within one tile plus alpha of ftot / P, and at 10k x 10k the largest cost is below the equal-tiles

@@ -417,6 +417,10 @@ class _HipBatch:
     def solve(self, targets=None) -> list:
         """Solve every problem; targets: one (a_target, b_target) per problem replacing its own (both given where
         the problem had them), or None for the problems as given."""
+        if targets is not None:
+            targets = list(targets)
+            if len(targets) != len(self.prepared):
+                raise ValueError(f"solve(targets): {len(targets)} targets for {len(self.prepared)} problems")
         with torch.cuda.device(self.dev):
             if targets is not None:
                 for (p, _), su, (at, bt) in zip(self.prepared, self.setups, targets):

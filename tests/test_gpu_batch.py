@@ -9,6 +9,7 @@ GPU's workgroups, merged inside the launch.
   one stopped early by its max_iters while the others go on): each agrees with its own sinkhorn() to float32
   rounding, and with the oracle's float64 run within the solver sweep's bar.
 * The wot pipeline batched against the same pairs one at a time: the same maps to float32 rounding.
+* More loops than CUs (300 small problems): one workgroup per pass, every loop as its own to float32 rounding.
 """
 
 import numpy as np
@@ -123,3 +124,28 @@ def test_wot_transport_maps_batched_match_one_at_a_time():
         assert ef < 2e-5 and eg < 2e-5, (k, ef, eg)
         for Ga, Gb in zip(a.learned_growth, b.learned_growth):
             np.testing.assert_allclose(Ga, Gb, rtol=1e-3)
+
+
+def test_batch_of_more_loops_than_cus():
+    """300 small problems (24-120 points a side, d 8, balanced and unbalanced): more loops than the GPU has CUs, so
+    every pass gets one workgroup (its own single-workgroup split) and a launch runs 300 of them; each loop agrees
+    with its own sinkhorn() to float32 rounding."""
+    rng = np.random.default_rng(505)
+    qs = []
+    for k in range(300):
+        n, m = int(rng.integers(24, 121)), int(rng.integers(24, 121))
+        x = rng.normal(size=(n, 8))
+        y = rng.normal(size=(m, 8)) + 0.2
+        o = dict(eps=0.1, max_iters=int(rng.integers(8, 25)), fixed_iters=True)
+        if k % 3 == 1:
+            o["rho"] = 1.0
+        qs.append(dict(x=x, y=y, opts=SinkhornOptions(kernel="hip", backend=ROCM, **o)))
+    print("batch of 300 small problems", flush=True)
+    batch = sinkhorn_batch(qs)
+    worst = 0.0
+    for q, got in zip(qs, batch):
+        alone = sinkhorn(**q)
+        assert got.iterations == alone.iterations == q["opts"].max_iters
+        worst = max(worst, inf_rel(got.f, alone.f), inf_rel(got.g, alone.g))
+    print(f"  largest difference from the loops alone {worst:.2e}", flush=True)
+    assert worst < 2e-6

@@ -342,6 +342,13 @@ def cost_median(xc: np.ndarray, yc: np.ndarray, device) -> float:
     """median over all pairs of max(|xc_i|^2 + |yc_j|^2 - 2 xc_i . yc_j, 0) in float64, np.median's definition,
     on the GPU (sk_cost_median_f64): the exact-median branch of normalization(how="median")
     (src/trnopt/sinkhorn.py:229-233) without the n x m matrix. xc, yc: centred float64 (n, d), (m, d)."""
+    return float(cost_median_enqueue(xc, yc, device).item())
+
+
+def cost_median_enqueue(xc: np.ndarray, yc: np.ndarray, device) -> torch.Tensor:
+    """cost_median enqueued on the current stream, not waited for: its (1,) float64 device result. Several
+    pairs' medians enqueued back to back are read with one synchronisation (the inputs and workspace go back to
+    the caching allocator, which hands them out again only to work ordered after this on the same stream)."""
     xc = np.ascontiguousarray(xc, dtype=np.float64)
     yc = np.ascontiguousarray(yc, dtype=np.float64)
     if xc.ndim != 2 or yc.ndim != 2 or xc.shape[1] != yc.shape[1]:
@@ -354,7 +361,7 @@ def cost_median(xc: np.ndarray, yc: np.ndarray, device) -> float:
     ws = _workspace(lb.sk_cost_median_workspace_bytes(n, m, d), device)
     _check(lb.sk_cost_median_f64(X.data_ptr(), Y.data_ptr(), n, m, d, out.data_ptr(), ws.data_ptr(), ws.numel(),
                                  _stream()), "sk_cost_median_f64")
-    return float(out.item())
+    return out
 
 
 # ---------------------------------------------------------------------------------------------------------

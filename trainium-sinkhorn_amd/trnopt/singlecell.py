@@ -63,7 +63,8 @@ class _WotPair:
     normalisation once, then per growth iteration the problem for sinkhorn() and the learned growth from its
     result."""
 
-    def __init__(self, x0, x1, growth, delta_days, eps, lambda1, lambda2, tol, stage_tol, opts):
+    def __init__(self, x0, x1, growth, delta_days, eps, lambda1, lambda2, tol, stage_tol, opts, norm=None,
+                 norm_seconds=0.0):
         self.x0, self.x1 = x0, x1
         self.I, self.J = I, J = len(x0), len(x1)
         self.G = np.ones(I) if growth is None else np.power(np.asarray(growth, dtype=np.float64), delta_days)
@@ -71,8 +72,11 @@ class _WotPair:
         hip = _use_hip(opts, np.shape(x0)[1])
         t = time.perf_counter()
         # once per pair (the cost does not change across growth iterations); on the GPU when the fused path runs
-        norm = normalization(x0, x1, how="median", device=_gpu_device(opts) if hip and np.shape(x0)[1] <= 128 else None)
-        self.seconds = time.perf_counter() - t
+        # (norm: already taken, with several pairs' medians at once, in norm_seconds)
+        if norm is None:
+            norm = normalization(x0, x1, how="median",
+                                 device=_gpu_device(opts) if hip and np.shape(x0)[1] <= 128 else None)
+        self.seconds = time.perf_counter() - t + norm_seconds
         self.base = replace(opts, eps=eps, rho=(lambda1, lambda2), normalize=norm, eps_stages=wot_eps_stages(eps),
                             stage_tol=stage_tol, tol=tol, eps_start=None, fixed_iters=False)
         self.a, self.b = np.full(I, 1.0 / I), np.full(J, 1.0 / J)
@@ -162,9 +166,12 @@ def _wot_maps_batched(pairs, growths, days, eps: float = 0.05, lambda1: float = 
     one batched solve (sinkhorn_batch's), the pairs' clouds prepared and packed once for all growth iterations
     (only the row and column targets change between them). A pair's `seconds` is its normalisation plus the whole
     of each batch it took part in."""
-    from .sinkhorn import _HipBatch
-    ws = [_WotPair(x0, x1, growths[k], days[k], eps, lambda1, lambda2, tol, stage_tol, opts)
-          for k, (x0, x1) in enumerate(pairs)]
+    from .sinkhorn import _HipBatch, median_normalizations
+    t = time.perf_counter()
+    norms = median_normalizations(pairs, _gpu_device(opts or SinkhornOptions()))
+    dt = time.perf_counter() - t
+    ws = [_WotPair(x0, x1, growths[k], days[k], eps, lambda1, lambda2, tol, stage_tol, opts, norm=norms[k],
+                   norm_seconds=dt) for k, (x0, x1) in enumerate(pairs)]
     batch = None
     for _ in range(growth_iters):
         t = time.perf_counter()

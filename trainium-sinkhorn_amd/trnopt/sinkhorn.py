@@ -220,6 +220,32 @@ def _hip_finish(p, s, st):
     return f, g, fb, gb, int(st.it), float(st.err), bool(st.converged)
 
 
+def _hip_finish_many(ps, setups, states) -> list:
+    """_hip_finish for several solves at once: every solve's potentials (and unbalanced half-steps) enqueued,
+    then one read-back for all of them instead of one each."""
+    from . import hip_sinkhorn as hk
+    parts, spans = [], []
+    for p, s, st in zip(ps, setups, states):
+        X, Y, loop = s.X, s.Y, s.loop
+        q = [(loop.fh + X.sq)[:X.n], (loop.gh + Y.sq)[:Y.n]]
+        if not p.balanced:
+            q.append((hk.half_step(X, Y, loop.gh, s.c1, use_off=False) + X.sq)[:X.n])
+            q.append((hk.half_step(Y, X, loop.fh, s.c1, use_off=False) + Y.sq)[:Y.n])
+        spans.append((len(parts), X.n, Y.n))
+        parts.extend(q)
+    host = torch.cat(parts).to("cpu", torch.float64).numpy()
+    out, pos = [], 0
+    for (p, _, st), (_, n, m) in zip(zip(ps, setups, states), spans):
+        f, g = host[pos:pos + n], host[pos + n:pos + n + m]
+        pos += n + m
+        fb = gb = None
+        if not p.balanced:
+            fb, gb = host[pos:pos + n], host[pos + n:pos + n + m]
+            pos += n + m
+        out.append((f, g, fb, gb, int(st.it), float(st.err), bool(st.converged)))
+    return out
+
+
 def _solve_hip(p, opts: SinkhornOptions):
     dev = _gpu_device(opts)
     with torch.cuda.device(dev):
@@ -287,6 +313,28 @@ def normalization(x: np.ndarray, y: np.ndarray, samples: int = 20_000, seed: int
         dd = ((x[i] - y[j]) ** 2).sum(axis=1)
         scale = float(np.median(dd) if how == "median" else dd.mean())
     return center, (scale if scale > 0 else 1.0)
+
+
+def median_normalizations(pairs, device, samples: int = 20_000, seed: int = 0) -> list:
+    """normalization(x, y, how="median", device=device) for every (x, y) of `pairs`, the exact medians of all of
+    them enqueued on the GPU and read back with one synchronisation (a pipeline's pairs, each otherwise a round
+    trip of its own). The same (center, cost_scale) as the one-pair call, pair by pair."""
+    from . import hip_sinkhorn as hk
+    out, pending = [], []
+    for x, y in pairs:
+        x = np.asarray(x, dtype=np.float64)
+        y = np.asarray(y, dtype=np.float64)
+        if len(x) * len(y) > 100_000_000:
+            out.append(normalization(x, y, samples=samples, seed=seed, how="median", device=device))
+            continue
+        center = np.concatenate([x, y]).mean(axis=0)
+        pending.append((len(out), hk.cost_median_enqueue(x - center, y - center, device)))
+        out.append(center)
+    if pending:
+        scales = torch.cat([t for _, t in pending]).cpu().numpy()
+        for (k, _), scale in zip(pending, scales):
+            out[k] = (out[k], float(scale) if scale > 0 else 1.0)
+    return out
 
 
 def _gpu_device(opts: SinkhornOptions):
@@ -437,8 +485,8 @@ class _HipBatch:
             self._fresh = False
             t0 = time.perf_counter()
             sts = self.batch.run()
-            return [_result(p, o, *_hip_finish(p, su, st), t0)
-                    for (p, o), su, st in zip(self.prepared, self.setups, sts)]
+            fin = _hip_finish_many([p for p, _ in self.prepared], self.setups, sts)
+            return [_result(p, o, *r, t0) for (p, o), r in zip(self.prepared, fin)]
 
 
 def transport_plan(x, y, res: SinkhornResult, a=None, b=None) -> np.ndarray:

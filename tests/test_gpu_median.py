@@ -85,3 +85,21 @@ def test_solver_uses_the_gpu_median(hip):
     res = sinkhorn(x, y, opts=SinkhornOptions(kernel="hip", backend=Backend.preset("rocm"), normalize="median",
                                              eps=0.1, max_iters=50, fixed_iters=True))
     assert abs(res.cost_scale - normalization(x, y, how="median")[1]) <= 1e-12 * res.cost_scale
+
+
+def test_median_normalizations_equal_the_one_pair_calls(hip):
+    """median_normalizations (a pipeline's pairs, every exact median enqueued at once, one read-back) gives each
+    pair's normalization(how="median", device) bit for bit, including a pair above the exact median's 1e8 cost
+    pairs, which takes the sampled median on the host as the one-pair call does."""
+    import torch
+    from trnopt.sinkhorn import median_normalizations, normalization
+    dev = torch.device("cuda", 0)
+    pairs = [data.clouds(n=n, m=m, d=d, seed=s) for n, m, d, s in ((300, 257, 30, 1), (40, 900, 7, 2), (1, 1, 3, 3),
+                                                                   (1200, 1100, 64, 4))]
+    rng = np.random.default_rng(5)
+    pairs.append((rng.normal(size=(10_001, 2)), rng.normal(size=(10_000, 2))))    # 1.00001e8 pairs
+    got = median_normalizations(pairs, dev)
+    for (x, y), (c, s) in zip(pairs, got):
+        c1, s1 = normalization(x, y, how="median", device=dev)
+        np.testing.assert_array_equal(c, c1)
+        assert s == s1, (s, s1)

@@ -246,6 +246,18 @@ def test_converged_plan_matches_brute_force_and_row_sums():
     np.testing.assert_allclose(P.sum(1), 1 / len(x), rtol=1e-5)
 
 
+def test_raw_cost_plan_matches_log_domain_solver():
+    """tests/test_sinkhorn.py:143-152 of the reference (the raw cost, eps 0.5, tol 1e-9, plan within 1e-6), with
+    POT's log-domain solver, which is not installed here, replaced by the same textbook iteration on the dense
+    float64 C (uniform marginals, g from zero), run to 1e-13."""
+    x, y = data.clouds(n=120, m=80, d=4, seed=5)
+    r = ref.sinkhorn_ref(x, y, eps=0.5, normalize=False, tol=1e-9, max_iters=10_000)
+    assert r.converged
+    f, g, _ = brute.sinkhorn_dense(x, y, 0.5, g0=np.zeros(len(y)), iters=20_000, tol=1e-13)
+    Q = brute.dense_plan(x, y, f, g, 0.5)
+    assert np.abs(ref.transport_plan(x, y, r) - Q).max() / Q.max() < 1e-6
+
+
 def test_float32_oracle_close_to_float64():
     x, y = data.clouds(n=400, m=350, d=10, seed=3)
     o = dict(eps=0.05, tol=1e-5, max_iters=3000)

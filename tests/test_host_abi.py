@@ -231,6 +231,14 @@ def test_input_validation():
         sinkhorn(x, y, a=-np.full(20, 0.05), opts=SinkhornOptions(rho=1.0))
     with pytest.raises(ValueError, match="positive"):
         sinkhorn(x, y, b=np.full(14, 1 / 14), opts=SinkhornOptions(rho=1.0))
+    with pytest.raises(ValueError, match="same d"):
+        sinkhorn(x, y[:, :2])
+    with pytest.raises(ValueError, match="2-D"):
+        sinkhorn(x[:, 0], y)
+    with pytest.raises(ValueError, match="at least one point"):
+        sinkhorn(x[:0], y, opts=SinkhornOptions(rho=1.0, normalize=False))
+    with pytest.raises(ValueError, match="at least one point"):
+        sinkhorn(x, y[:0], opts=SinkhornOptions(rho=1.0, normalize=False))
 
 
 def test_presets():

@@ -25,7 +25,7 @@ from dataclasses import dataclass, replace
 
 import numpy as np
 
-from .sinkhorn import (SinkhornOptions, SinkhornResult, _gpu_device, _use_hip, normalization, sinkhorn,
+from .sinkhorn import (SinkhornOptions, SinkhornResult, _cloud_dim, _gpu_device, _use_hip, normalization, sinkhorn,
                        transport_plan)
 
 PAIR_KEYS = ("f", "g", "eps", "center", "cost_scale", "row_mass", "col_mass", "learned_growth", "cells0",
@@ -69,13 +69,14 @@ class _WotPair:
         self.I, self.J = I, J = len(x0), len(x1)
         self.G = np.ones(I) if growth is None else np.power(np.asarray(growth, dtype=np.float64), delta_days)
         opts = opts or SinkhornOptions()
-        hip = _use_hip(opts, np.shape(x0)[1])
+        d = _cloud_dim(x0, x1)
+        hip = _use_hip(opts, d)
         t = time.perf_counter()
         # once per pair (the cost does not change across growth iterations); on the GPU when the fused path runs
         # (norm: already taken, with several pairs' medians at once, in norm_seconds)
         if norm is None:
             norm = normalization(x0, x1, how="median",
-                                 device=_gpu_device(opts) if hip and np.shape(x0)[1] <= 128 else None)
+                                 device=_gpu_device(opts) if hip and d <= 128 else None)
         self.seconds = time.perf_counter() - t + norm_seconds
         self.base = replace(opts, eps=eps, rho=(lambda1, lambda2), normalize=norm, eps_stages=wot_eps_stages(eps),
                             stage_tol=stage_tol, tol=tol, eps_start=None, fixed_iters=False)
@@ -128,8 +129,9 @@ def wot_transport_maps(pairs, growth=None, delta_days=1.0, streams: int = 4, bat
         x0, x1 = pairs[k]
         return wot_transport_map(x0, x1, growths[k], days[k], **kw)
 
-    fused = n >= 2 and all(_use_hip(opts, np.shape(x0)[1]) for x0, _ in pairs)
-    if fused and batch and len({np.shape(x0)[1] for x0, _ in pairs}) == 1:
+    dims = [_cloud_dim(x0, x1) for x0, x1 in pairs]
+    fused = n >= 2 and all(_use_hip(opts, d) for d in dims)
+    if fused and batch and len(set(dims)) == 1:
         return _wot_maps_batched(pairs, growths, days, **kw)
     if streams == 1 or not fused:
         return [one(k) for k in range(n)]

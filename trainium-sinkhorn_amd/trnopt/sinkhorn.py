@@ -279,6 +279,17 @@ def _use_hip(opts: SinkhornOptions, d: int) -> bool:
 # ---------------------------------------------------------------------------------------------------------
 # Inputs, normalisation, driver
 
+def _cloud_dim(x, y) -> int:
+    """d of two clouds x (n, d) and y (m, d), checked: 2-D, one d >= 1, at least one point each. (The reference
+    fails later on such input, inside numpy or torch; here before any device work.)"""
+    sx, sy = np.shape(x), np.shape(y)
+    if len(sx) != 2 or len(sy) != 2 or sx[1] != sy[1] or sx[1] < 1:
+        raise ValueError(f"x (n, d) and y (m, d) must be 2-D with the same d >= 1, got {sx} and {sy}")
+    if sx[0] == 0 or sy[0] == 0:
+        raise ValueError(f"x and y need at least one point each, got {sx[0]} and {sy[0]}")
+    return int(sx[1])
+
+
 def _log_weights(w, n: int, name: str) -> np.ndarray:
     if w is None:
         return np.full(n, -np.log(n))
@@ -348,6 +359,7 @@ def _prepare(x, y, a, b, opts: SinkhornOptions, a_target, b_target, hip: bool = 
     be = opts.backend
     x = np.asarray(x, dtype=np.float64)
     y = np.asarray(y, dtype=np.float64)
+    _cloud_dim(x, y)
     log_a, log_b = _log_weights(a, len(x), "a"), _log_weights(b, len(y), "b")
     balanced = opts.rho is None
     if balanced and abs(np.exp(log_a).sum() - np.exp(log_b).sum()) > 1e-9 * np.exp(log_a).sum():
@@ -399,7 +411,7 @@ def sinkhorn(x, y, a=None, b=None, opts: SinkhornOptions | None = None, a_target
     rho KL(P 1 | a_target) and rho KL(P^T 1 | b_target) pull the plan's sums toward a_target and b_target (default
     a and b): wot's formulation is a uniform reference, a_target = growth / I, b_target = mean growth / J."""
     opts = opts or SinkhornOptions()
-    hip = _use_hip(opts, np.shape(x)[1])
+    hip = _use_hip(opts, _cloud_dim(x, y))
     p = _prepare(x, y, a, b, opts, a_target, b_target, hip)
     if max(1, int(opts.cores)) > 1:
         raise ValueError("cores > 1 split rows across NeuronCores in the reference; this build runs on one GPU")
@@ -446,7 +458,7 @@ class _HipBatch:
         prepared = []
         for q in problems:
             opts = q.get("opts") or SinkhornOptions()
-            if not _use_hip(opts, np.shape(q["x"])[1]):
+            if not _use_hip(opts, _cloud_dim(q["x"], q["y"])):
                 raise ValueError("sinkhorn_batch runs the fused kernels: kernel 'hip' on a ROCm GPU, float32, d <= 128")
             if max(1, int(opts.cores)) > 1:
                 raise ValueError("cores > 1 split rows across NeuronCores in the reference; this build runs on one GPU")

@@ -24,8 +24,10 @@ from trnopt import Backend
 from trnopt.sinkhorn import SinkhornOptions, sinkhorn
 
 pytestmark = pytest.mark.gpu
-# The default sweep; SK_SOLVER_SWEEP_CASES=N runs the first N seeded cases instead (a longer one-off sweep).
+# The default sweep; SK_SOLVER_SWEEP_CASES=N runs N seeded cases instead (a longer one-off sweep), from case
+# SK_SOLVER_SWEEP_FIRST on (default 0).
 N_CASES = int(os.environ.get("SK_SOLVER_SWEEP_CASES", "96"))
+FIRST_CASE = int(os.environ.get("SK_SOLVER_SWEEP_FIRST", "0"))
 TOL = 1e-5
 
 
@@ -84,7 +86,7 @@ def _check_case(k):
         assert ef <= max(TOL, 1.5 * rf) and eg <= max(TOL, 1.5 * rg), (ef, eg, rf, rg)
 
 
-@pytest.mark.parametrize("k", range(N_CASES))
+@pytest.mark.parametrize("k", range(FIRST_CASE, FIRST_CASE + N_CASES))
 def test_solver_random_sweep(k):
     _check_case(k)
 

@@ -24,8 +24,10 @@ from oracle import brute
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
-# The default sweep; SK_SWEEP_CASES=N runs the first N seeded cases instead (a longer one-off sweep).
+# The default sweep; SK_SWEEP_CASES=N runs N seeded cases instead (a longer one-off sweep), from case
+# SK_SWEEP_FIRST on (default 0).
 N_CASES = int(os.environ.get("SK_SWEEP_CASES", "160"))
+FIRST_CASE = int(os.environ.get("SK_SWEEP_FIRST", "0"))
 
 
 def _case(k, shape=None):
@@ -65,7 +67,7 @@ def _budget(r32, c32, col_term, eps, kappa, want):
     return kappa * (contraction + column + lse) + 4.0 * 2.0 ** -24 * np.abs(want) + 1e-30
 
 
-@pytest.mark.parametrize("k", range(N_CASES))
+@pytest.mark.parametrize("k", range(FIRST_CASE, FIRST_CASE + N_CASES))
 def test_half_step_random_sweep(hip, k):
     _check_case(hip, _case(k), f"sweep case {k}")
 

@@ -149,3 +149,33 @@ def test_batch_of_more_loops_than_cus():
         worst = max(worst, inf_rel(got.f, alone.f), inf_rel(got.g, alone.g))
     print(f"  largest difference from the loops alone {worst:.2e}", flush=True)
     assert worst < 2e-6
+
+
+def test_batch_refusals_leave_every_problem_as_it_was():
+    """sinkhorn_batch refuses problems of different d and options the fused path does not take; a batch's
+    solve(targets) refuses the wrong number of targets, targets for a problem made without them and a bad target
+    of a later problem, each before any problem's offsets change: the next plain solve repeats the first bit for
+    bit."""
+    from trnopt.sinkhorn import _HipBatch
+    x, y, _ = _clouds(300, 280, 8, 5)
+    x2, y2, _ = _clouds(200, 220, 9, 6)
+    ok = SinkhornOptions(kernel="hip", backend=ROCM, eps=0.1, rho=1.0, max_iters=30, fixed_iters=True)
+    with pytest.raises(ValueError, match="one d"):
+        sinkhorn_batch([dict(x=x, y=y, opts=ok), dict(x=x2, y=y2, opts=ok)])
+    with pytest.raises(ValueError, match="fused kernels"):
+        sinkhorn_batch([dict(x=x, y=y, opts=SinkhornOptions(kernel="torch", backend=ROCM))])
+    at, bt = np.full(300, 1 / 300), np.full(280, 1 / 280)
+    at2, bt2 = np.full(100, 1.2 / 100), np.full(90, 1 / 90)
+    for second in (dict(), dict(a_target=at2, b_target=bt2)):
+        batch = _HipBatch([dict(x=x, y=y, opts=ok, a_target=at, b_target=bt),
+                           dict(x=x[:100], y=y[:90], opts=ok, **second)])
+        first = batch.solve()
+        with pytest.raises(ValueError, match="1 targets for 2"):
+            batch.solve([(at * 1.1, bt)])
+        with pytest.raises(ValueError, match="without marginal targets" if not second else "positive"):
+            batch.solve([(at * 1.1, bt), (-at2, bt2)])
+        again = batch.solve()
+        for r0, r1 in zip(first, again):
+            np.testing.assert_array_equal(r0.f, r1.f)
+            np.testing.assert_array_equal(r0.g, r1.g)
+            assert r0.iterations == r1.iterations == 30

@@ -477,19 +477,24 @@ class _HipBatch:
     def solve(self, targets=None) -> list:
         """Solve every problem; targets: one (a_target, b_target) per problem replacing its own (both given where
         the problem had them), or None for the problems as given."""
+        offs = None
         if targets is not None:
             targets = list(targets)
             if len(targets) != len(self.prepared):
                 raise ValueError(f"solve(targets): {len(targets)} targets for {len(self.prepared)} problems")
+            # every target checked before any problem's offsets change
+            offs = []
+            for (p, _), (at, bt) in zip(self.prepared, targets):
+                if p.off_x is None or p.off_y is None:
+                    raise ValueError("solve(targets): the problem was made without marginal targets")
+                offs.append((_log_weights(at, len(p.xs), "a_target") - p.log_a,
+                             _log_weights(bt, len(p.ys), "b_target") - p.log_b))
         with torch.cuda.device(self.dev):
-            if targets is not None:
-                for (p, _), su, (at, bt) in zip(self.prepared, self.setups, targets):
-                    if p.off_x is None or p.off_y is None:
-                        raise ValueError("solve(targets): the problem was made without marginal targets")
-                    p.off_x = _log_weights(at, len(p.xs), "a_target") - p.log_a
-                    p.off_y = _log_weights(bt, len(p.ys), "b_target") - p.log_b
-                    su.X.set_off(p.off_x)
-                    su.Y.set_off(p.off_y)
+            if offs is not None:
+                for (p, _), su, (ox, oy) in zip(self.prepared, self.setups, offs):
+                    p.off_x, p.off_y = ox, oy
+                    su.X.set_off(ox)
+                    su.Y.set_off(oy)
             if not self._fresh:
                 for su in self.setups:
                     su.loop.fh.zero_()
